@@ -1,0 +1,185 @@
+/*
+ * mamba_int.h — C ABI of libmamba_int.so, the MI355X (gfx950) integer Mamba
+ * inference path (spec mi-spec-1).
+ *
+ * Conventions (every entry point):
+ *   - plain device pointers and sizes; the caller owns every buffer (the
+ *     library allocates nothing on the device);
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); all
+ *     work is enqueued asynchronously on it, nothing synchronises;
+ *   - arguments are validated on the host before anything is enqueued; an
+ *     invalid call returns a non-zero mi_status and enqueues nothing;
+ *   - mi_last_error_string() describes the last failure of the calling thread;
+ *   - a size of zero (batch, len, m, tokens ...) is a valid no-op;
+ *   - calls that share no output buffer may run concurrently on different
+ *     streams.
+ *
+ * Reference interfaces replaced (file:line in Jayluci4/mamba-integer):
+ *   launch_dyadic_scan           src/cuda_kernels/dyadic_mamba_kernel.cu:135-153
+ *   DyadicScanFunction.apply     src/mamba_integer_model.py:260-316
+ *   ssd_chunked_scan_forward     src/triton_kernels/ssd_chunked_scan.py:382-422
+ *   BitLinear.forward            src/rational_bitnet.py:167-213
+ *   activation_quant_dynamic     src/rational_bitnet.py:88-111
+ *   get_ternary_weights          src/rational_bitnet.py:215-219
+ *   launch_bitlinear             src/cuda_kernels/bitlinear.cu:18-91
+ *   fast_bitnet_matmul           src/triton_kernels/bitnet_kernels.py:198-218
+ *   BitShiftNormFunction.forward src/mamba_integer_model.py:200-223
+ *   launch_bitshift_norm         src/cuda_kernels/bitshift_norm.cu:9-115
+ *   launch_squareplus            src/cuda_kernels/squareplus_kernel.cu:11-68
+ *   launch_conv1d_step           src/cuda_kernels/conv1d_step.cu:60-79
+ *   MambaIntegerBlock.forward    src/mamba_integer_model.py:396-447
+ */
+#ifndef MAMBA_INT_H
+#define MAMBA_INT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    MI_OK = 0,
+    MI_ERR_NULL_POINTER = 1,   /* a required pointer is NULL */
+    MI_ERR_BAD_DIM = 2,        /* a size is negative, too large or inconsistent */
+    MI_ERR_BAD_ALIGNMENT = 3,  /* a pointer or leading dimension breaks the alignment rule */
+    MI_ERR_BAD_ARG = 4,        /* a shift, kind or other scalar is out of range */
+    MI_ERR_HIP = 5             /* the HIP runtime reported an error at launch */
+} mi_status;
+
+/* Output kinds of mi_bitlinear (spec rule 3). */
+typedef enum {
+    MI_OUT_INT32 = 0,      /* int32 acc */
+    MI_OUT_INT8 = 1,       /* int8 sat8(rshr(acc, shift)) */
+    MI_OUT_DECAY_MOD = 2,  /* int8 clamp(rshr(acc, shift), -20, 20) */
+    MI_OUT_RESIDUAL = 3,   /* int32 r = satR(r + rshr(acc*res_mult, res_shift)), in place */
+    MI_OUT_FLOAT = 4       /* fp32 acc * (w_scale * x_scale[m]) */
+} mi_out_kind;
+
+/* Library and spec version, e.g. "libmamba_int 0.1 (mi-spec-1, gfx950)". */
+const char *mi_version(void);
+/* Message of the calling thread's last failed call ("" if none). */
+const char *mi_last_error_string(void);
+
+/* ----------------------------------------------------------------- scans */
+
+/* Dyadic selective scan, config-1 layout (replaces launch_dyadic_scan,
+ * dyadic_mamba_kernel.cu:135-153, with the integer rule of :53-59).
+ * x int8 [batch,len,d]; b, c int8 [batch,len,nstate]; decay_num int32
+ * [d,nstate] in [0, 2^decay_shift]; y int32 [batch,len,d];
+ * h_in / h_out int32 [batch,d,nstate], each nullable (NULL h_in = zero state;
+ * h_in == h_out allowed).  decay_shift in [1,16]; nstate in [1,128]. */
+mi_status mi_dyadic_scan(const int8_t *x, const int8_t *b, const int8_t *c,
+                         const int32_t *decay_num, int decay_shift, int32_t *y,
+                         const int32_t *h_in, int32_t *h_out, int batch, int len, int d,
+                         int nstate, void *stream);
+
+/* Float-compat form with the exact semantics of the reference kernel
+ * launch_dyadic_scan (dyadic_mamba_kernel.cu:8-67,134-153): x, h fp32
+ * [batch,seq,dim]; nums, shifts int32 [batch,seq,dim] (shift in [0,62]);
+ * int64 state; scale_bits in [0,62]. */
+mi_status mi_dyadic_scan_f32(const float *x, const int32_t *nums, const int32_t *shifts,
+                             float *h, int batch, int seq, int dim, int scale_bits,
+                             void *stream);
+
+/* Elementwise recurrence, the integer form of DyadicScanFunction.apply
+ * (mamba_integer_model.py:260-316): u, nums int32 [batch,len,channels];
+ * h int32 [batch,len,channels] = sat32(floor(h_prev*num / 2^shift) + u);
+ * h_in / h_out int32 [batch,channels] nullable.  decay_shift in [1,30]. */
+mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t *nums, int decay_shift,
+                                     int32_t *h, const int32_t *h_in, int32_t *h_out,
+                                     int batch, int len, int channels, void *stream);
+
+/* Chunked multi-head scan, config-4 layout (replaces ssd_chunked_scan_forward,
+ * ssd_chunked_scan.py:382-422, head layout of ssd_multihead.py:541-566).
+ * x int8 [batch,len,heads,head_dim]; b, c int8 [batch,len,heads,nstate];
+ * decay_num int32 [heads] in [0, 2^decay_shift]; y int32
+ * [batch,len,heads,head_dim]; chunk_states int32
+ * [batch,ceil(len/chunk),heads,head_dim,nstate] nullable (state at the end of
+ * each chunk); h_in / h_out int32 [batch,heads,head_dim,nstate] nullable.
+ * Results are identical to the sequential scan for every chunk length. */
+mi_status mi_ssd_chunked_scan(const int8_t *x, const int8_t *b, const int8_t *c,
+                              const int32_t *decay_num, int decay_shift, int32_t *y,
+                              int32_t *chunk_states, const int32_t *h_in, int32_t *h_out,
+                              int batch, int len, int heads, int head_dim, int nstate, int chunk,
+                              void *stream);
+
+/* ------------------------------------------------------------ BitLinear */
+
+/* Pack ternary int8 [n,k] (values in {-1,0,1}, k % 16 == 0) into the 2-bit
+ * layout [n, k/4] (spec rule 2); the storage half of get_ternary_weights
+ * (rational_bitnet.py:215-219) and export_int8.py:79-82. */
+mi_status mi_pack_ternary(const int8_t *w, uint8_t *packed, int n, int k, void *stream);
+
+/* activation_quant_dynamic, 8 bits (rational_bitnet.py:88-111): x fp32
+ * [m,k] -> xq int8 [m,k], x_scale fp32 [m] (= amax/127). */
+mi_status mi_act_quant_f32(const float *x, int8_t *xq, float *x_scale, int m, int k,
+                           void *stream);
+
+/* out[m, n] = kind(sum_k a[m,k] * W[n,k]) (replaces BitLinear.forward's
+ * F.linear + rescale, rational_bitnet.py:204-208, and launch_bitlinear).
+ * a int8 [m, lda] (16-byte aligned, lda % 16 == 0); w_packed [n, k/4]
+ * (4-byte aligned); out [m, ldo] of the kind's element type (ldo % 4 == 0);
+ * k % 16 == 0.  shift in [0,31] for INT8/DECAY_MOD; res_shift in [0,62] for
+ * RESIDUAL; x_scale [m] and w_scale for FLOAT.  Chooses the MFMA tile GEMM
+ * for m > 64 and the register-unpack GEMV path for m <= 64. */
+mi_status mi_bitlinear(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
+                       int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
+                       const float *x_scale, float w_scale, void *stream);
+/* Same contract, forcing the MFMA tile GEMM (prefill path). */
+mi_status mi_bitlinear_gemm(const int8_t *a, int lda, const uint8_t *w_packed, void *out,
+                            int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
+                            int res_shift, const float *x_scale, float w_scale, void *stream);
+/* Same contract, forcing the decode GEMV (m <= 64). */
+mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, void *out,
+                            int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
+                            int res_shift, const float *x_scale, float w_scale, void *stream);
+
+/* ---------------------------------------------------------- block ops */
+
+/* Integer BitShiftNorm (spec rule 4.1; mamba_integer_model.py:144-184,
+ * 200-223): r int32 [tokens,dim] (Q8) -> out int8 [tokens,dim]; gamma int16
+ * [dim] (Q8). dim in [1, 8192]. */
+mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens,
+                           int dim, void *stream);
+
+/* Embedding (mamba_integer_model.py:470,487): r[t,:] = emb[ids[t],:] << 4.
+ * ids int64 [tokens] (each in [0,vocab)), emb int8 [vocab,dim], r int32. */
+mi_status mi_embed(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim,
+                   int vocab, void *stream);
+
+/* Depthwise causal conv (width 4) + squareplus (spec rules 4.3-4.4;
+ * mamba_integer_model.py:378,404-411; step form conv1d_step.cu:12-58).
+ * xz int8 [batch,len,xz_stride], x branch in columns [0,d_inner);
+ * conv_w int8 [d_inner,4]; conv_b int32 [d_inner]; state_in / state_out int8
+ * [batch,3,d_inner] nullable (NULL state_in = zeros; in == out allowed);
+ * xs int8 [batch,len,d_inner]. */
+mi_status mi_conv_squareplus(const int8_t *xz, int xz_stride, const int8_t *conv_w,
+                             const int32_t *conv_b, const int8_t *state_in, int8_t *state_out,
+                             int8_t *xs, int batch, int len, int d_inner, void *stream);
+
+/* Fused model scan (spec rules 4.7-4.11; MambaIntegerBlock.forward,
+ * mamba_integer_model.py:413-444): decay from base + dm, dt from dm, input
+ * xs*dt (x) B, scan, y = C.h, gate by z, requant.
+ * xs, dm int8 [batch,len,d_inner]; xp int8 [batch,len,xp_stride] with B at
+ * columns [b_off, b_off+nstate) and C at [b_off+nstate, b_off+2*nstate);
+ * z int8 [batch,len,z_stride] at column z_off; base int32 [d_inner,nstate] in
+ * [0,32000]; yo int8 [batch,len,d_inner]; h_in / h_out int32
+ * [batch,d_inner,nstate] nullable.  decay_shift == 15; nstate in [1,64]. */
+mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int8_t *xp, int xp_stride,
+                        int b_off, const int8_t *z, int z_stride, int z_off,
+                        const int32_t *base, int decay_shift, int s_y, int8_t *yo,
+                        const int32_t *h_in, int32_t *h_out, int batch, int len, int d_inner,
+                        int nstate, void *stream);
+
+/* Greedy pick (scripts/sft_mamba_integer.py:138-141 argmax): out[r] = first
+ * index of the maximum of logits[r, 0:cols] (int32 [rows, ld]). */
+mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, int cols,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA_INT_H */

@@ -1,0 +1,408 @@
+// BitLinear b1.58 on gfx950 (spec mi-spec-1, rules 2-3).
+//
+// acc[m,n] = sum_k a[m,k] * W[n,k], a int8, W ternary in the 2-bit word layout
+// (16 weights per 32-bit word; (word >> 2j) & 0x03030303 holds 4 codes in byte
+// order).  One v_perm_b32 against the byte table {0x00, 0x01, 0xFE, 0xFF}
+// turns 4 codes into 4 int8 weights, so a packed word becomes one 16-byte
+// MFMA operand in 4 AND/shift + 4 permute instructions.
+//
+// The product is computed as C^T = W * A^T with v_mfma_i32_16x16x64_i8:
+// MFMA operand A = 16 weight rows (n), operand B = 16 activation rows (m).
+// Lane l holds 16 consecutive k of row l%16 for k-group l/16 in both
+// operands, and result register r of lane l is (n = 4*(l/16) + r, m = l%16):
+// four consecutive output features of one token, i.e. one dword of int8
+// output or one 16-byte vector of int32 output per lane.
+//
+//   prefill GEMM: 128(n) x 128(m) block tile, 4 waves of 64x64, K staged 128 at
+//                 a time through LDS (packed weights stay packed in LDS and are
+//                 unpacked in registers), double buffered, one barrier per stage.
+//   decode GEMV:  m <= 64; a block owns 16 output features, its 4 waves split
+//                 K; each lane streams 16-byte words of packed weights straight
+//                 from HBM and unpacks them in registers.
+#include "mi_common.hpp"
+
+namespace mi {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i unpack16(uint32_t w) {
+    const uint32_t lut = 0xFFFE0100u;  // byte c = value of code c
+    v4i r;
+    r[0] = (int)__builtin_amdgcn_perm(lut, lut, w & 0x03030303u);
+    r[1] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 2) & 0x03030303u);
+    r[2] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 4) & 0x03030303u);
+    r[3] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 6) & 0x03030303u);
+    return r;
+}
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+struct GemmArgs {
+    const int8_t *a;
+    const uint32_t *w;   // [N][K/16] words
+    void *out;
+    const float *x_scale;
+    int64_t lda, ldo;
+    int M, N, K;
+    int kw;              // K / 16 words per weight row
+    int shift;
+    int32_t res_mult;
+    int res_shift;
+    float w_scale;
+};
+
+// Epilogue for 4 consecutive features n..n+3 of token m (n % 4 == 0).
+template <int KIND>
+__device__ __forceinline__ void store4(const GemmArgs &g, int m, int n, v4i acc) {
+    if (m >= g.M || n >= g.N) return;
+    const bool full = n + 3 < g.N;
+    if constexpr (KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD) {
+        int8_t *o = (int8_t *)g.out + (int64_t)m * g.ldo + n;
+        int v[4];
+        for (int r = 0; r < 4; ++r) {
+            int q = rshr32(acc[r], g.shift);
+            v[r] = KIND == MI_OUT_INT8 ? clamp32(q, -127, 127) : clamp32(q, -20, 20);
+        }
+        if (full) {
+            *reinterpret_cast<uint32_t *>(o) = (uint32_t)(v[0] & 255) | ((uint32_t)(v[1] & 255) << 8) |
+                                               ((uint32_t)(v[2] & 255) << 16) | ((uint32_t)(v[3] & 255) << 24);
+        } else {
+            for (int r = 0; r < 4 && n + r < g.N; ++r) o[r] = (int8_t)v[r];
+        }
+    } else if constexpr (KIND == MI_OUT_INT32) {
+        int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + n;
+        if (full) {
+            *reinterpret_cast<v4i *>(o) = acc;
+        } else {
+            for (int r = 0; r < 4 && n + r < g.N; ++r) o[r] = acc[r];
+        }
+    } else if constexpr (KIND == MI_OUT_RESIDUAL) {
+        int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + n;
+        for (int r = 0; r < 4 && n + r < g.N; ++r) {
+            const int64_t delta = rshr64((int64_t)acc[r] * g.res_mult, g.res_shift);
+            o[r] = (int32_t)clamp64((int64_t)o[r] + delta, -kResidualLimit, kResidualLimit);
+        }
+    } else {  // MI_OUT_FLOAT: fp32(acc) * (w_scale * x_scale[m]) as rational_bitnet.py:208
+        float *o = (float *)g.out + (int64_t)m * g.ldo + n;
+        const float sc = __fmul_rn(g.w_scale, g.x_scale[m]);
+        for (int r = 0; r < 4 && n + r < g.N; ++r) o[r] = __fmul_rn((float)acc[r], sc);
+    }
+}
+
+// ------------------------------------------------------------ prefill GEMM
+constexpr int kBM = 128, kBN = 128, kBK = 128;
+constexpr int kApitch = kBK + 16;       // bytes per staged activation row (bank-conflict free b128 reads)
+constexpr int kWpitch = kBK / 16 + 4;   // words per staged weight row (conflict free b32 reads)
+
+template <int KIND>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+    __shared__ __align__(16) int8_t sA[2][kBM * kApitch];
+    __shared__ __align__(16) uint32_t sW[2][kBN * kWpitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int l16 = lane & 15, lq = lane >> 4;
+
+    // blockIdx.x walks m-tiles fastest so the blocks that share a weight tile run together
+    const int mtiles = (g.M + kBM - 1) / kBM;
+    const int m0 = (blockIdx.x % mtiles) * kBM;
+    const int n0 = (blockIdx.x / mtiles) * kBN;
+
+    uint4 ra[4];
+    uint32_t rw[4];
+    auto load_stage = [&](int k0) {
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;         // 1024 pieces of 16 bytes
+            const int row = i >> 3, c16 = i & 7;
+            const int m = m0 + row, k = k0 + c16 * 16;
+            ra[j] = (m < g.M && k < g.K) ? *reinterpret_cast<const uint4 *>(g.a + (int64_t)m * g.lda + k)
+                                         : make_uint4(0, 0, 0, 0);
+        }
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;         // 1024 words
+            const int row = i >> 3, c = i & 7;
+            const int n = n0 + row, kw = (k0 >> 4) + c;
+            rw[j] = (n < g.N && kw < g.kw) ? g.w[(int64_t)n * g.kw + kw] : 0u;
+        }
+    };
+    auto store_stage = [&](int buf) {
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            const int row = i >> 3, c16 = i & 7;
+            *reinterpret_cast<uint4 *>(&sA[buf][row * kApitch + c16 * 16]) = ra[j];
+        }
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            const int row = i >> 3, c = i & 7;
+            sW[buf][row * kWpitch + c] = rw[j];
+        }
+    };
+
+    v4i acc[4][4];
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    const int nk = (g.K + kBK - 1) / kBK;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
+        for (int ks = 0; ks < kBK / 64; ++ks) {
+            v4i fw[4], fa[4];
+            for (int i = 0; i < 4; ++i) {
+                const int row = wn * 64 + i * 16 + l16;
+                fw[i] = unpack16(sW[buf][row * kWpitch + ks * 4 + lq]);
+            }
+            for (int j = 0; j < 4; ++j) {
+                const int row = wm * 64 + j * 16 + l16;
+                fa[j] = *reinterpret_cast<const v4i *>(&sA[buf][row * kApitch + ks * 64 + lq * 16]);
+            }
+            for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fw[i], fa[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j)
+            store4<KIND>(g, m0 + wm * 64 + j * 16 + l16, n0 + wn * 64 + i * 16 + 4 * lq, acc[i][j]);
+}
+
+// -------------------------------------------------------------- decode GEMV
+// Block = 4 waves owning 16 output features; wave w takes the 256-wide K
+// super-steps w, w+4, ...  Lane (r = l%16, q = l/16) loads words
+// [16s + 4q, 16s + 4q + 4) of weight row n0 + r (one 16-byte load when the
+// row pitch allows it) and feeds MFMA j with word 16s + 4q + j against
+// activation bytes k = 16*(16s + 4q + j) .. +16 of token 16t + r.
+template <int MT, int KIND, bool VEC>
+__global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
+    __shared__ v4i red[3][MT][64];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int n = n0 + l16;
+    const int nsuper = (g.kw + 15) / 16;
+
+    v4i acc[MT];
+    for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
+
+    for (int s = wave; s < nsuper; s += 4) {
+        const int w0 = 16 * s + 4 * lq;
+        uint32_t wv[4];
+        if (VEC) {
+            if (n < g.N && w0 < g.kw) {
+                const uint4 q = *reinterpret_cast<const uint4 *>(g.w + (int64_t)n * g.kw + w0);
+                wv[0] = q.x; wv[1] = q.y; wv[2] = q.z; wv[3] = q.w;
+            } else {
+                wv[0] = wv[1] = wv[2] = wv[3] = 0u;
+            }
+        } else {
+            for (int j = 0; j < 4; ++j)
+                wv[j] = (n < g.N && w0 + j < g.kw) ? g.w[(int64_t)n * g.kw + w0 + j] : 0u;
+        }
+        for (int j = 0; j < 4; ++j) {
+            const v4i fw = unpack16(wv[j]);
+            const int k = 16 * (w0 + j);
+            for (int t = 0; t < MT; ++t) {
+                const int m = 16 * t + l16;
+                v4i fa = v4i{0, 0, 0, 0};
+                if (m < g.M && k < g.K) fa = *reinterpret_cast<const v4i *>(g.a + (int64_t)m * g.lda + k);
+                acc[t] = mfma(fw, fa, acc[t]);
+            }
+        }
+    }
+    if (wave > 0)
+        for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
+    __syncthreads();
+    if (wave == 0) {
+        for (int t = 0; t < MT; ++t) {
+            v4i v = acc[t] + red[0][t][lane] + red[1][t][lane] + red[2][t][lane];
+            store4<KIND>(g, 16 * t + l16, n0 + 4 * lq, v);
+        }
+    }
+}
+
+// ------------------------------------------------------------ helpers
+__global__ void pack_ternary_kernel(const int8_t *w, uint32_t *p, int64_t words, int kw) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= words) return;
+    const int8_t *src = w + i * 16;  // row-major [n][k]: word i covers k = 16*(i%kw) of row i/kw
+    uint32_t word = 0;
+    for (int q = 0; q < 16; ++q) word |= ((uint32_t)src[q] & 3u) << (8 * (q & 3) + 2 * (q >> 2));
+    p[i] = word;
+}
+
+// activation_quant_dynamic (rational_bitnet.py:102-111) in IEEE fp32, one
+// block per row.
+__global__ __launch_bounds__(256) void act_quant_kernel(const float *x, int8_t *xq, float *x_scale, int K) {
+    __shared__ float red[256];
+    const int64_t row = blockIdx.x;
+    const float *xr = x + row * K;
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(xr[k]));
+    red[threadIdx.x] = amax;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const float scale = fmaxf(red[0], 1e-8f);
+    const float inv = __fdiv_rn(127.0f, scale);
+    for (int k = threadIdx.x; k < K; k += 256) {
+        float q = rintf(__fmul_rn(xr[k], inv));
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        xq[row * K + k] = (int8_t)q;
+    }
+    if (threadIdx.x == 0) x_scale[row] = __fdiv_rn(scale, 127.0f);
+}
+
+// ------------------------------------------------------------ dispatch
+mi_status validate(const char *fn, const int8_t *a, int lda, const uint8_t *w, void *out, int ldo, int kind, int m,
+                   int n, int k, int shift, int res_shift, const float *x_scale) {
+    MI_REQUIRE(m >= 0 && n >= 0 && k >= 0, MI_ERR_BAD_DIM, "%s: negative size (m=%d n=%d k=%d)", fn, m, n, k);
+    MI_REQUIRE(k % 16 == 0, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 16", fn, k);
+    MI_REQUIRE(kind >= MI_OUT_INT32 && kind <= MI_OUT_FLOAT, MI_ERR_BAD_ARG, "%s: unknown output kind %d", fn, kind);
+    if ((int64_t)m * n == 0) return MI_OK;
+    MI_REQUIRE(a && w && out, MI_ERR_NULL_POINTER, "%s: a, w_packed and out are required", fn);
+    MI_REQUIRE(lda >= k && lda % 16 == 0, MI_ERR_BAD_ALIGNMENT, "%s: lda=%d must be >= k and a multiple of 16", fn, lda);
+    MI_REQUIRE(ldo >= n && ldo % 4 == 0, MI_ERR_BAD_ALIGNMENT, "%s: ldo=%d must be >= n and a multiple of 4", fn, ldo);
+    MI_REQUIRE(aligned(a, 16), MI_ERR_BAD_ALIGNMENT, "%s: a must be 16-byte aligned", fn);
+    MI_REQUIRE(aligned(w, 4), MI_ERR_BAD_ALIGNMENT, "%s: w_packed must be 4-byte aligned", fn);
+    MI_REQUIRE(aligned(out, kind == MI_OUT_INT8 || kind == MI_OUT_DECAY_MOD ? 4 : 16), MI_ERR_BAD_ALIGNMENT,
+               "%s: out is misaligned", fn);
+    if (kind == MI_OUT_INT8 || kind == MI_OUT_DECAY_MOD)
+        MI_REQUIRE(shift >= 0 && shift <= 30, MI_ERR_BAD_ARG, "%s: shift=%d outside [0,30]", fn, shift);
+    if (kind == MI_OUT_RESIDUAL)
+        MI_REQUIRE(res_shift >= 0 && res_shift <= 62, MI_ERR_BAD_ARG, "%s: res_shift=%d outside [0,62]", fn, res_shift);
+    if (kind == MI_OUT_FLOAT) MI_REQUIRE(x_scale, MI_ERR_NULL_POINTER, "%s: x_scale is required for FLOAT output", fn);
+    return MI_OK;
+}
+
+GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ldo, int m, int n, int k, int shift,
+                   int32_t res_mult, int res_shift, const float *x_scale, float w_scale) {
+    GemmArgs g{};
+    g.a = a; g.w = reinterpret_cast<const uint32_t *>(w); g.out = out; g.x_scale = x_scale;
+    g.lda = lda; g.ldo = ldo; g.M = m; g.N = n; g.K = k; g.kw = k / 16;
+    g.shift = shift; g.res_mult = res_mult; g.res_shift = res_shift; g.w_scale = w_scale;
+    return g;
+}
+
+template <int KIND>
+hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
+    const int blocks = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);
+    hipLaunchKernelGGL(gemm_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(int kind, const GemmArgs &g, hipStream_t st) {
+    switch (kind) {
+        case MI_OUT_INT32: return launch_gemm_kind<MI_OUT_INT32>(g, st);
+        case MI_OUT_INT8: return launch_gemm_kind<MI_OUT_INT8>(g, st);
+        case MI_OUT_DECAY_MOD: return launch_gemm_kind<MI_OUT_DECAY_MOD>(g, st);
+        case MI_OUT_RESIDUAL: return launch_gemm_kind<MI_OUT_RESIDUAL>(g, st);
+        default: return launch_gemm_kind<MI_OUT_FLOAT>(g, st);
+    }
+}
+
+template <int MT, int KIND>
+hipError_t launch_gemv_mt(const GemmArgs &g, hipStream_t st) {
+    const dim3 grid((unsigned)((g.N + 15) / 16));
+    const bool vec = (g.kw % 4 == 0) && aligned(g.w, 16);
+    if (vec)
+        hipLaunchKernelGGL((gemv_kernel<MT, KIND, true>), grid, dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL((gemv_kernel<MT, KIND, false>), grid, dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+
+template <int KIND>
+hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
+    if (g.M <= 16) return launch_gemv_mt<1, KIND>(g, st);
+    if (g.M <= 32) return launch_gemv_mt<2, KIND>(g, st);
+    return launch_gemv_mt<4, KIND>(g, st);
+}
+
+hipError_t launch_gemv(int kind, const GemmArgs &g, hipStream_t st) {
+    switch (kind) {
+        case MI_OUT_INT32: return launch_gemv_kind<MI_OUT_INT32>(g, st);
+        case MI_OUT_INT8: return launch_gemv_kind<MI_OUT_INT8>(g, st);
+        case MI_OUT_DECAY_MOD: return launch_gemv_kind<MI_OUT_DECAY_MOD>(g, st);
+        case MI_OUT_RESIDUAL: return launch_gemv_kind<MI_OUT_RESIDUAL>(g, st);
+        default: return launch_gemv_kind<MI_OUT_FLOAT>(g, st);
+    }
+}
+
+enum class Path { kAuto, kGemm, kGemv };
+
+mi_status bitlinear_impl(const char *fn, Path path, const int8_t *a, int lda, const uint8_t *w, void *out, int ldo,
+                         int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
+                         const float *x_scale, float w_scale, void *stream) {
+    clear_error();
+    mi_status st = validate(fn, a, lda, w, out, ldo, kind, m, n, k, shift, res_shift, x_scale);
+    if (st != MI_OK || (int64_t)m * n == 0) return st;
+    if (path == Path::kGemv) MI_REQUIRE(m <= 64, MI_ERR_BAD_DIM, "%s: the GEMV path takes m <= 64 (m=%d)", fn, m);
+    const GemmArgs g = make_args(a, lda, w, out, ldo, m, n, k, shift, res_mult, res_shift, x_scale, w_scale);
+    const bool gemv = path == Path::kGemv || (path == Path::kAuto && m <= 64);
+    hipError_t e = gemv ? launch_gemv(kind, g, as_stream(stream)) : launch_gemm(kind, g, as_stream(stream));
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status mi_bitlinear(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo, int kind,
+                                  int m, int n, int k, int shift, int32_t res_mult, int res_shift,
+                                  const float *x_scale, float w_scale, void *stream) {
+    return bitlinear_impl("mi_bitlinear", Path::kAuto, a, lda, w_packed, out, ldo, kind, m, n, k, shift, res_mult,
+                          res_shift, x_scale, w_scale, stream);
+}
+
+extern "C" mi_status mi_bitlinear_gemm(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
+                                       int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
+                                       const float *x_scale, float w_scale, void *stream) {
+    return bitlinear_impl("mi_bitlinear_gemm", Path::kGemm, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
+                          res_mult, res_shift, x_scale, w_scale, stream);
+}
+
+extern "C" mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
+                                       int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
+                                       const float *x_scale, float w_scale, void *stream) {
+    return bitlinear_impl("mi_bitlinear_gemv", Path::kGemv, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
+                          res_mult, res_shift, x_scale, w_scale, stream);
+}
+
+extern "C" mi_status mi_pack_ternary(const int8_t *w, uint8_t *packed, int n, int k, void *stream) {
+    clear_error();
+    MI_REQUIRE(n >= 0 && k >= 0, MI_ERR_BAD_DIM, "mi_pack_ternary: negative size");
+    MI_REQUIRE(k % 16 == 0, MI_ERR_BAD_DIM, "mi_pack_ternary: k=%d must be a multiple of 16", k);
+    if ((int64_t)n * k == 0) return MI_OK;
+    MI_REQUIRE(w && packed, MI_ERR_NULL_POINTER, "mi_pack_ternary: w and packed are required");
+    MI_REQUIRE(aligned(packed, 4), MI_ERR_BAD_ALIGNMENT, "mi_pack_ternary: packed must be 4-byte aligned");
+    const int64_t words = (int64_t)n * (k / 16);
+    hipLaunchKernelGGL(pack_ternary_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, as_stream(stream), w,
+                       reinterpret_cast<uint32_t *>(packed), words, k / 16);
+    return check_launch("mi_pack_ternary");
+}
+
+extern "C" mi_status mi_act_quant_f32(const float *x, int8_t *xq, float *x_scale, int m, int k, void *stream) {
+    clear_error();
+    MI_REQUIRE(m >= 0 && k >= 0, MI_ERR_BAD_DIM, "mi_act_quant_f32: negative size");
+    if (m == 0) return MI_OK;
+    MI_REQUIRE(k > 0, MI_ERR_BAD_DIM, "mi_act_quant_f32: k must be positive");
+    MI_REQUIRE(x && xq && x_scale, MI_ERR_NULL_POINTER, "mi_act_quant_f32: x, xq and x_scale are required");
+    hipLaunchKernelGGL(act_quant_kernel, dim3((unsigned)m), dim3(256), 0, as_stream(stream), x, xq, x_scale, k);
+    return check_launch("mi_act_quant_f32");
+}

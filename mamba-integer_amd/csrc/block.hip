@@ -1,0 +1,237 @@
+// Elementwise and row stages of the integer Mamba block on gfx950 (spec
+// mi-spec-1, rules 4.1, 4.3-4.4 and the model's embedding / greedy pick).
+#include "mi_common.hpp"
+
+namespace mi {
+namespace {
+
+// ------------------------------------------------------------ BitShiftNorm
+// One block per token.  The row is read once into registers; the mean and the
+// sum of squares are exact int64 block reductions.
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxPer = 32;  // dim <= 8192
+
+__device__ int64_t block_sum64(int64_t v, int64_t *red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    int64_t t = 0;
+    for (int w = 0; w < kNormThreads / 64; ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+__global__ __launch_bounds__(kNormThreads) void norm_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
+                                                            int dim) {
+    __shared__ int64_t red[kNormThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int32_t *rr = r + row * dim;
+    int32_t v[kNormMaxPer];
+    int64_t s = 0;
+    for (int j = 0; j < kNormMaxPer; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        v[j] = i < dim ? rr[i] : 0;
+        s += v[j];
+    }
+    const int64_t sum = block_sum64(s, red);
+    const int64_t mu = sum >= 0 ? sum / dim : -((-sum + dim - 1) / dim);  // floor
+    int64_t q = 0;
+    for (int j = 0; j < kNormMaxPer; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < dim) {
+            const int64_t x = v[j] - mu;
+            q += x * x;
+        }
+    }
+    const int64_t S = block_sum64(q, red);
+    // threshold table of _find_power_of_2_scale (mamba_integer_model.py:169-182)
+    // on var = S / (dim * 2^16): k = #[var >= 4^j, j=1..8] - #[var < 4^-j, j=1..3]
+    int kk = 0;
+    for (int j = 1; j <= 8; ++j) kk += S >= ((int64_t)dim << (2 * (j + 8)));
+    for (int j = 1; j <= 3; ++j) kk -= S < ((int64_t)dim << (2 * (8 - j)));
+    const int sh = 12 + kk;
+    for (int j = 0; j < kNormMaxPer; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < dim) out[row * dim + i] = (int8_t)clamp64(rshr64((int64_t)(v[j] - mu) * gamma[i], sh), -127, 127);
+    }
+}
+
+// --------------------------------------------------------------- embedding
+__global__ void embed_kernel(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)tokens * dim) return;
+    const int64_t t = i / dim;
+    const int c = (int)(i % dim);
+    const int64_t id = ids[t];
+    // an id outside [0, vocab) reads as a zero row instead of faulting
+    r[i] = (id >= 0 && id < vocab) ? (int32_t)emb[id * dim + c] * 16 : 0;
+}
+
+// ----------------------------------------------------- conv + squareplus
+// Exact squareplus of spec rule 4.4: a Newton step on the hardware
+// reciprocal-square-root estimate gives sqrt(v^2 + 2^22) to within a unit,
+// and two bounded integer corrections make it the exact floor.
+__device__ __forceinline__ int sqp_q(int32_t c) {
+    const int32_t v = clamp32(c, -51200, 51200);
+    const uint32_t av = (uint32_t)(v < 0 ? -v : v);
+    const uint32_t Y = av * av + (1u << 22);  // < 2^32
+    const float yf = (float)Y;
+    float rs = __builtin_amdgcn_rsqf(yf);
+    rs = rs * (1.5f - 0.5f * yf * rs * rs);
+    uint32_t s = (uint32_t)(yf * rs);
+    if (s > 65535u) s = 65535u;
+    for (int it = 0; it < 4 && (uint64_t)s * s > Y; ++it) --s;
+    for (int it = 0; it < 4 && (uint64_t)(s + 1) * (s + 1) <= Y; ++it) ++s;
+    return clamp32(rshr32(v + (int32_t)s, 7), -127, 127);
+}
+
+constexpr int kConvTT = 16;  // time steps per thread
+
+// Thread = (b, group of kConvTT steps, 4 channels).  The thread of step-group 0
+// owns the conv state of its channels: it reads state_in and writes state_out
+// (from the inputs x[L-3..L-1], which no thread modifies), so in-place state
+// updates are race free.
+__global__ __launch_bounds__(256) void conv_sqp_kernel(const int8_t *xz, int64_t xz_stride, const int8_t *w,
+                                                       const int32_t *bias, const int8_t *st_in, int8_t *st_out,
+                                                       int8_t *xs, int B, int L, int D) {
+    const int D4 = D / 4;
+    const int TG = (L + kConvTT - 1) / kConvTT;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)B * TG * D4) return;
+    const int d4 = (int)(i % D4);
+    const int tg = (int)((i / D4) % TG);
+    const int b = (int)(i / ((int64_t)D4 * TG));
+    const int d = d4 * 4;
+
+    int wv[4][4], bv[4];
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t ww = *reinterpret_cast<const uint32_t *>(w + (int64_t)(d + c) * 4);
+        for (int j = 0; j < 4; ++j) wv[c][j] = (int)(int8_t)(ww >> (8 * j));
+        bv[c] = bias[d + c];
+    }
+    auto xrow = [&](int t) -> uint32_t {  // 4 channels of x at time t (t may be < 0: conv state)
+        if (t >= 0) return *reinterpret_cast<const uint32_t *>(xz + ((int64_t)b * L + t) * xz_stride + d);
+        if (!st_in) return 0u;
+        return *reinterpret_cast<const uint32_t *>(st_in + ((int64_t)b * 3 + (3 + t)) * D + d);
+    };
+    const int t0 = tg * kConvTT;
+    const int t1 = min(L, t0 + kConvTT);
+    uint32_t win[3] = {xrow(t0 - 3), xrow(t0 - 2), xrow(t0 - 1)};
+    uint32_t keep_state[3] = {win[0], win[1], win[2]};  // x[-3..-1] for the state update when L < 3
+    for (int t = t0; t < t1; ++t) {
+        const uint32_t cur = xrow(t);
+        uint32_t o = 0;
+        for (int c = 0; c < 4; ++c) {
+            int32_t acc = bv[c];
+            acc += wv[c][0] * (int)(int8_t)(win[0] >> (8 * c));
+            acc += wv[c][1] * (int)(int8_t)(win[1] >> (8 * c));
+            acc += wv[c][2] * (int)(int8_t)(win[2] >> (8 * c));
+            acc += wv[c][3] * (int)(int8_t)(cur >> (8 * c));
+            o |= (uint32_t)(sqp_q(acc) & 255) << (8 * c);
+        }
+        *reinterpret_cast<uint32_t *>(xs + ((int64_t)b * L + t) * D + d) = o;
+        win[0] = win[1];
+        win[1] = win[2];
+        win[2] = cur;
+    }
+    if (tg == 0 && st_out) {
+        for (int j = 0; j < 3; ++j) {
+            const int t = L - 3 + j;
+            const uint32_t val = t >= 0 ? *reinterpret_cast<const uint32_t *>(xz + ((int64_t)b * L + t) * xz_stride + d)
+                                        : keep_state[3 + t];
+            *reinterpret_cast<uint32_t *>(st_out + ((int64_t)b * 3 + j) * D + d) = val;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- argmax
+__global__ __launch_bounds__(256) void argmax_kernel(const int32_t *logits, int64_t ld, int64_t *out, int cols) {
+    __shared__ int32_t sv[256];
+    __shared__ int32_t si[256];
+    const int64_t row = blockIdx.x;
+    const int32_t *lr = logits + row * ld;
+    int32_t best = INT32_MIN;
+    int32_t bi = 0x7fffffff;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        const int32_t v = lr[c];
+        if (v > best) { best = v; bi = c; }  // strided scan keeps the first max of this thread
+    }
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            const int32_t v2 = sv[threadIdx.x + s], i2 = si[threadIdx.x + s];
+            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 < si[threadIdx.x])) {
+                sv[threadIdx.x] = v2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[row] = si[0];
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
+                                      void *stream) {
+    clear_error();
+    MI_REQUIRE(tokens >= 0, MI_ERR_BAD_DIM, "mi_bitshift_norm: negative tokens");
+    MI_REQUIRE(dim >= 1 && dim <= kNormThreads * kNormMaxPer, MI_ERR_BAD_DIM, "mi_bitshift_norm: dim=%d outside [1,%d]",
+               dim, kNormThreads * kNormMaxPer);
+    if (tokens == 0) return MI_OK;
+    MI_REQUIRE(r && gamma && out, MI_ERR_NULL_POINTER, "mi_bitshift_norm: r, gamma and out are required");
+    hipLaunchKernelGGL(norm_kernel, dim3((unsigned)tokens), dim3(kNormThreads), 0, as_stream(stream), r, gamma, out, dim);
+    return check_launch("mi_bitshift_norm");
+}
+
+extern "C" mi_status mi_embed(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab,
+                              void *stream) {
+    clear_error();
+    MI_REQUIRE(tokens >= 0 && dim >= 0 && vocab >= 0, MI_ERR_BAD_DIM, "mi_embed: negative size");
+    if ((int64_t)tokens * dim == 0) return MI_OK;
+    MI_REQUIRE(ids && emb && r, MI_ERR_NULL_POINTER, "mi_embed: ids, emb and r are required");
+    const int64_t n = (int64_t)tokens * dim;
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), ids, emb, r,
+                       tokens, dim, vocab);
+    return check_launch("mi_embed");
+}
+
+extern "C" mi_status mi_conv_squareplus(const int8_t *xz, int xz_stride, const int8_t *conv_w, const int32_t *conv_b,
+                                        const int8_t *state_in, int8_t *state_out, int8_t *xs, int batch, int len,
+                                        int d_inner, void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_conv_squareplus: negative size");
+    MI_REQUIRE(d_inner % 4 == 0, MI_ERR_BAD_DIM, "mi_conv_squareplus: d_inner=%d must be a multiple of 4", d_inner);
+    MI_REQUIRE(xz_stride >= d_inner && xz_stride % 4 == 0, MI_ERR_BAD_ALIGNMENT,
+               "mi_conv_squareplus: xz_stride=%d must be >= d_inner and a multiple of 4", xz_stride);
+    if ((int64_t)batch * d_inner == 0 || len == 0) {
+        MI_REQUIRE(!state_out || state_out == state_in, MI_ERR_BAD_ARG,
+                   "mi_conv_squareplus: len=0 leaves state_out unwritten; pass state_out == state_in");
+        return MI_OK;
+    }
+    MI_REQUIRE(xz && conv_w && conv_b && xs, MI_ERR_NULL_POINTER, "mi_conv_squareplus: xz, conv_w, conv_b, xs required");
+    MI_REQUIRE(aligned(xz, 4) && aligned(conv_w, 4) && aligned(xs, 4) && aligned(state_in, 4) && aligned(state_out, 4),
+               MI_ERR_BAD_ALIGNMENT, "mi_conv_squareplus: pointers must be 4-byte aligned");
+    const int64_t threads = (int64_t)batch * ((len + kConvTT - 1) / kConvTT) * (d_inner / 4);
+    hipLaunchKernelGGL(conv_sqp_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, as_stream(stream), xz,
+                       (int64_t)xz_stride, conv_w, conv_b, state_in, state_out, xs, batch, len, d_inner);
+    return check_launch("mi_conv_squareplus");
+}
+
+extern "C" mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, int cols, void *stream) {
+    clear_error();
+    MI_REQUIRE(rows >= 0 && cols >= 0, MI_ERR_BAD_DIM, "mi_argmax_i32: negative size");
+    MI_REQUIRE(ld >= cols, MI_ERR_BAD_DIM, "mi_argmax_i32: ld=%d < cols=%d", ld, cols);
+    if (rows == 0) return MI_OK;
+    MI_REQUIRE(cols >= 1, MI_ERR_BAD_DIM, "mi_argmax_i32: cols must be positive");
+    MI_REQUIRE(logits && out, MI_ERR_NULL_POINTER, "mi_argmax_i32: logits and out are required");
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), logits, (int64_t)ld, out,
+                       cols);
+    return check_launch("mi_argmax_i32");
+}

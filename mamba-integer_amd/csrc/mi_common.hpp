@@ -1,0 +1,71 @@
+// Shared helpers of libmamba_int: status reporting, argument checks and the
+// integer rounding/saturation primitives of spec mi-spec-1.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mamba_int.h"
+
+namespace mi {
+
+// Records a message for mi_last_error_string() and returns `st`.
+mi_status fail(mi_status st, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Checks the launch just enqueued; returns MI_OK or MI_ERR_HIP with a message.
+mi_status check_launch(const char *what);
+// Clears the calling thread's error message (start of every entry point).
+void clear_error();
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// ------------------------------------------------------ integer primitives
+__host__ __device__ __forceinline__ int64_t rshr64(int64_t v, int s) {
+    return s <= 0 ? v : ((v + ((int64_t)1 << (s - 1))) >> s);
+}
+__host__ __device__ __forceinline__ int32_t rshr32(int32_t v, int s) {
+    // exact for |v| < 2^31 - 2^(s-1): callers guarantee it (|acc| <= K*127)
+    return s <= 0 ? v : ((v + (1 << (s - 1))) >> s);
+}
+__host__ __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+__host__ __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+__host__ __device__ __forceinline__ int32_t sat32_64(int64_t v) {
+    return (int32_t)clamp64(v, INT32_MIN, INT32_MAX);
+}
+__host__ __device__ __forceinline__ int32_t sat8(int32_t v) { return clamp32(v, -127, 127); }
+constexpr int32_t kResidualLimit = (1 << 23) - 1;
+
+// Exact floor(sqrt(v)) for v < 2^62 (host and device): a float estimate
+// refined by integer correction steps.
+__host__ __device__ __forceinline__ uint64_t isqrt64(uint64_t v) {
+    uint64_t s = (uint64_t)sqrt((double)v);
+    while (s * s > v) --s;
+    while ((s + 1) * (s + 1) <= v) ++s;
+    return s;
+}
+
+// dt of spec rule 4.8 (mamba_integer_model.py:427) for dm in [-20, 20].
+__host__ __device__ inline int32_t dt_q16(int dm) {
+    int64_t s = (int64_t)dm * 65536 +
+                (int64_t)isqrt64((uint64_t)((int64_t)dm * dm) * (1ull << 32) + (1ull << 34));
+    int64_t sq = s >> 1;
+    return (int32_t)clamp64(rshr64(655 * sq, 16), 66, 6554);
+}
+
+// Gate of spec rule 4.11 (mamba_integer_model.py:124-132), Q15, z in Q4.
+__host__ __device__ inline int32_t gate_q15(int z) {
+    int32_t a = z < 0 ? -z : z;
+    int32_t q = (16384 * a) / (16 + a);
+    return 16384 + (z < 0 ? -q : q);
+}
+
+}  // namespace mi
+
+#define MI_REQUIRE(cond, st, ...)                     \
+    do {                                              \
+        if (!(cond)) return ::mi::fail((st), __VA_ARGS__); \
+    } while (0)

@@ -1,0 +1,565 @@
+// Dyadic selective scans for gfx950 (spec mi-spec-1, rule 1 and 4.7-4.11).
+//
+// The recurrence h_t = sat32(floor(h_{t-1} * n / 2^k) + u_t) is not
+// associative (the floor does not compose), so exact parallelism comes only
+// from independent lanes: (batch, head, channel, state).  Time stays
+// sequential inside every lane.  The scan is integer-VALU bound, so the
+// kernels are built around a short per-update instruction sequence:
+//
+//   state kept split as h = hh * 2^k + hl with hl in [0, 2^k):
+//     c   = (hl * n) >> k          v_mul_u32_u24 + v_lshrrev      (hl*n < 2^32)
+//     h'  = hh * n + c             v_mad_i32_i24                  (fits int32)
+//     h'' = sat32(h' + u)          v_add_i32 clamp
+//     hh, hl = split(h'')          v_ashrrev + v_and
+//     yhi += C*hh; ylo += C*hl     2 x v_mad_i32_i24               (exact int32 partials)
+//
+// floor(h*n/2^k) = hh*n + floor(hl*n/2^k) exactly because hh*n is an integer,
+// and y = 2^k * sum(C*hh) + sum(C*hl) is recombined in int64 once per step.
+// This holds for 0 <= n <= 2^k with k = 15 and N <= 128 (|hh| <= 2^16, so
+// |sum C*hh| <= 128*128*2^16 = 2^30; hl*n < 2^31); other shifts and shapes
+// take the plain int64 kernels at the end.
+//
+// Layout: a block owns CH = 256/G channels of one (batch, head); G adjacent
+// lanes share a channel and hold S = N/G states each; their partial y sums
+// are combined with DPP adds.  Inputs of TC time steps are staged through LDS
+// (prefetched into registers one chunk ahead), x-like bytes transposed to
+// channel-major so one ds_read_b32 serves 4 steps; outputs are staged in LDS
+// and written with 16-byte stores.
+#include "mi_common.hpp"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTC = 64;  // time steps per staged chunk
+
+enum ScanMode { kModeChannel = 0, kModeHead = 1, kModeModel = 2 };
+
+template <int G>
+__device__ __forceinline__ int group_sum(int v) {
+    // Sum over the G adjacent lanes of a channel group; every lane gets it.
+    if constexpr (G >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    if constexpr (G >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    if constexpr (G >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    if constexpr (G >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); // row_mirror
+    return v;
+}
+
+__device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
+
+struct ScanArgs {
+    const int8_t *x;       // channel/head modes: x; model mode: xs
+    const int8_t *bsrc;    // B rows
+    const int8_t *csrc;    // C rows
+    const int32_t *decay;  // [P][N] (channel), [H] (head), base [P][N] (model)
+    int32_t *y;            // int32 y (channel/head)
+    int8_t *yo;            // int8 gated output (model)
+    int32_t *chunk_states; // head mode, nullable
+    const int32_t *h_in;
+    int32_t *h_out;
+    const int8_t *dm;      // model
+    const int8_t *z;       // model
+    int64_t x_row;         // element stride between consecutive (b,t) rows of x/y (= H*P)
+    int64_t bc_row;        // stride between consecutive (b,t) rows of B/C
+    int64_t z_row;         // model: row stride of z
+    int B, L, H, P;
+    int k;
+    int s_y;
+    int nchunks_out;       // head mode: number of chunk_states chunks (ceil(L/cs))
+    int cs;                // head mode: chunk length of chunk_states
+};
+
+// Loads 16 consecutive bytes (16-byte aligned) or zeros when out of range.
+__device__ __forceinline__ uint4 load16(const int8_t *p, bool ok) {
+    if (ok) return *reinterpret_cast<const uint4 *>(p);
+    return make_uint4(0, 0, 0, 0);
+}
+
+template <int N, int G, int MODE>
+__global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
+    constexpr int S = N / G;
+    constexpr int CH = kThreads / G;
+    constexpr int XP = kTC + 4;                 // padded row of the transposed x tiles
+    constexpr int X16 = CH / 16;                // 16-byte pieces per time row of x
+    constexpr int XPIECES = kTC * X16;          // per chunk
+    constexpr int XPER = (XPIECES + kThreads - 1) / kThreads;
+    constexpr int BC16 = N / 16;
+    constexpr int BCPIECES = kTC * BC16;
+    constexpr int BCPER = (BCPIECES + kThreads - 1) / kThreads;
+    constexpr bool MODEL = MODE == kModeModel;
+    constexpr int NXA = MODEL ? 3 : 1;          // staged x-like arrays: x | xs, dm, z
+
+    __shared__ __align__(16) int8_t s_xa[NXA][CH][XP];
+    __shared__ __align__(16) int8_t s_b[kTC][N];
+    __shared__ __align__(16) int8_t s_c[kTC][N];
+    __shared__ __align__(16) int8_t s_o8[MODEL ? kTC : 1][MODEL ? CH : 16];
+    constexpr bool STAGE_Y = !MODEL && CH <= 64;  // int32 y staged in LDS (16 KB at most)
+    __shared__ __align__(16) int32_t s_o32[STAGE_Y ? kTC : 1][STAGE_Y ? CH : 4];
+    __shared__ int32_t s_dt[MODEL ? 41 : 1];
+    __shared__ int32_t s_gate[MODEL ? 256 : 1];
+
+    const int tid = threadIdx.x;
+    const int ch = tid / G;
+    const int g = tid % G;
+    const int p0 = blockIdx.x * CH;
+    const int hd = blockIdx.y;
+    const int b = blockIdx.z;
+    const int p = p0 + ch;
+    const bool active = p < a.P;
+    const int k = a.k;
+    const int32_t kmask = (1 << k) - 1;
+
+    if constexpr (MODEL) {
+        for (int i = tid; i < 41; i += kThreads) s_dt[i] = dt_q16(i - 20);
+        for (int i = tid; i < 256; i += kThreads) s_gate[i] = gate_q15(i - 128);
+    }
+
+    // ---- per-thread constants and state
+    int32_t ndec[S];
+    int32_t hh[S], hl[S];
+    {
+        const int64_t sidx = ((((int64_t)b * a.H + hd) * a.P + (active ? p : 0)) * N) + g * S;
+        for (int s = 0; s < S; ++s) {
+            int32_t hv = (a.h_in && active) ? a.h_in[sidx + s] : 0;
+            hh[s] = hv >> k;
+            hl[s] = hv & kmask;
+            if constexpr (MODE == kModeChannel || MODE == kModeModel)
+                ndec[s] = active ? a.decay[(int64_t)p * N + g * S + s] : 0;
+            else
+                ndec[s] = a.decay[hd];
+        }
+    }
+
+    // ---- staging registers
+    uint4 rx[NXA][XPER];
+    uint4 rb[BCPER], rc[BCPER];
+    const int64_t row0 = (int64_t)b * a.L;  // first (b, t=0) row index
+
+    auto prefetch = [&](int t0) {
+        for (int j = 0; j < XPER; ++j) {
+            const int i = tid + j * kThreads;
+            const int tt = i / X16, c16 = i % X16;
+            const bool ok = i < XPIECES && t0 + tt < a.L && p0 + c16 * 16 < a.P;
+            const int64_t rr = row0 + t0 + tt;
+            if constexpr (MODEL) {
+                const int64_t off = rr * a.x_row + p0 + c16 * 16;
+                rx[0][j] = load16(a.x + off, ok);
+                rx[1][j] = load16(a.dm + off, ok);
+                rx[2][j] = load16(a.z + rr * a.z_row + p0 + c16 * 16, ok);
+            } else {
+                rx[0][j] = load16(a.x + rr * a.x_row + (int64_t)hd * a.P + p0 + c16 * 16, ok);
+            }
+        }
+        for (int j = 0; j < BCPER; ++j) {
+            const int i = tid + j * kThreads;
+            const int tt = i / BC16, c16 = i % BC16;
+            const bool ok = i < BCPIECES && t0 + tt < a.L;
+            const int64_t off = (row0 + t0 + tt) * a.bc_row + (MODE == kModeHead ? (int64_t)hd * N : 0) + c16 * 16;
+            rb[j] = load16(a.bsrc + off, ok);
+            rc[j] = load16(a.csrc + off, ok);
+        }
+    };
+    auto stash = [&]() {
+        for (int j = 0; j < XPER; ++j) {
+            const int i = tid + j * kThreads;
+            if (i >= XPIECES) break;
+            const int tt = i / X16, c16 = i % X16;
+            for (int q = 0; q < NXA; ++q) {
+                const uint32_t w[4] = {rx[q][j].x, rx[q][j].y, rx[q][j].z, rx[q][j].w};
+                for (int e = 0; e < 16; ++e) s_xa[q][c16 * 16 + e][tt] = (int8_t)(w[e >> 2] >> (8 * (e & 3)));
+            }
+        }
+        for (int j = 0; j < BCPER; ++j) {
+            const int i = tid + j * kThreads;
+            if (i >= BCPIECES) break;
+            const int tt = i / BC16, c16 = i % BC16;
+            *reinterpret_cast<uint4 *>(&s_b[tt][c16 * 16]) = rb[j];
+            *reinterpret_cast<uint4 *>(&s_c[tt][c16 * 16]) = rc[j];
+        }
+    };
+
+    const int nchunks = (a.L + kTC - 1) / kTC;
+    prefetch(0);
+    for (int cidx = 0; cidx < nchunks; ++cidx) {
+        const int t0 = cidx * kTC;
+        const int tn = min(kTC, a.L - t0);
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (cidx + 1 < nchunks) prefetch(t0 + kTC);
+
+        for (int t4 = 0; t4 < tn; t4 += 4) {
+            const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_xa[0][ch][t4]);
+            uint32_t dmw = 0, zw = 0;
+            if constexpr (MODEL) {
+                dmw = *reinterpret_cast<const uint32_t *>(&s_xa[1][ch][t4]);
+                zw = *reinterpret_cast<const uint32_t *>(&s_xa[2][ch][t4]);
+            }
+            const int tend = min(4, tn - t4);
+            for (int tt = 0; tt < tend; ++tt) {
+                const int t = t4 + tt;
+                int xv = sbyte(xw, tt);
+                int32_t nt[S];
+                if constexpr (MODEL) {
+                    const int dmv = clamp32(sbyte(dmw, tt), -20, 20);
+                    xv = (xv * s_dt[dmv + 20] + 512) >> 10;           // rshr(xs * dt, 10)
+                    for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + dmv, 0, 32000);
+                } else {
+                    for (int s = 0; s < S; ++s) nt[s] = ndec[s];
+                }
+                uint32_t bw[(S + 3) / 4], cw[(S + 3) / 4];
+                if constexpr (S >= 4) {
+                    for (int q = 0; q < S / 4; ++q) {
+                        bw[q] = *reinterpret_cast<const uint32_t *>(&s_b[t][g * S + 4 * q]);
+                        cw[q] = *reinterpret_cast<const uint32_t *>(&s_c[t][g * S + 4 * q]);
+                    }
+                } else {
+                    uint32_t bb = 0, cc = 0;
+                    for (int s = 0; s < S; ++s) {
+                        bb |= (uint32_t)(uint8_t)s_b[t][g * S + s] << (8 * s);
+                        cc |= (uint32_t)(uint8_t)s_c[t][g * S + s] << (8 * s);
+                    }
+                    bw[0] = bb;
+                    cw[0] = cc;
+                }
+                int yhi = 0, ylo = 0;
+                for (int s = 0; s < S; ++s) {
+                    const int bv = sbyte(bw[s >> 2], s & 3);
+                    const int cv = sbyte(cw[s >> 2], s & 3);
+                    const int u = __mul24(bv, xv);
+                    const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt[s]) >> k);
+                    const int d = __mul24(hh[s], nt[s]) + c;
+                    const int hn = __builtin_elementwise_add_sat(d, u);
+                    hh[s] = hn >> k;
+                    hl[s] = hn & kmask;
+                    yhi += __mul24(cv, hh[s]);
+                    ylo += __mul24(cv, hl[s]);
+                }
+                yhi = group_sum<G>(yhi);
+                ylo = group_sum<G>(ylo);
+                const int64_t y64 = ((int64_t)yhi << k) + ylo;
+                const int32_t y32 = sat32_64(y64);
+                if (g == 0) {
+                    if constexpr (MODEL) {
+                        const int zv = sbyte(zw, tt);
+                        const int64_t yg = ((int64_t)y32 * s_gate[zv + 128]) >> 15;
+                        s_o8[t][ch] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
+                    } else if constexpr (STAGE_Y) {
+                        s_o32[t][ch] = y32;
+                    } else if (active) {
+                        a.y[(row0 + t0 + t) * a.x_row + (int64_t)hd * a.P + p] = y32;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // ---- write the staged outputs of this chunk
+        if constexpr (MODEL) {
+            for (int i = tid; i < kTC * X16; i += kThreads) {
+                const int tt = i / X16, c16 = i % X16;
+                if (tt < tn && p0 + c16 * 16 < a.P)
+                    *reinterpret_cast<uint4 *>(a.yo + (row0 + t0 + tt) * a.x_row + p0 + c16 * 16) =
+                        *reinterpret_cast<const uint4 *>(&s_o8[tt][c16 * 16]);
+            }
+        } else if constexpr (STAGE_Y) {
+            constexpr int Y4 = CH / 4;
+            for (int i = tid; i < kTC * Y4; i += kThreads) {
+                const int tt = i / Y4, c4 = i % Y4;
+                if (tt < tn && p0 + c4 * 4 < a.P)
+                    *reinterpret_cast<uint4 *>(a.y + (row0 + t0 + tt) * a.x_row + (int64_t)hd * a.P + p0 + c4 * 4) =
+                        *reinterpret_cast<const uint4 *>(&s_o32[tt][c4 * 4]);
+            }
+        }
+        if constexpr (MODE == kModeHead) {
+            // chunk_states at every multiple of cs (cs is a multiple of kTC) and at the end
+            const int tdone = t0 + tn;
+            if (a.chunk_states && active && (tdone % a.cs == 0 || tdone == a.L)) {
+                const int cc = (tdone - 1) / a.cs;
+                int32_t *dst = a.chunk_states +
+                               ((((int64_t)b * a.nchunks_out + cc) * a.H + hd) * a.P + p) * N + g * S;
+                for (int s = 0; s < S; ++s) dst[s] = (hh[s] << k) + hl[s];
+            }
+        }
+    }
+    if (a.h_out && active) {
+        const int64_t sidx = ((((int64_t)b * a.H + hd) * a.P + p) * N) + g * S;
+        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = (hh[s] << k) + hl[s];
+    }
+}
+
+// ---------------------------------------------------------------- generic
+// Plain int64 kernels for every shape the fast kernel does not take, and for
+// chunk lengths that are not multiples of the staging chunk.  One thread per
+// (b, head, channel), all states in a loop, inputs read straight from global.
+template <int MODE>
+__global__ __launch_bounds__(256) void scan_generic_kernel(ScanArgs a, int N) {
+    const int64_t lane = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t lanes = (int64_t)a.B * a.H * a.P;
+    if (lane >= lanes) return;
+    const int p = (int)(lane % a.P);
+    const int hd = (int)((lane / a.P) % a.H);
+    const int b = (int)(lane / ((int64_t)a.P * a.H));
+    int32_t h[128];
+    const int64_t sidx = (((int64_t)b * a.H + hd) * a.P + p) * N;
+    for (int n = 0; n < N; ++n) h[n] = a.h_in ? a.h_in[sidx + n] : 0;
+    for (int t = 0; t < a.L; ++t) {
+        const int64_t rr = (int64_t)b * a.L + t;
+        int64_t xv;
+        int dmv = 0;
+        const int8_t *brow, *crow;
+        if constexpr (MODE == kModeModel) {
+            dmv = clamp32(a.dm[rr * a.x_row + p], -20, 20);
+            xv = rshr64((int64_t)a.x[rr * a.x_row + p] * dt_q16(dmv), 10);
+            brow = a.bsrc + rr * a.bc_row;
+            crow = a.csrc + rr * a.bc_row;
+        } else {
+            xv = a.x[rr * a.x_row + (int64_t)hd * a.P + p];
+            brow = a.bsrc + rr * a.bc_row + (MODE == kModeHead ? (int64_t)hd * N : 0);
+            crow = a.csrc + rr * a.bc_row + (MODE == kModeHead ? (int64_t)hd * N : 0);
+        }
+        int64_t acc = 0;
+        for (int n = 0; n < N; ++n) {
+            int64_t nd;
+            if constexpr (MODE == kModeChannel) nd = a.decay[(int64_t)p * N + n];
+            else if constexpr (MODE == kModeHead) nd = a.decay[hd];
+            else nd = clamp64((int64_t)a.decay[(int64_t)p * N + n] + dmv, 0, 32000);
+            const int64_t dec = ((int64_t)h[n] * nd) >> a.k;
+            h[n] = sat32_64(dec + (int64_t)brow[n] * xv);
+            acc += (int64_t)crow[n] * h[n];
+        }
+        const int32_t y32 = sat32_64(acc);
+        if constexpr (MODE == kModeModel) {
+            const int zv = a.z[rr * a.z_row + p];
+            const int64_t yg = ((int64_t)y32 * gate_q15(zv)) >> 15;
+            a.yo[rr * a.x_row + p] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
+        } else {
+            a.y[rr * a.x_row + (int64_t)hd * a.P + p] = y32;
+        }
+        if constexpr (MODE == kModeHead) {
+            if (a.chunk_states && ((t + 1) % a.cs == 0 || t + 1 == a.L)) {
+                const int cc = t / a.cs;
+                int32_t *dst = a.chunk_states + ((((int64_t)b * a.nchunks_out + cc) * a.H + hd) * a.P + p) * N;
+                for (int n = 0; n < N; ++n) dst[n] = h[n];
+            }
+        }
+    }
+    if (a.h_out)
+        for (int n = 0; n < N; ++n) a.h_out[sidx + n] = h[n];
+}
+
+// ------------------------------------------------------------- dispatch
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
+// Lanes per channel: enough waves to cover the 1024 SIMDs when possible,
+// overridable with MI_SCAN_G for tuning.
+int pick_g(int N, int64_t channels) {
+    int forced = env_int("MI_SCAN_G", 0);
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)
+        if (N % forced == 0 && N / forced <= 32) return forced;
+    int g = 1;
+    while (g < 16 && N % (2 * g) == 0 && (N / g > 32 || channels * g / 64 < 1024)) g *= 2;
+    return g;
+}
+
+template <int N, int MODE>
+hipError_t launch_fast_n(int G, const ScanArgs &a, hipStream_t st) {
+    auto grid = [&](int ch) { return dim3((unsigned)((a.P + ch - 1) / ch), (unsigned)a.H, (unsigned)a.B); };
+    switch (G) {
+#define MI_CASE_G(GG)                                                                   \
+    case GG:                                                                            \
+        if constexpr (N / GG >= 1 && N / GG <= 32) {                                    \
+            hipLaunchKernelGGL((scan_kernel<N, GG, MODE>), grid(kThreads / GG), dim3(kThreads), 0, st, a); \
+            return hipGetLastError();                                                   \
+        }                                                                               \
+        break;
+        MI_CASE_G(1)
+        MI_CASE_G(2)
+        MI_CASE_G(4)
+        MI_CASE_G(8)
+        MI_CASE_G(16)
+#undef MI_CASE_G
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int MODE>
+hipError_t launch_scan(const ScanArgs &a, int N, bool fast, hipStream_t st) {
+    if (fast) {
+        const int G = pick_g(N, (int64_t)a.B * a.H * a.P);
+        switch (N) {
+            case 16: return launch_fast_n<16, MODE>(G, a, st);
+            case 32: return launch_fast_n<32, MODE>(G, a, st);
+            case 64: return launch_fast_n<64, MODE>(G, a, st);
+            case 128:
+                if constexpr (MODE != kModeModel) return launch_fast_n<128, MODE>(G, a, st);
+                break;
+        }
+    }
+    const int64_t lanes = (int64_t)a.B * a.H * a.P;
+    hipLaunchKernelGGL((scan_generic_kernel<MODE>), dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, st, a, N);
+    return hipGetLastError();
+}
+
+bool fast_shape(int N, int P, int k, int mode) {
+    if (N != 16 && N != 32 && N != 64 && !(N == 128 && mode != kModeModel)) return false;
+    if (P % 16 != 0) return false;
+    // k = 15 only: hl*n < 2^15 * (2^15 + 1) < 2^31, so the product's sign bit is
+    // clear (the compiler lowers the unsigned shift of the 24-bit product to an
+    // arithmetic shift, which is exact only then), and sum C*hh stays in int32.
+    if (k != 15) return false;
+    if (getenv("MI_SCAN_GENERIC")) return false;
+    return true;
+}
+
+// ------------------------------------------------ float-compat reference
+// Exact semantics of the reference launch_dyadic_scan
+// (dyadic_mamba_kernel.cu:35-63): one lane per (b, d), int64 state.
+__global__ __launch_bounds__(256) void scan_f32_kernel(const float *x, const int32_t *nums, const int32_t *shifts,
+                                                       float *h, int B, int S, int D, int sb) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)B * D) return;
+    const int d = (int)(idx % D);
+    const int b = (int)(idx / D);
+    const float scale_f = (float)((long long)1 << sb);
+    long long hc = 0;
+    for (int t = 0; t < S; ++t) {
+        const int64_t off = ((int64_t)b * S + t) * D + d;
+        const float xs = x[off] * scale_f;
+        const long long xf = (long long)xs;
+        hc = hc * (long long)nums[off];
+        hc = hc >> shifts[off];
+        hc += xf;
+        h[off] = (float)hc / scale_f;
+    }
+}
+
+// Elementwise integer recurrence: one lane per (b, channel), int32 state.
+__global__ __launch_bounds__(256) void scan_elem_kernel(const int32_t *u, const int32_t *n, int k, int32_t *h,
+                                                        const int32_t *h_in, int32_t *h_out, int B, int L, int C) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)B * C) return;
+    const int c = (int)(idx % C);
+    const int b = (int)(idx / C);
+    int32_t s = h_in ? h_in[idx] : 0;
+    for (int t = 0; t < L; ++t) {
+        const int64_t off = ((int64_t)b * L + t) * C + c;
+        s = sat32_64((((int64_t)s * n[off]) >> k) + (int64_t)u[off]);
+        h[off] = s;
+    }
+    if (h_out) h_out[idx] = s;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status mi_dyadic_scan(const int8_t *x, const int8_t *b, const int8_t *c, const int32_t *decay_num,
+                                    int decay_shift, int32_t *y, const int32_t *h_in, int32_t *h_out, int batch,
+                                    int len, int d, int nstate, void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && d >= 0, MI_ERR_BAD_DIM, "mi_dyadic_scan: negative size");
+    MI_REQUIRE(nstate >= 1 && nstate <= 128, MI_ERR_BAD_DIM, "mi_dyadic_scan: nstate=%d outside [1,128]", nstate);
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 16, MI_ERR_BAD_ARG, "mi_dyadic_scan: decay_shift=%d outside [1,16]",
+               decay_shift);
+    if ((int64_t)batch * d == 0) return MI_OK;
+    MI_REQUIRE(decay_num && y, MI_ERR_NULL_POINTER, "mi_dyadic_scan: decay_num and y are required");
+    if (len > 0) MI_REQUIRE(x && b && c, MI_ERR_NULL_POINTER, "mi_dyadic_scan: x, b and c are required");
+    ScanArgs a{};
+    a.x = x; a.bsrc = b; a.csrc = c; a.decay = decay_num; a.y = y; a.h_in = h_in; a.h_out = h_out;
+    a.x_row = d; a.bc_row = nstate; a.B = batch; a.L = len; a.H = 1; a.P = d; a.k = decay_shift;
+    const bool fast = len > 0 && fast_shape(nstate, d, decay_shift, kModeChannel) && aligned(x, 16) && aligned(b, 16) &&
+                      aligned(c, 16) && aligned(y, 16);
+    if (len == 0 && !h_out) return MI_OK;
+    hipError_t e = launch_scan<kModeChannel>(a, nstate, fast, as_stream(stream));
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_dyadic_scan: launch failed: %s", hipGetErrorString(e));
+    return MI_OK;
+}
+
+extern "C" mi_status mi_ssd_chunked_scan(const int8_t *x, const int8_t *b, const int8_t *c, const int32_t *decay_num,
+                                         int decay_shift, int32_t *y, int32_t *chunk_states, const int32_t *h_in,
+                                         int32_t *h_out, int batch, int len, int heads, int head_dim, int nstate,
+                                         int chunk, void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && heads >= 0 && head_dim >= 0, MI_ERR_BAD_DIM,
+               "mi_ssd_chunked_scan: negative size");
+    MI_REQUIRE(nstate >= 1 && nstate <= 128, MI_ERR_BAD_DIM, "mi_ssd_chunked_scan: nstate=%d outside [1,128]", nstate);
+    MI_REQUIRE(chunk >= 1, MI_ERR_BAD_ARG, "mi_ssd_chunked_scan: chunk=%d must be >= 1", chunk);
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 16, MI_ERR_BAD_ARG,
+               "mi_ssd_chunked_scan: decay_shift=%d outside [1,16]", decay_shift);
+    if ((int64_t)batch * heads * head_dim == 0 || (len == 0 && !h_out)) return MI_OK;
+    MI_REQUIRE(decay_num && (len == 0 || (x && b && c && y)), MI_ERR_NULL_POINTER,
+               "mi_ssd_chunked_scan: x, b, c, decay_num, y required");
+    ScanArgs a{};
+    a.x = x; a.bsrc = b; a.csrc = c; a.decay = decay_num; a.y = y; a.chunk_states = chunk_states;
+    a.h_in = h_in; a.h_out = h_out;
+    a.x_row = (int64_t)heads * head_dim; a.bc_row = (int64_t)heads * nstate;
+    a.B = batch; a.L = len; a.H = heads; a.P = head_dim; a.k = decay_shift;
+    a.cs = chunk; a.nchunks_out = (len + chunk - 1) / chunk;
+    const bool fast = len > 0 && fast_shape(nstate, head_dim, decay_shift, kModeHead) && (chunk % kTC == 0) && aligned(x, 16) &&
+                      aligned(b, 16) && aligned(c, 16) && aligned(y, 16);
+    hipError_t e = launch_scan<kModeHead>(a, nstate, fast, as_stream(stream));
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_ssd_chunked_scan: launch failed: %s", hipGetErrorString(e));
+    return MI_OK;
+}
+
+extern "C" mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int8_t *xp, int xp_stride, int b_off,
+                                   const int8_t *z, int z_stride, int z_off, const int32_t *base, int decay_shift,
+                                   int s_y, int8_t *yo, const int32_t *h_in, int32_t *h_out, int batch, int len,
+                                   int d_inner, int nstate, void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_block_scan: negative size");
+    MI_REQUIRE(nstate >= 1 && nstate <= 64, MI_ERR_BAD_DIM, "mi_block_scan: nstate=%d outside [1,64]", nstate);
+    MI_REQUIRE(decay_shift == 15, MI_ERR_BAD_ARG, "mi_block_scan: decay_shift=%d, the model path uses 15", decay_shift);
+    MI_REQUIRE(s_y >= 0 && s_y <= 40, MI_ERR_BAD_ARG, "mi_block_scan: s_y=%d outside [0,40]", s_y);
+    MI_REQUIRE(b_off >= 0 && b_off + 2 * nstate <= xp_stride, MI_ERR_BAD_DIM,
+               "mi_block_scan: B/C columns [%d,%d) exceed xp_stride=%d", b_off, b_off + 2 * nstate, xp_stride);
+    MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride, MI_ERR_BAD_DIM,
+               "mi_block_scan: z columns exceed z_stride=%d", z_stride);
+    if ((int64_t)batch * d_inner == 0 || (len == 0 && !h_out)) return MI_OK;
+    MI_REQUIRE(base && (len == 0 || (xs && dm && xp && z && yo)), MI_ERR_NULL_POINTER,
+               "mi_block_scan: a required pointer is NULL");
+    ScanArgs a{};
+    a.x = xs; a.dm = dm; a.z = z + z_off; a.bsrc = xp + b_off; a.csrc = xp + b_off + nstate; a.decay = base;
+    a.yo = yo; a.h_in = h_in; a.h_out = h_out;
+    a.x_row = d_inner; a.bc_row = xp_stride; a.z_row = z_stride;
+    a.B = batch; a.L = len; a.H = 1; a.P = d_inner; a.k = decay_shift; a.s_y = s_y;
+    const bool fast = len > 0 && fast_shape(nstate, d_inner, decay_shift, kModeModel) && aligned(xs, 16) && aligned(dm, 16) &&
+                      aligned(a.z, 16) && aligned(a.bsrc, 16) && aligned(a.csrc, 16) && aligned(yo, 16) &&
+                      xp_stride % 16 == 0 && z_stride % 16 == 0;
+    hipError_t e = launch_scan<kModeModel>(a, nstate, fast, as_stream(stream));
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_block_scan: launch failed: %s", hipGetErrorString(e));
+    return MI_OK;
+}
+
+extern "C" mi_status mi_dyadic_scan_f32(const float *x, const int32_t *nums, const int32_t *shifts, float *h,
+                                        int batch, int seq, int dim, int scale_bits, void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && seq >= 0 && dim >= 0, MI_ERR_BAD_DIM, "mi_dyadic_scan_f32: negative size");
+    MI_REQUIRE(scale_bits >= 0 && scale_bits <= 62, MI_ERR_BAD_ARG, "mi_dyadic_scan_f32: scale_bits=%d outside [0,62]",
+               scale_bits);
+    if ((int64_t)batch * seq * dim == 0) return MI_OK;
+    MI_REQUIRE(x && nums && shifts && h, MI_ERR_NULL_POINTER, "mi_dyadic_scan_f32: a required pointer is NULL");
+    const int64_t lanes = (int64_t)batch * dim;
+    hipLaunchKernelGGL(scan_f32_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, as_stream(stream), x,
+                       nums, shifts, h, batch, seq, dim, scale_bits);
+    return check_launch("mi_dyadic_scan_f32");
+}
+
+extern "C" mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t *nums, int decay_shift, int32_t *h,
+                                                const int32_t *h_in, int32_t *h_out, int batch, int len, int channels,
+                                                void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && channels >= 0, MI_ERR_BAD_DIM, "mi_dyadic_scan_elementwise: negative size");
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG,
+               "mi_dyadic_scan_elementwise: decay_shift=%d outside [1,30]", decay_shift);
+    if ((int64_t)batch * channels == 0 || len == 0) return MI_OK;
+    MI_REQUIRE(u && nums && h, MI_ERR_NULL_POINTER, "mi_dyadic_scan_elementwise: u, nums and h are required");
+    const int64_t lanes = (int64_t)batch * channels;
+    hipLaunchKernelGGL(scan_elem_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, as_stream(stream), u,
+                       nums, decay_shift, h, h_in, h_out, batch, len, channels);
+    return check_launch("mi_dyadic_scan_elementwise");
+}

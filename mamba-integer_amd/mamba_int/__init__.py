@@ -1,0 +1,8 @@
+"""mamba_int: MI355X-native integer Mamba inference path (spec mi-spec-1).
+
+Host side in Python on PyTorch-ROCm; compute in libmamba_int.so (gfx950 HIP
+kernels behind the C ABI of include/mamba_int.h).
+"""
+from .params import ModelDims, ModelParams, LayerParams, init_random_params, pack_ternary, unpack_ternary  # noqa: F401
+
+SPEC_VERSION = "mi-spec-1"

@@ -1,0 +1,246 @@
+"""Device runner of the integer Mamba stack (spec rules 4.1-4.12).
+
+Orchestrates the per-layer kernels in the block order of
+``MambaIntegerBlock.forward`` (``mamba_integer_model.py:396-447``) and the
+model order of ``MambaIntegerModel.forward`` (``:486-495``).  Adds what the
+reference lacks: a recurrent decode step with per-layer conv and scan state
+(the reference recomputes the whole prefix per token,
+``scripts/inference.py:147-161``), and a HIP-graph-captured greedy decode loop.
+
+Activations live in preallocated int8/int32 workspaces sized for one
+(batch, length); the int32 residual is updated in place by the out_proj
+epilogue.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from . import ops
+from .params import LayerParams, ModelParams
+
+
+@dataclass
+class DeviceLayer:
+    gamma: torch.Tensor
+    w_in: torch.Tensor
+    s_in: int
+    conv_w: torch.Tensor
+    conv_b: torch.Tensor
+    w_x: torch.Tensor
+    s_x: int
+    w_dt: torch.Tensor
+    s_dt: int
+    base: torch.Tensor
+    k: int
+    s_y: int
+    w_out: torch.Tensor
+    res_mult: int
+    res_shift: int
+
+
+@dataclass
+class DecodeState:
+    """Recurrent state of every layer: conv ring [B,3,D] int8, scan state [B,D,N] int32."""
+    conv: List[torch.Tensor]
+    h: List[torch.Tensor]
+
+    def clone(self) -> "DecodeState":
+        return DecodeState([c.clone() for c in self.conv], [h.clone() for h in self.h])
+
+
+def _dev(a, device) -> torch.Tensor:
+    return torch.from_numpy(a.copy()).to(device)
+
+
+class _Workspace:
+    def __init__(self, dims, T: int, device):
+        D, d = dims.d_inner, dims.d_model
+        self.T = T
+        self.r = torch.empty((T, d), dtype=torch.int32, device=device)
+        self.a = torch.empty((T, d), dtype=torch.int8, device=device)
+        self.xz = torch.empty((T, 2 * D), dtype=torch.int8, device=device)
+        self.xs = torch.empty((T, D), dtype=torch.int8, device=device)
+        self.xp = torch.empty((T, dims.xp_width), dtype=torch.int8, device=device)
+        self.dm = torch.empty((T, D), dtype=torch.int8, device=device)
+        self.yo = torch.empty((T, D), dtype=torch.int8, device=device)
+
+
+class IntegerMambaRunner:
+    def __init__(self, params: ModelParams, device: str = "cuda"):
+        self.dims = params.dims
+        self.dims.validate()
+        if self.dims.xp_width % 16 or self.dims.dt_rank % 16:
+            raise ValueError("dt_rank and dt_rank + 2*d_state must be multiples of 16")
+        self.device = torch.device(device)
+        dv = self.device
+        self.emb = _dev(params.emb, dv)
+        self.layers: List[DeviceLayer] = []
+        for lp in params.layers:
+            self.layers.append(DeviceLayer(
+                gamma=_dev(lp.gamma, dv), w_in=_dev(lp.w_in, dv), s_in=lp.s_in,
+                conv_w=_dev(lp.conv_w, dv), conv_b=_dev(lp.conv_b, dv),
+                w_x=_dev(lp.w_x, dv), s_x=lp.s_x, w_dt=_dev(lp.w_dt, dv), s_dt=lp.s_dt,
+                base=_dev(lp.base, dv), k=lp.k, s_y=lp.s_y, w_out=_dev(lp.w_out, dv),
+                res_mult=lp.res_mult, res_shift=lp.res_shift))
+        self.gamma_f = _dev(params.gamma_f, dv)
+        self.w_head = _dev(params.w_head, dv)
+        self._ws: Dict[int, _Workspace] = {}
+        self._graphs: Dict[int, tuple] = {}
+        # optional (before, after) callables around every fused scan launch
+        # (the bench times that kernel with events on the launch stream)
+        self.scan_timer = None
+
+    # ------------------------------------------------------------ plumbing
+    def _workspace(self, T: int) -> _Workspace:
+        ws = self._ws.get(T)
+        if ws is None:
+            ws = _Workspace(self.dims, T, self.device)
+            self._ws[T] = ws
+        return ws
+
+    def new_state(self, batch: int) -> DecodeState:
+        D, N = self.dims.d_inner, self.dims.d_state
+        return DecodeState(
+            conv=[torch.zeros((batch, 3, D), dtype=torch.int8, device=self.device) for _ in self.layers],
+            h=[torch.zeros((batch, D, N), dtype=torch.int32, device=self.device) for _ in self.layers])
+
+    # ---------------------------------------------------------------- layers
+    def _layer(self, ly: DeviceLayer, ws: _Workspace, B: int, L: int, conv_state: torch.Tensor,
+               h_state: torch.Tensor, fresh: bool) -> None:
+        dims = self.dims
+        D, N, R, d = dims.d_inner, dims.d_state, dims.dt_rank, dims.d_model
+        T = B * L
+        ops.bitshift_norm(ws.r, ly.gamma, out=ws.a)
+        ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
+        ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
+                            state_out=conv_state, out=ws.xs, batch=B)
+        ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+        ops.bitlinear(ws.xp, ly.w_dt, ops.OUT_DECAY_MOD, D, k=R, shift=ly.s_dt, out=ws.dm,
+                      lda=dims.xp_width, m=T)
+        if self.scan_timer is not None:
+            self.scan_timer[0]()
+        ops.block_scan(ws.xs, ws.dm, ws.xp, R, ws.xz, D, ly.base, ly.k, ly.s_y,
+                       h_in=None if fresh else h_state, h_out=h_state, out=ws.yo, batch=B)
+        if self.scan_timer is not None:
+            self.scan_timer[1]()
+        ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                      res_shift=ly.res_shift)
+
+    def _head(self, r_rows: torch.Tensor) -> torch.Tensor:
+        a = ops.bitshift_norm(r_rows, self.gamma_f)
+        return ops.bitlinear(a, self.w_head, ops.OUT_INT32, self.dims.vocab_size)
+
+    def _run(self, ids: torch.Tensor, state: DecodeState, fresh: bool) -> _Workspace:
+        B, L = ids.shape
+        ws = self._workspace(B * L)
+        ops.embed(ids.reshape(-1).contiguous(), self.emb, out=ws.r)
+        for i, ly in enumerate(self.layers):
+            self._layer(ly, ws, B, L, state.conv[i], state.h[i], fresh)
+        return ws
+
+    # ------------------------------------------------------------ public API
+    @torch.no_grad()
+    def forward_logits(self, ids: torch.Tensor) -> torch.Tensor:
+        """All-position int32 logits [B, L, V] (MambaIntegerModel.forward)."""
+        B, L = ids.shape
+        state = self.new_state(B)
+        ws = self._run(ids, state, fresh=True)
+        return self._head(ws.r).view(B, L, -1)
+
+    @torch.no_grad()
+    def prefill(self, ids: torch.Tensor, state: Optional[DecodeState] = None
+                ) -> Tuple[torch.Tensor, DecodeState]:
+        """Last-position int32 logits [B, V] and the recurrent state after the prompt."""
+        B, L = ids.shape
+        fresh = state is None
+        if state is None:
+            state = self.new_state(B)
+        ws = self._run(ids, state, fresh=fresh)
+        last = ws.r.view(B, L, -1)[:, -1, :].contiguous()
+        return self._head(last), state
+
+    @torch.no_grad()
+    def decode_step(self, tokens: torch.Tensor, state: DecodeState) -> torch.Tensor:
+        """One recurrent step for tokens [B] int64; updates `state` in place."""
+        ws = self._run(tokens.view(-1, 1), state, fresh=False)
+        return self._head(ws.r)
+
+    @torch.no_grad()
+    def generate(self, ids: torch.Tensor, n_new: int, use_graph: bool = True) -> torch.Tensor:
+        """Greedy decode (first maximal index): returns [B, n_new] int64 token ids."""
+        logits, state = self.prefill(ids)
+        return self.decode_loop(logits, state, n_new, use_graph=use_graph)
+
+    @torch.no_grad()
+    def decode_loop(self, logits: torch.Tensor, state: DecodeState, n_new: int,
+                    use_graph: bool = True) -> torch.Tensor:
+        """Greedy continuation from last-position logits [B, V] and `state`."""
+        B = logits.shape[0]
+        out = torch.empty((B, n_new), dtype=torch.int64, device=self.device)
+        if n_new == 0:
+            return out
+        tok = ops.argmax(logits)
+        out[:, 0] = tok
+        if not use_graph:
+            for i in range(1, n_new):
+                logits = self.decode_step(tok, state)
+                tok = ops.argmax(logits)
+                out[:, i] = tok
+            return out
+        step = self._decode_graph(B, state)
+        step.tok_in.copy_(tok)
+        for i in range(1, n_new):
+            step.graph.replay()
+            out[:, i] = step.tok_out
+            step.tok_in.copy_(step.tok_out)
+        # hand the state back to the caller's tensors
+        for i in range(len(self.layers)):
+            state.conv[i].copy_(step.state.conv[i])
+            state.h[i].copy_(step.state.h[i])
+        return out
+
+    def _decode_graph(self, B: int, state: DecodeState):
+        """Captures embed -> layers -> head -> argmax for batch B as one HIP graph."""
+        g = self._graphs.get(B)
+        if g is None:
+            tok_in = torch.zeros((B,), dtype=torch.int64, device=self.device)
+            gstate = self.new_state(B)
+            # warm the workspaces outside capture (allocation happens here)
+            ws = self._workspace(B)
+            head_a = torch.empty((B, self.dims.d_model), dtype=torch.int8, device=self.device)
+            logits = torch.empty((B, self.dims.vocab_size), dtype=torch.int32, device=self.device)
+            tok_out = torch.empty((B,), dtype=torch.int64, device=self.device)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                # one eager step first: every kernel is loaded before capture
+                ops.embed(tok_in, self.emb, out=ws.r)
+                for i, ly in enumerate(self.layers):
+                    self._layer(ly, ws, B, 1, gstate.conv[i], gstate.h[i], fresh=False)
+                ops.bitshift_norm(ws.r, self.gamma_f, out=head_a)
+                ops.bitlinear(head_a, self.w_head, ops.OUT_INT32, self.dims.vocab_size, out=logits)
+                ops.argmax(logits, out=tok_out)
+            side.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    ops.embed(tok_in, self.emb, out=ws.r)
+                    for i, ly in enumerate(self.layers):
+                        self._layer(ly, ws, B, 1, gstate.conv[i], gstate.h[i], fresh=False)
+                    ops.bitshift_norm(ws.r, self.gamma_f, out=head_a)
+                    ops.bitlinear(head_a, self.w_head, ops.OUT_INT32, self.dims.vocab_size, out=logits)
+                    ops.argmax(logits, out=tok_out)
+            torch.cuda.current_stream().wait_stream(side)
+
+            class _G:
+                pass
+            g = _G()
+            g.graph, g.tok_in, g.tok_out, g.state = graph, tok_in, tok_out, gstate
+            self._graphs[B] = g
+        for i in range(len(self.layers)):
+            g.state.conv[i].copy_(state.conv[i])
+            g.state.h[i].copy_(state.h[i])
+        return g

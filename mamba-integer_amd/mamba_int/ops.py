@@ -1,0 +1,197 @@
+"""Torch-facing wrappers of the C ABI (device tensors in, device tensors out).
+
+PyTorch provides device memory and the current HIP stream; every op runs in
+libmamba_int.so.  Inputs must be contiguous device tensors of the stated
+dtype; outputs are allocated here (or passed in with ``out=``) so callers that
+capture HIP graphs can keep static buffers.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import OUT_DECAY_MOD, OUT_FLOAT, OUT_INT8, OUT_INT32, OUT_RESIDUAL  # noqa: F401
+
+_vp = ctypes.c_void_p
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else _vp(t.data_ptr())
+
+
+def _stream():
+    return _vp(torch.cuda.current_stream().cuda_stream)
+
+
+def _req(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (libmamba_int has no host path)")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def _opt(t, dtype, name):
+    return None if t is None else _req(t, dtype, name)
+
+
+# ------------------------------------------------------------------ scans
+def dyadic_scan(x, b, c, decay_num, decay_shift: int = 15, h_in=None, h_out=None, out=None):
+    """Config-1 scan: x int8 [B,L,D], b/c int8 [B,L,N], decay_num int32 [D,N] -> y int32 [B,L,D]."""
+    _req(x, torch.int8, "x"); _req(b, torch.int8, "b"); _req(c, torch.int8, "c")
+    _req(decay_num, torch.int32, "decay_num")
+    B, L, D = x.shape
+    N = b.shape[-1]
+    y = out if out is not None else torch.empty((B, L, D), dtype=torch.int32, device=x.device)
+    _req(y, torch.int32, "y")
+    _lib.call("mi_dyadic_scan", _ptr(x), _ptr(b), _ptr(c), _ptr(decay_num), decay_shift, _ptr(y),
+              _ptr(_opt(h_in, torch.int32, "h_in")), _ptr(_opt(h_out, torch.int32, "h_out")),
+              B, L, D, N, _stream())
+    return y
+
+
+def dyadic_scan_f32(x, nums, shifts, scale_bits: int = 20):
+    """Reference launch_dyadic_scan semantics: x fp32 [B,S,D], nums/shifts int32 -> h fp32."""
+    _req(x, torch.float32, "x"); _req(nums, torch.int32, "nums"); _req(shifts, torch.int32, "shifts")
+    B, S, D = x.shape
+    h = torch.empty_like(x)
+    _lib.call("mi_dyadic_scan_f32", _ptr(x), _ptr(nums), _ptr(shifts), _ptr(h), B, S, D, scale_bits, _stream())
+    return h
+
+
+def dyadic_scan_elementwise(u, nums, decay_shift: int, h_in=None, h_out=None):
+    _req(u, torch.int32, "u"); _req(nums, torch.int32, "nums")
+    B, L, C = u.shape
+    h = torch.empty_like(u)
+    _lib.call("mi_dyadic_scan_elementwise", _ptr(u), _ptr(nums), decay_shift, _ptr(h),
+              _ptr(_opt(h_in, torch.int32, "h_in")), _ptr(_opt(h_out, torch.int32, "h_out")),
+              B, L, C, _stream())
+    return h
+
+
+def ssd_chunked_scan(x, b, c, decay_num, decay_shift: int, chunk: int, chunk_states=None,
+                     h_in=None, h_out=None):
+    """Config-4 scan: x int8 [B,L,H,P], b/c int8 [B,L,H,N], decay_num int32 [H] -> y int32 [B,L,H,P]."""
+    _req(x, torch.int8, "x"); _req(b, torch.int8, "b"); _req(c, torch.int8, "c")
+    _req(decay_num, torch.int32, "decay_num")
+    B, L, H, P = x.shape
+    N = b.shape[-1]
+    y = torch.empty((B, L, H, P), dtype=torch.int32, device=x.device)
+    _lib.call("mi_ssd_chunked_scan", _ptr(x), _ptr(b), _ptr(c), _ptr(decay_num), decay_shift, _ptr(y),
+              _ptr(_opt(chunk_states, torch.int32, "chunk_states")),
+              _ptr(_opt(h_in, torch.int32, "h_in")), _ptr(_opt(h_out, torch.int32, "h_out")),
+              B, L, H, P, N, chunk, _stream())
+    return y
+
+
+# ---------------------------------------------------------------- BitLinear
+def pack_ternary(w: torch.Tensor) -> torch.Tensor:
+    _req(w, torch.int8, "w")
+    n, k = w.shape
+    p = torch.empty((n, k // 4), dtype=torch.uint8, device=w.device)
+    _lib.call("mi_pack_ternary", _ptr(w), _ptr(p), n, k, _stream())
+    return p
+
+
+def act_quant(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    _req(x, torch.float32, "x")
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    _lib.call("mi_act_quant_f32", _ptr(x), _ptr(q), _ptr(s), m, k, _stream())
+    return q, s
+
+
+_OUT_DTYPE = {OUT_INT32: torch.int32, OUT_INT8: torch.int8, OUT_DECAY_MOD: torch.int8,
+              OUT_RESIDUAL: torch.int32, OUT_FLOAT: torch.float32}
+_ENTRY = {"auto": "mi_bitlinear", "gemm": "mi_bitlinear_gemm", "gemv": "mi_bitlinear_gemv"}
+
+
+def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Optional[int] = None,
+              shift: int = 0, out: Optional[torch.Tensor] = None, res_mult: int = 0, res_shift: int = 0,
+              x_scale: Optional[torch.Tensor] = None, w_scale: float = 0.0, path: str = "auto",
+              lda: Optional[int] = None, m: Optional[int] = None) -> torch.Tensor:
+    """out = kind(a[:, :k] @ W^T).  a int8 [m, lda] (a row-strided view is passed by
+    its storage with ``lda``); RESIDUAL updates ``out`` (int32 [m, n]) in place."""
+    if a.dtype != torch.int8 or not a.is_cuda:
+        raise TypeError("a must be an int8 device tensor")
+    if lda is None:
+        _req(a, torch.int8, "a")
+        lda = a.shape[-1]
+    if m is None:
+        m = a.shape[0]
+    if k is None:
+        k = lda
+    _req(w_packed, torch.uint8, "w_packed")
+    if out is None:
+        if kind == OUT_RESIDUAL:
+            raise ValueError("RESIDUAL output updates `out` in place; pass it")
+        out = torch.empty((m, n), dtype=_OUT_DTYPE[kind], device=a.device)
+    _req(out, _OUT_DTYPE[kind], "out")
+    _lib.call(_ENTRY[path], _ptr(a), lda, _ptr(w_packed), _ptr(out), out.shape[-1], kind, m, n, k,
+              shift, int(res_mult), res_shift, _ptr(_opt(x_scale, torch.float32, "x_scale")),
+              ctypes.c_float(w_scale), _stream())
+    return out
+
+
+# ---------------------------------------------------------------- block ops
+def bitshift_norm(r: torch.Tensor, gamma: torch.Tensor, out=None) -> torch.Tensor:
+    _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma")
+    T, d = r.shape
+    o = out if out is not None else torch.empty((T, d), dtype=torch.int8, device=r.device)
+    _lib.call("mi_bitshift_norm", _ptr(r), _ptr(gamma), _ptr(o), T, d, _stream())
+    return o
+
+
+def embed(ids: torch.Tensor, emb: torch.Tensor, out=None) -> torch.Tensor:
+    _req(ids, torch.int64, "ids"); _req(emb, torch.int8, "emb")
+    V, d = emb.shape
+    T = ids.numel()
+    r = out if out is not None else torch.empty((T, d), dtype=torch.int32, device=ids.device)
+    _lib.call("mi_embed", _ptr(ids), _ptr(emb), _ptr(r), T, d, V, _stream())
+    return r
+
+
+def conv_squareplus(xz: torch.Tensor, d_inner: int, conv_w, conv_b, state_in=None, state_out=None,
+                    out=None, batch: Optional[int] = None) -> torch.Tensor:
+    """xz int8 [B, L, W] (or [B*L, W] with ``batch``), x branch = columns [0, d_inner)."""
+    _req(xz, torch.int8, "xz"); _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
+    W = xz.shape[-1]
+    B = xz.shape[0] if batch is None else batch
+    L = xz.numel() // (W * B)
+    xs = out if out is not None else torch.empty((B, L, d_inner), dtype=torch.int8, device=xz.device)
+    _lib.call("mi_conv_squareplus", _ptr(xz), W, _ptr(conv_w), _ptr(conv_b),
+              _ptr(_opt(state_in, torch.int8, "state_in")), _ptr(_opt(state_out, torch.int8, "state_out")),
+              _ptr(xs), B, L, d_inner, _stream())
+    return xs
+
+
+def block_scan(xs, dm, xp, b_off: int, z, z_off: int, base, decay_shift: int, s_y: int,
+               h_in=None, h_out=None, out=None, batch: Optional[int] = None) -> torch.Tensor:
+    """Fused model scan; xs/dm int8 [B,L,D] (or [B*L,D] with ``batch``)."""
+    for t, nm in ((xs, "xs"), (dm, "dm"), (xp, "xp"), (z, "z")):
+        _req(t, torch.int8, nm)
+    _req(base, torch.int32, "base")
+    D, N = base.shape
+    B = xs.shape[0] if batch is None else batch
+    L = xs.numel() // (D * B)
+    yo = out if out is not None else torch.empty((B, L, D), dtype=torch.int8, device=xs.device)
+    _lib.call("mi_block_scan", _ptr(xs), _ptr(dm), _ptr(xp), xp.shape[-1], b_off, _ptr(z), z.shape[-1], z_off,
+              _ptr(base), decay_shift, s_y, _ptr(yo), _ptr(_opt(h_in, torch.int32, "h_in")),
+              _ptr(_opt(h_out, torch.int32, "h_out")), B, L, D, N, _stream())
+    return yo
+
+
+def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
+    _req(logits, torch.int32, "logits")
+    rows, cols = logits.shape
+    o = out if out is not None else torch.empty((rows,), dtype=torch.int64, device=logits.device)
+    _lib.call("mi_argmax_i32", _ptr(logits), cols, _ptr(o), rows, cols, _stream())
+    return o

@@ -1,0 +1,151 @@
+"""Integer parameters of the integer Mamba model (spec mi-spec-1).
+
+The reference keeps float parameters and quantizes at run time
+(``rational_bitnet.py:185-188``); the integer path stores what that
+quantization produces: 2-bit packed ternary matrices, int8 embedding and conv
+taps, int32 decay numerators, and the per-layer power-of-2 shifts.
+
+Config keys follow the reference schema (``configs/config_mamba_integer_l4.json``;
+``MambaIntegerBlock.__init__``, ``mamba_integer_model.py:369-394``):
+``d_model``, ``n_layer``, ``vocab_size``, ``ssm_cfg.{d_state, dt_rank}``;
+``d_inner = 2 * d_model`` as ``mamba_integer_model.py:373``.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List
+
+import numpy as np
+
+DECAY_SHIFT = 15          # decay_shifts buffer value (mamba_integer_model.py:389)
+DECAY_MAX = 32000         # clamp of decay_nums (mamba_integer_model.py:424)
+R_LIM = (1 << 23) - 1     # residual saturation
+EMB_SHIFT = 4             # r0 = emb << 4 (Q4 -> Q8)
+
+
+@dataclass
+class ModelDims:
+    d_model: int
+    n_layer: int
+    vocab_size: int
+    d_state: int
+    dt_rank: int
+
+    @property
+    def d_inner(self) -> int:
+        return 2 * self.d_model
+
+    @property
+    def xp_width(self) -> int:
+        return self.dt_rank + 2 * self.d_state
+
+    @staticmethod
+    def from_config(config: dict) -> "ModelDims":
+        ssm = config.get("ssm_cfg", {})
+        d_model = int(config["d_model"])
+        dt_rank = ssm.get("dt_rank")
+        if dt_rank is None:
+            dt_rank = -(-d_model // 16)
+        return ModelDims(d_model=d_model, n_layer=int(config["n_layer"]),
+                         vocab_size=int(config["vocab_size"]),
+                         d_state=int(ssm.get("d_state", 16)), dt_rank=int(dt_rank))
+
+    def validate(self) -> None:
+        for name, v in (("d_model", self.d_model), ("d_inner", self.d_inner),
+                        ("dt_rank", self.dt_rank)):
+            if v % 16 != 0:
+                raise ValueError(f"{name}={v} must be a multiple of 16 (2-bit packing unit)")
+        if not (1 <= self.d_state <= 64):
+            raise ValueError(f"d_state={self.d_state} outside [1, 64]")
+
+
+def requant_shift(k: int) -> int:
+    """Initial power-of-2 requant shift for fan-in k: floor(log2(2k/3)/2)."""
+    return max(0, int(math.floor(math.log2(2.0 * k / 3.0) / 2.0)))
+
+
+def _bitpos() -> np.ndarray:
+    q = np.arange(16)
+    return 8 * (q & 3) + 2 * (q >> 2)
+
+
+def pack_ternary(w: np.ndarray) -> np.ndarray:
+    """int8 {-1,0,1} [N,K] -> uint8 [N,K/4]: K/16 little-endian words per row,
+    weight 16w+4j+i at bits [8i+2j, 8i+2j+1] of word w; codes 0->00, +1->01,
+    -1->11."""
+    w = np.asarray(w)
+    n, k = w.shape
+    if k % 16:
+        raise ValueError("K must be a multiple of 16")
+    if np.any((w < -1) | (w > 1)):
+        raise ValueError("ternary weights must lie in {-1, 0, 1}")
+    code = (w.astype(np.int64) & 3).astype(np.uint64).reshape(n, k // 16, 16)
+    words = np.bitwise_or.reduce(code << _bitpos().astype(np.uint64), axis=-1).astype("<u4")
+    return words.view(np.uint8).reshape(n, k // 4)
+
+
+def unpack_ternary(p: np.ndarray, k: int) -> np.ndarray:
+    p = np.ascontiguousarray(p, dtype=np.uint8)
+    n = p.shape[0]
+    words = p.reshape(n, k // 16, 4).view("<u4")[..., 0].astype(np.int64)
+    codes = (words[..., None] >> _bitpos()) & 3
+    vals = np.where(codes >= 2, codes - 4, codes).astype(np.int8)
+    return vals.reshape(n, k)
+
+
+@dataclass
+class LayerParams:
+    gamma: np.ndarray        # int16 [d] Q8
+    w_in: np.ndarray         # uint8 [2D, d/4]
+    s_in: int
+    conv_w: np.ndarray       # int8 [D, 4] Q6
+    conv_b: np.ndarray       # int32 [D] Q10
+    w_x: np.ndarray          # uint8 [R+2N, D/4]
+    s_x: int
+    w_dt: np.ndarray         # uint8 [D, R/4]
+    s_dt: int
+    base: np.ndarray         # int32 [D, N]
+    k: int
+    s_y: int
+    w_out: np.ndarray        # uint8 [d, D/4]
+    res_mult: int
+    res_shift: int
+
+
+@dataclass
+class ModelParams:
+    dims: ModelDims
+    emb: np.ndarray          # int8 [V, d] Q4
+    layers: List[LayerParams] = field(default_factory=list)
+    gamma_f: np.ndarray = None   # int16 [d]
+    w_head: np.ndarray = None    # uint8 [V, d/4]
+
+
+def _ternary(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    return pack_ternary(rng.integers(-1, 2, size=(n, k), dtype=np.int8))
+
+
+def init_random_params(dims: ModelDims, seed: int) -> ModelParams:
+    """Random integer model: ternary weights i.i.d. in {-1,0,1} with p=1/3,
+    decays uniform [16384, 32000] with shift 15 (a synthetic checkpoint)."""
+    dims.validate()
+    rng = np.random.default_rng(seed)
+    d, D, N, R, V = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank, dims.vocab_size
+    emb = rng.integers(-64, 65, size=(V, d), dtype=np.int8)
+    layers = []
+    for _ in range(dims.n_layer):
+        layers.append(LayerParams(
+            gamma=np.full(d, 256, dtype=np.int16),
+            w_in=_ternary(rng, 2 * D, d), s_in=requant_shift(d),
+            conv_w=rng.integers(-32, 33, size=(D, 4), dtype=np.int8),
+            conv_b=rng.integers(-512, 513, size=D, dtype=np.int32),
+            w_x=_ternary(rng, R + 2 * N, D), s_x=requant_shift(D),
+            w_dt=_ternary(rng, D, R), s_dt=requant_shift(R) + 3,
+            base=rng.integers(16384, 32001, size=(D, N), dtype=np.int32),
+            k=DECAY_SHIFT, s_y=14,
+            w_out=_ternary(rng, d, D), res_mult=4719, res_shift=16,
+        ))
+    return ModelParams(dims=dims, emb=emb, layers=layers,
+                       gamma_f=np.full(d, 256, dtype=np.int16),
+                       w_head=_ternary(rng, V, d))

@@ -1,0 +1,106 @@
+"""GPU parity of the full integer Mamba stack against the CPU oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def T(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def H(t):
+    return t.cpu().numpy()
+
+
+def _small():
+    from mamba_int import ModelDims, init_random_params
+    dims = ModelDims(d_model=128, n_layer=3, vocab_size=500, d_state=16, dt_rank=16)
+    return init_random_params(dims, 21)
+
+
+def test_model_forward_logits(cuda):
+    from mamba_int.model import IntegerMambaRunner
+    p = _small()
+    ids = np.random.default_rng(0).integers(0, 500, size=(2, 70))
+    ref = O.OracleModel(p).forward(ids)
+    got = H(IntegerMambaRunner(p).forward_logits(T(ids)))
+    assert np.array_equal(got, ref)
+
+
+def test_model_prefill_decode_and_generate(cuda):
+    from mamba_int.model import IntegerMambaRunner
+    p = _small()
+    ids = np.random.default_rng(1).integers(0, 500, size=(3, 40))
+    om = O.OracleModel(p)
+    run = IntegerMambaRunner(p)
+    lg_ref, st_ref = om.prefill(ids)
+    lg, st = run.prefill(T(ids))
+    assert np.array_equal(H(lg), lg_ref)
+    for i in range(3):
+        assert np.array_equal(H(st.conv[i]), st_ref[i].conv)
+        assert np.array_equal(H(st.h[i]), st_ref[i].h)
+    gen_ref = om.generate(ids, 6)
+    assert np.array_equal(H(run.generate(T(ids), 6, use_graph=False)), gen_ref)
+    assert np.array_equal(H(run.generate(T(ids), 6, use_graph=True)), gen_ref)
+
+
+def test_decode_equals_prefill_at_every_position(cuda):
+    """Invariant: step-decode logits at position t equal prefill logits at t."""
+    from mamba_int.model import IntegerMambaRunner
+    p = _small()
+    ids = np.random.default_rng(2).integers(0, 500, size=(2, 24))
+    run = IntegerMambaRunner(p)
+    full = H(run.forward_logits(T(ids)))
+    lg, st = run.prefill(T(ids[:, :5]))
+    assert np.array_equal(H(lg), full[:, 4])
+    for t in range(5, 24):
+        lg = run.decode_step(T(ids[:, t]), st)
+        assert np.array_equal(H(lg), full[:, t])
+
+
+def test_graph_replays_match_eager(cuda):
+    """The captured decode graph, replayed many times with eager work between
+    replays, gives the eager result every time."""
+    from mamba_int.model import IntegerMambaRunner
+    p = _small()
+    ids = np.random.default_rng(3).integers(0, 500, size=(4, 16))
+    run = IntegerMambaRunner(p)
+    eager = H(run.generate(T(ids), 12, use_graph=False))
+    for _ in range(3):
+        assert np.array_equal(H(run.generate(T(ids), 12, use_graph=True)), eager)
+        run.forward_logits(T(ids))
+
+
+def test_config3_width_model_one_sequence(cuda):
+    """Config-3 architecture (d768 x 24, d_inner 1536, N16, vocab 32000) on one
+    64-token sequence + 4 decode steps, bit-exact with the oracle."""
+    from mamba_int import ModelDims, init_random_params
+    from mamba_int.model import IntegerMambaRunner
+    dims = ModelDims(d_model=768, n_layer=24, vocab_size=32000, d_state=16, dt_rank=48)
+    p = init_random_params(dims, 3)
+    ids = np.random.default_rng(3).integers(0, 32000, size=(1, 64))
+    run = IntegerMambaRunner(p)
+    om = O.OracleModel(p)
+    lg_ref, _ = om.prefill(ids)
+    lg, _ = run.prefill(T(ids))
+    assert np.array_equal(H(lg), lg_ref)
+    assert np.array_equal(H(run.generate(T(ids), 4, use_graph=True)), om.generate(ids, 4))
+
+
+def test_dropin_model_api(cuda):
+    import torch
+    from mamba_integer_model import MambaIntegerModel
+    cfg = {"d_model": 128, "n_layer": 2, "vocab_size": 300, "ssm_cfg": {"d_state": 16, "dt_rank": 16}}
+    m = MambaIntegerModel(cfg, seed=5)
+    ids = torch.randint(0, 300, (2, 20)).cuda()
+    logits = m(ids)
+    assert logits.shape == (2, 20, 300) and logits.dtype == torch.float32
+    ref = O.OracleModel(m.params).forward(ids.cpu().numpy())
+    assert np.array_equal(H(m.forward_int(ids)), ref)
+    out = m.generate(ids, 5)
+    assert out.shape == (2, 25)
+    assert np.array_equal(H(out[:, 20:]), O.OracleModel(m.params).generate(ids.cpu().numpy(), 5))

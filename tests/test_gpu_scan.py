@@ -1,0 +1,180 @@
+"""GPU parity of the scans against the CPU oracle (bit-exact)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import i8
+
+pytestmark = pytest.mark.gpu
+
+
+def T(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def H(t):
+    return t.cpu().numpy()
+
+
+def _scan_inputs(rng, B, L, D, N, nlo=16384, nhi=32767):
+    x = i8(rng, B, L, D)
+    b = i8(rng, B, L, N)
+    c = i8(rng, B, L, N)
+    n = rng.integers(nlo, nhi + 1, size=(D, N), dtype=np.int32)
+    return x, b, c, n
+
+
+def test_scan_config1_bit_exact(cuda):
+    """Config 1: B1 L256 D512 N16, n ~ U[16384, 32767], k = 15."""
+    from mamba_int import ops
+    rng = np.random.default_rng(1)
+    x, b, c, n = _scan_inputs(rng, 1, 256, 512, 16)
+    hs = np.zeros((1, 512, 16), np.int32)
+    y_ref, h_ref = O.dyadic_scan(x, b, c, n, 15, h_state=hs)
+    h_out = T(hs)
+    y = ops.dyadic_scan(T(x), T(b), T(c), T(n), 15, h_out=h_out)
+    assert np.array_equal(H(y), y_ref)
+    assert np.array_equal(H(h_out), h_ref)
+
+
+@pytest.mark.parametrize("B,L,D,N,G", [
+    (2, 100, 64, 16, 0), (1, 1, 16, 16, 0), (3, 130, 48, 32, 0), (2, 65, 128, 64, 0),
+    (1, 200, 32, 128, 0), (2, 77, 64, 16, 1), (2, 77, 64, 16, 2), (2, 77, 64, 16, 4),
+    (2, 77, 64, 16, 8), (2, 77, 64, 16, 16), (1, 50, 40, 16, 0), (2, 33, 32, 8, 0), (1, 19, 16, 5, 0),
+])
+def test_scan_shapes(cuda, B, L, D, N, G):
+    """Fast kernel at every lane split, ragged D (generic path), odd N, odd L."""
+    from mamba_int import ops
+    rng = np.random.default_rng(B * 1000 + L * 10 + D + N)
+    x, b, c, n = _scan_inputs(rng, B, L, D, N)
+    y_ref = O.dyadic_scan(x, b, c, n, 15)
+    if G:
+        os.environ["MI_SCAN_G"] = str(G)
+    try:
+        y = ops.dyadic_scan(T(x), T(b), T(c), T(n), 15)
+    finally:
+        os.environ.pop("MI_SCAN_G", None)
+    assert np.array_equal(H(y), y_ref)
+
+
+def test_scan_state_continuation(cuda):
+    """Two calls with the carried state equal one call over the whole sequence."""
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(7)
+    x, b, c, n = _scan_inputs(rng, 2, 300, 64, 16)
+    y_ref = O.dyadic_scan(x, b, c, n, 15)
+    h = torch.zeros((2, 64, 16), dtype=torch.int32, device="cuda")
+    y1 = ops.dyadic_scan(T(x[:, :131]), T(b[:, :131]), T(c[:, :131]), T(n), 15, h_out=h)
+    y2 = ops.dyadic_scan(T(x[:, 131:]), T(b[:, 131:]), T(c[:, 131:]), T(n), 15, h_in=h, h_out=h)
+    assert np.array_equal(np.concatenate([H(y1), H(y2)], axis=1), y_ref)
+
+
+def test_scan_extremes_saturation(cuda):
+    """n = 2^k (pure accumulation) with maximal inputs drives h into int32 saturation."""
+    from mamba_int import ops
+    B, L, D, N = 1, 64, 16, 16
+    x = np.full((B, L, D), 127, np.int8)
+    b = np.full((B, L, N), 127, np.int8)
+    c = np.full((B, L, N), -128, np.int8)
+    n = np.full((D, N), 1 << 15, np.int32)
+    h0 = np.full((B, D, N), 2**31 - 100000, np.int32)
+    y_ref, h_ref = O.dyadic_scan(x, b, c, n, 15, h_state=h0)
+    hin = T(h0)
+    hout = T(np.zeros_like(h0))
+    y = ops.dyadic_scan(T(x), T(b), T(c), T(n), 15, h_in=hin, h_out=hout)
+    assert np.array_equal(H(y), y_ref)
+    assert np.array_equal(H(hout), h_ref)
+    assert (h_ref == 2**31 - 1).all()
+
+
+def test_scan_k16_and_generic_shift(cuda):
+    from mamba_int import ops
+    rng = np.random.default_rng(3)
+    for k, nhi in ((16, 65536), (12, 4096), (1, 2)):
+        x, b, c, n = _scan_inputs(rng, 2, 70, 32, 16, nlo=0, nhi=nhi)
+        y_ref = O.dyadic_scan(x, b, c, n, k)
+        y = ops.dyadic_scan(T(x), T(b), T(c), T(n), k)
+        assert np.array_equal(H(y), y_ref), k
+
+
+def test_scan_f32_reference_semantics(cuda):
+    """mi_dyadic_scan_f32 = the reference launch_dyadic_scan (int64 state, fp32 I/O)."""
+    from mamba_int import ops
+    rng = np.random.default_rng(5)
+    B, S, D = 2, 100, 256
+    x = rng.standard_normal((B, S, D)).astype(np.float32)
+    nums = rng.integers(20000, 32000, size=(B, S, D), dtype=np.int32)
+    shifts = np.full((B, S, D), 15, np.int32)
+    h_ref = O.dyadic_scan_f32(x, nums, shifts, 20)
+    h = ops.dyadic_scan_f32(T(x), T(nums), T(shifts), 20)
+    assert np.array_equal(H(h).view(np.uint32), h_ref.view(np.uint32))
+
+
+def test_scan_elementwise(cuda):
+    from mamba_int import ops
+    rng = np.random.default_rng(9)
+    B, L, C = 2, 90, 300
+    u = rng.integers(-2**20, 2**20, size=(B, L, C), dtype=np.int32)
+    nn = rng.integers(0, 32768, size=(B, L, C), dtype=np.int32)
+    h_ref = O.dyadic_scan_elementwise(u, nn, 15)
+    h = ops.dyadic_scan_elementwise(T(u), T(nn), 15)
+    assert np.array_equal(H(h), h_ref)
+
+
+@pytest.mark.parametrize("B,L,H_,P,N,cs", [
+    (2, 512, 3, 64, 128, 256), (1, 300, 2, 64, 128, 64), (1, 130, 2, 32, 64, 100), (2, 64, 1, 16, 16, 64),
+])
+def test_ssd_chunked(cuda, B, L, H_, P, N, cs):
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(L + H_ + P + N)
+    x = i8(rng, B, L, H_, P)
+    b = i8(rng, B, L, H_, N)
+    c = i8(rng, B, L, H_, N)
+    n = rng.integers(24576, 32768, size=(H_,), dtype=np.int32)
+    y_ref, cst_ref, h_ref = O.ssd_chunked_scan(x, b, c, n, 15, cs, want_chunk_states=True,
+                                               h_state=np.zeros((B, H_, P, N), np.int32))
+    nc = -(-L // cs)
+    cst = torch.zeros((B, nc, H_, P, N), dtype=torch.int32, device="cuda")
+    hout = torch.zeros((B, H_, P, N), dtype=torch.int32, device="cuda")
+    y = ops.ssd_chunked_scan(T(x), T(b), T(c), T(n), 15, cs, chunk_states=cst, h_out=hout)
+    assert np.array_equal(H(y), y_ref)
+    assert np.array_equal(H(cst), cst_ref)
+    assert np.array_equal(H(hout), h_ref)
+
+
+def test_ssd_config4_full_size_slice(cuda):
+    """Config 4 at full size (B4 L8192 H24 P64 N128, cs 256) on the GPU; lanes are
+    independent, so batch 3 / heads 5 and 17 are checked exactly against the oracle."""
+    from mamba_int import ops
+    rng = np.random.default_rng(4)
+    B, L, H_, P, N = 4, 8192, 24, 64, 128
+    x = i8(rng, B, L, H_, P)
+    b = i8(rng, B, L, H_, N)
+    c = i8(rng, B, L, H_, N)
+    n = rng.integers(24576, 32768, size=(H_,), dtype=np.int32)
+    y = H(ops.ssd_chunked_scan(T(x), T(b), T(c), T(n), 15, 256))
+    for hd in (5, 17):
+        y_ref = O.ssd_chunked_scan(x[3:4, :, hd:hd + 1], b[3:4, :, hd:hd + 1], c[3:4, :, hd:hd + 1],
+                                   n[hd:hd + 1], 15, 256)
+        assert np.array_equal(y[3:4, :, hd:hd + 1], y_ref)
+
+
+def test_ssd_equals_channel_scan(cuda):
+    """Per head, the chunked multi-head scan equals the config-1 scan with a constant decay."""
+    from mamba_int import ops
+    rng = np.random.default_rng(11)
+    B, L, H_, P, N = 1, 256, 2, 64, 64
+    x = i8(rng, B, L, H_, P)
+    b = i8(rng, B, L, H_, N)
+    c = i8(rng, B, L, H_, N)
+    n = rng.integers(24576, 32768, size=(H_,), dtype=np.int32)
+    y = H(ops.ssd_chunked_scan(T(x), T(b), T(c), T(n), 15, 128))
+    for hd in range(H_):
+        yc = H(ops.dyadic_scan(T(np.ascontiguousarray(x[:, :, hd])), T(np.ascontiguousarray(b[:, :, hd])),
+                               T(np.ascontiguousarray(c[:, :, hd])), T(np.full((P, N), n[hd], np.int32)), 15))
+        assert np.array_equal(y[:, :, hd], yc)
