@@ -63,6 +63,101 @@ def cpu_baseline(params, threads):
     }
 
 
+def _time_kernel(fn, iters=20, warmup=2, reps=3):
+    """Milliseconds per launch of fn(): `iters` launches captured in one HIP graph,
+    the graph replayed `reps` times between HIP events (median), so host launch
+    overhead is not part of the figure."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(cur)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for _ in range(iters):
+                fn()
+    cur.wait_stream(side)
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) / iters)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def kernel_table():
+    """Per-config kernel timings: config-1 scan, config-2 GEMM and GEMV (weights
+    rotated over 512 copies so the GEMV reads HBM, not the 256 MB MALL), the
+    config-3 decode GEMVs, config-4 chunked scan."""
+    import numpy as np
+    import torch
+    from mamba_int import ops, pack_ternary
+    dev = "cuda:0"
+    rng = np.random.default_rng(1)
+    out = {}
+
+    def t8(*shape):
+        return torch.from_numpy(rng.integers(-127, 128, size=shape, dtype=np.int8)).to(dev)
+
+    # config 1: B1 L256 D512 N16
+    x, b, c = t8(1, 256, 512), t8(1, 256, 16), t8(1, 256, 16)
+    n = torch.from_numpy(rng.integers(16384, 32768, size=(512, 16), dtype=np.int32)).to(dev)
+    ms = _time_kernel(lambda: ops.dyadic_scan(x, b, c, n, 15))
+    byt = 696320
+    out["config1_scan"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
+                           "G_updates_s": 256 * 512 * 16 / ms / 1e6}
+    # config 2: GEMM M4096 K768 N3072 -> int8, and GEMV M1
+    M, K, N = 4096, 768, 3072
+    a = t8(M, K)
+    wp = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(N, K), dtype=np.int8))).to(dev)
+    o8 = torch.empty((M, N), dtype=torch.int8, device=dev)
+    ms = _time_kernel(lambda: ops.bitlinear(a, wp, ops.OUT_INT8, N, shift=5, out=o8, path="gemm"))
+    tops = 2 * M * N * K / ms / 1e9
+    out["config2_gemm"] = {"ms": ms, "TOPS": tops, "mfma_frac": tops / 5000.0,
+                           "GB_s": 16318464 / ms / 1e6}
+    copies = 512
+    wrot = wp.repeat(copies, 1).view(copies, N, K // 4)
+    a1 = a[:1].contiguous()
+    o1 = torch.empty((1, N), dtype=torch.int8, device=dev)
+    idx = {"i": 0}
+
+    def gemv():
+        ops.bitlinear(a1, wrot[idx["i"] % copies], ops.OUT_INT8, N, shift=5, out=o1, path="gemv")
+        idx["i"] += 1
+    ms = _time_kernel(gemv, iters=copies)
+    byt = 593664
+    out["config2_gemv_m1"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
+                              "note": "weights rotated over 512 copies (302 MB > MALL)"}
+    # config-3 decode GEMVs at batch 8
+    for name, (NN, KK) in {"in_proj": (3072, 768), "out_proj": (768, 1536), "lm_head": (32000, 768)}.items():
+        w = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(NN, KK), dtype=np.int8))).to(dev)
+        a8 = t8(8, KK)
+        o = torch.empty((8, NN), dtype=torch.int32, device=dev)
+        ms = _time_kernel(lambda: ops.bitlinear(a8, w, ops.OUT_INT32, NN, out=o, path="gemv"))
+        byt = NN * KK // 4 + 8 * KK + 8 * NN * 4
+        out[f"config3_decode_{name}_gemv"] = {"ms": ms, "GB_s": byt / ms / 1e6, "bytes": byt}
+    # config 4: B4 L8192 H24 P64 N128, chunk 256
+    B, L, H, P, NS = 4, 8192, 24, 64, 128
+    x4, b4, c4 = t8(B, L, H, P), t8(B, L, H, NS), t8(B, L, H, NS)
+    n4 = torch.from_numpy(rng.integers(24576, 32768, size=(H,), dtype=np.int32)).to(dev)
+    ms = _time_kernel(lambda: ops.ssd_chunked_scan(x4, b4, c4, n4, 15, 256), iters=3, warmup=1)
+    byt = 452984928
+    upd = B * L * H * P * NS
+    out["config4_ssd"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
+                          "G_updates_s": upd / ms / 1e6}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -70,6 +165,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--kernels", action="store_true", help="also time each config's kernel")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the integer inference path has no "
@@ -166,6 +262,8 @@ def main():
             "valu_updates_per_s": updates / (scan_avg_ms * 1e-3),
         },
     }
+    if args.kernels:
+        line["kernels"] = kernel_table()
     if not args.no_cpu:
         threads = len(os.sched_getaffinity(0))
         line["cpu_baseline"] = cpu_baseline(params, threads)

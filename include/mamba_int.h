@@ -121,33 +121,43 @@ mi_status mi_act_quant_f32(const float *x, int8_t *xq, float *x_scale, int m, in
  * F.linear + rescale, rational_bitnet.py:204-208, and launch_bitlinear).
  * a int8 [m, lda] (16-byte aligned, lda % 16 == 0); w_packed [n, k/4]
  * (4-byte aligned); out [m, ldo] of the kind's element type (ldo % 4 == 0);
- * k % 16 == 0.  shift in [0,31] for INT8/DECAY_MOD; res_shift in [0,62] for
- * RESIDUAL; x_scale [m] and w_scale for FLOAT.  Chooses the MFMA tile GEMM
- * for m > 64 and the register-unpack GEMV path for m <= 64. */
+ * k % 16 == 0.  shift in [0,30] for INT8/DECAY_MOD; res_shift in [0,62] for
+ * RESIDUAL; x_scale [m] and w_scale for FLOAT.  row_stats (RESIDUAL only,
+ * nullable, int64 [m,2], 8-byte aligned): the sum and the sum of squares of
+ * each updated residual row are added to it with atomics (the caller zeroes
+ * it), the row statistics of the next BitShiftNorm.  Chooses the MFMA tile
+ * GEMM for m > 64 and the register-unpack GEMV path for m <= 64. */
 mi_status mi_bitlinear(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
                        int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                       const float *x_scale, float w_scale, void *stream);
+                       const float *x_scale, float w_scale, int64_t *row_stats, void *stream);
 /* Same contract, forcing the MFMA tile GEMM (prefill path). */
 mi_status mi_bitlinear_gemm(const int8_t *a, int lda, const uint8_t *w_packed, void *out,
                             int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
-                            int res_shift, const float *x_scale, float w_scale, void *stream);
+                            int res_shift, const float *x_scale, float w_scale, int64_t *row_stats,
+                            void *stream);
 /* Same contract, forcing the decode GEMV (m <= 64). */
 mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, void *out,
                             int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
-                            int res_shift, const float *x_scale, float w_scale, void *stream);
+                            int res_shift, const float *x_scale, float w_scale, int64_t *row_stats,
+                            void *stream);
 
 /* ---------------------------------------------------------- block ops */
 
 /* Integer BitShiftNorm (spec rule 4.1; mamba_integer_model.py:144-184,
  * 200-223): r int32 [tokens,dim] (Q8) -> out int8 [tokens,dim]; gamma int16
- * [dim] (Q8). dim in [1, 8192]. */
+ * [dim] (Q8). dim in [1, 8192].  row_stats (nullable, int64 [tokens,2] =
+ * (sum r, sum r^2) per row, as mi_embed / RESIDUAL outputs accumulate them)
+ * turns the norm into an elementwise pass (dim % 4 == 0, r 16-byte aligned). */
 mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens,
-                           int dim, void *stream);
+                           int dim, const int64_t *row_stats, void *stream);
 
 /* Embedding (mamba_integer_model.py:470,487): r[t,:] = emb[ids[t],:] << 4.
- * ids int64 [tokens] (each in [0,vocab)), emb int8 [vocab,dim], r int32. */
+ * ids int64 [tokens] (an id outside [0,vocab) gives a zero row), emb int8
+ * [vocab,dim], r int32.  row_stats (nullable, int64
+ * [stats_layers,tokens,2]): layer 0 receives the row statistics of r, layers
+ * 1..stats_layers-1 are zeroed for the residual epilogues that follow. */
 mi_status mi_embed(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim,
-                   int vocab, void *stream);
+                   int vocab, int64_t *row_stats, int stats_layers, void *stream);
 
 /* Depthwise causal conv (width 4) + squareplus (spec rules 4.3-4.4;
  * mamba_integer_model.py:378,404-411; step form conv1d_step.cu:12-58).
@@ -177,6 +187,44 @@ mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int8_t *xp, in
  * index of the maximum of logits[r, 0:cols] (int32 [rows, ld]). */
 mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, int cols,
                         void *stream);
+
+/* ------------------------------------------------ fused decode stages */
+/* A decode step at small batch is bound by its chain of dependent kernels;
+ * these entries fuse the per-token stages of MambaIntegerBlock.forward
+ * (mamba_integer_model.py:396-447) and the one-step conv of
+ * launch_conv1d_step (conv1d_step.cu:60-79).  Same integer rules as the
+ * unfused ops, bit for bit. */
+
+/* BitShiftNorm of r (int32 [m,k], m <= 16, k % 16 == 0, k <= 3072, r 16-byte
+ * aligned; row statistics from row_stats when non-null) fused into
+ * the BitLinear GEMV: out[m, n] = INT8 (sat8(rshr(acc, shift))) or INT32 acc,
+ * out row stride ldo.  Replaces BitShiftNorm.forward + BitLinear.forward for
+ * one token per sequence (the lm_head path of MambaIntegerModel.forward,
+ * mamba_integer_model.py:492-494). */
+mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                            const uint8_t *w_packed, void *out, int ldo, int kind, int m, int n, int k,
+                            int shift, void *stream);
+
+/* Norm + in_proj (INT8, shift s_in) + depthwise conv step + squareplus:
+ * r int32 [m,d_model]; w_in packed [2*d_inner, d_model/4]; the x half goes
+ * through the conv with conv_state int8 [m,3,d_inner] updated in place and
+ * lands in xs int8 [m,d_inner]; the z half is written to xz int8
+ * [m,2*d_inner] at columns [d_inner, 2*d_inner).  m <= 16, d_model <= 3072. */
+mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                               const uint8_t *w_in, int s_in,
+                               const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
+                               int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream);
+
+/* dt_proj (DECAY_MOD, shift s_dt) + decay + dt + one scan step + y + gate +
+ * requant (spec rules 4.6-4.11 at L = 1): xp int8 [m,xp_stride] (dt_raw at
+ * [0,dt_rank), B, C after it); w_dt packed [d_inner, dt_rank/4]; xs int8
+ * [m,d_inner]; z int8 [m,z_stride] at column z_off; base int32
+ * [d_inner,nstate]; h_state int32 [m,d_inner,nstate] updated in place;
+ * yo int8 [m,d_inner].  dt_rank % 16 == 0, <= 256; nstate <= 64. */
+mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const uint8_t *w_dt, int s_dt,
+                          const int8_t *xs, const int8_t *z, int z_stride, int z_off, const int32_t *base,
+                          int decay_shift, int s_y, int32_t *h_state, int8_t *yo, int m, int d_inner,
+                          int nstate, void *stream);
 
 #ifdef __cplusplus
 }

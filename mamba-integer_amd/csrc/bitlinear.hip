@@ -19,26 +19,10 @@
 //   decode GEMV:  m <= 64; a block owns 16 output features, its 4 waves split
 //                 K; each lane streams 16-byte words of packed weights straight
 //                 from HBM and unpacks them in registers.
-#include "mi_common.hpp"
+#include "mi_mfma.hpp"
 
 namespace mi {
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4i unpack16(uint32_t w) {
-    const uint32_t lut = 0xFFFE0100u;  // byte c = value of code c
-    v4i r;
-    r[0] = (int)__builtin_amdgcn_perm(lut, lut, w & 0x03030303u);
-    r[1] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 2) & 0x03030303u);
-    r[2] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 4) & 0x03030303u);
-    r[3] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 6) & 0x03030303u);
-    return r;
-}
-
-__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
 
 struct GemmArgs {
     const int8_t *a;
@@ -52,12 +36,20 @@ struct GemmArgs {
     int32_t res_mult;
     int res_shift;
     float w_scale;
+    int64_t *row_stats;  // RESIDUAL: per-row (sum r, sum r^2) of the new residual, atomically added
 };
 
-// Epilogue for 4 consecutive features n..n+3 of token m (n % 4 == 0).
+struct RowStat {
+    int64_t s1, s2;
+};
+
+// Epilogue for 4 consecutive features n..n+3 of token m (n % 4 == 0).  For
+// RESIDUAL it returns the sum and the sum of squares of the new residual
+// values it wrote (the row statistics of the next BitShiftNorm).
 template <int KIND>
-__device__ __forceinline__ void store4(const GemmArgs &g, int m, int n, v4i acc) {
-    if (m >= g.M || n >= g.N) return;
+__device__ __forceinline__ RowStat store4(const GemmArgs &g, int m, int n, v4i acc) {
+    RowStat st{0, 0};
+    if (m >= g.M || n >= g.N) return st;
     const bool full = n + 3 < g.N;
     if constexpr (KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD) {
         int8_t *o = (int8_t *)g.out + (int64_t)m * g.ldo + n;
@@ -83,12 +75,29 @@ __device__ __forceinline__ void store4(const GemmArgs &g, int m, int n, v4i acc)
         int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + n;
         for (int r = 0; r < 4 && n + r < g.N; ++r) {
             const int64_t delta = rshr64((int64_t)acc[r] * g.res_mult, g.res_shift);
-            o[r] = (int32_t)clamp64((int64_t)o[r] + delta, -kResidualLimit, kResidualLimit);
+            const int32_t nv = (int32_t)clamp64((int64_t)o[r] + delta, -kResidualLimit, kResidualLimit);
+            o[r] = nv;
+            st.s1 += nv;
+            st.s2 += (int64_t)nv * nv;
         }
     } else {  // MI_OUT_FLOAT: fp32(acc) * (w_scale * x_scale[m]) as rational_bitnet.py:208
         float *o = (float *)g.out + (int64_t)m * g.ldo + n;
         const float sc = __fmul_rn(g.w_scale, g.x_scale[m]);
         for (int r = 0; r < 4 && n + r < g.N; ++r) o[r] = __fmul_rn((float)acc[r], sc);
+    }
+    return st;
+}
+
+// Adds the row statistics held by the four lanes l16, l16+16, l16+32, l16+48
+// (one token, sixteen features) to row_stats[m] with 64-bit atomics.
+__device__ __forceinline__ void flush_row_stat(const GemmArgs &g, RowStat st, int m, int lq) {
+    st.s1 += __shfl_xor(st.s1, 16);
+    st.s1 += __shfl_xor(st.s1, 32);
+    st.s2 += __shfl_xor(st.s2, 16);
+    st.s2 += __shfl_xor(st.s2, 32);
+    if (lq == 0 && m < g.M) {
+        atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m), (unsigned long long)st.s1);
+        atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m + 1), (unsigned long long)st.s2);
     }
 }
 
@@ -144,7 +153,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     };
 
     v4i acc[4][4];
+#pragma unroll
     for (int i = 0; i < 4; ++i)
+#pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
     const int nk = (g.K + kBK - 1) / kBK;
@@ -165,15 +176,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
                 fa[j] = *reinterpret_cast<const v4i *>(&sA[buf][row * kApitch + ks * 64 + lq * 16]);
             }
             for (int i = 0; i < 4; ++i)
-                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fw[i], fa[j], acc[i][j]);
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma_i8(fw[i], fa[j], acc[i][j]);
         }
         if (kt + 1 < nk) store_stage(buf ^ 1);
         __syncthreads();
     }
 
-    for (int i = 0; i < 4; ++i)
-        for (int j = 0; j < 4; ++j)
-            store4<KIND>(g, m0 + wm * 64 + j * 16 + l16, n0 + wn * 64 + i * 16 + 4 * lq, acc[i][j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = m0 + wm * 64 + j * 16 + l16;
+        RowStat st{0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const RowStat e = store4<KIND>(g, m, n0 + wn * 64 + i * 16 + 4 * lq, acc[i][j]);
+            st.s1 += e.s1;
+            st.s2 += e.s2;
+        }
+        if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
+    }
 }
 
 // -------------------------------------------------------------- decode GEMV
@@ -193,14 +213,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
     const int n = n0 + l16;
     const int nsuper = (g.kw + 15) / 16;
 
-    v4i acc[MT];
-    for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
-
-    for (int s = wave; s < nsuper; s += 4) {
+    auto load_w = [&](int s, uint32_t *wv) {
         const int w0 = 16 * s + 4 * lq;
-        uint32_t wv[4];
         if (VEC) {
-            if (n < g.N && w0 < g.kw) {
+            if (s < nsuper && n < g.N && w0 < g.kw) {
                 const uint4 q = *reinterpret_cast<const uint4 *>(g.w + (int64_t)n * g.kw + w0);
                 wv[0] = q.x; wv[1] = q.y; wv[2] = q.z; wv[3] = q.w;
             } else {
@@ -208,18 +224,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
             }
         } else {
             for (int j = 0; j < 4; ++j)
-                wv[j] = (n < g.N && w0 + j < g.kw) ? g.w[(int64_t)n * g.kw + w0 + j] : 0u;
+                wv[j] = (s < nsuper && n < g.N && w0 + j < g.kw) ? g.w[(int64_t)n * g.kw + w0 + j] : 0u;
         }
+    };
+
+    // the residual values wave 0 will update, fetched before the product
+    int32_t rpre[MT][4];
+    if (KIND == MI_OUT_RESIDUAL && wave == 0) {
+        for (int t = 0; t < MT; ++t) {
+            const int m = 16 * t + l16, nf = n0 + 4 * lq;
+            for (int r = 0; r < 4; ++r)
+                rpre[t][r] = (m < g.M && nf + r < g.N) ? ((const int32_t *)g.out)[(int64_t)m * g.ldo + nf + r] : 0;
+        }
+    }
+
+    v4i acc[MT];
+    for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
+    uint32_t cur[4], nxt[4];
+    load_w(wave, cur);
+    for (int s = wave; s < nsuper; s += 4) {
+        load_w(s + 4, nxt);  // next super-step's words in flight during this one
+        const int w0 = 16 * s + 4 * lq;
         for (int j = 0; j < 4; ++j) {
-            const v4i fw = unpack16(wv[j]);
+            const v4i fw = unpack16(cur[j]);
             const int k = 16 * (w0 + j);
             for (int t = 0; t < MT; ++t) {
                 const int m = 16 * t + l16;
                 v4i fa = v4i{0, 0, 0, 0};
                 if (m < g.M && k < g.K) fa = *reinterpret_cast<const v4i *>(g.a + (int64_t)m * g.lda + k);
-                acc[t] = mfma(fw, fa, acc[t]);
+                acc[t] = mfma_i8(fw, fa, acc[t]);
             }
         }
+        for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
     }
     if (wave > 0)
         for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
@@ -227,7 +263,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
     if (wave == 0) {
         for (int t = 0; t < MT; ++t) {
             v4i v = acc[t] + red[0][t][lane] + red[1][t][lane] + red[2][t][lane];
-            store4<KIND>(g, 16 * t + l16, n0 + 4 * lq, v);
+            const int m = 16 * t + l16, nf = n0 + 4 * lq;
+            if constexpr (KIND == MI_OUT_RESIDUAL) {
+                // RESIDUAL from the prefetched values (same rule as store4)
+                RowStat st{0, 0};
+                if (m < g.M && nf < g.N) {
+                    int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + nf;
+                    for (int r = 0; r < 4 && nf + r < g.N; ++r) {
+                        const int64_t delta = rshr64((int64_t)v[r] * g.res_mult, g.res_shift);
+                        const int32_t nv = (int32_t)clamp64((int64_t)rpre[t][r] + delta, -kResidualLimit,
+                                                            kResidualLimit);
+                        o[r] = nv;
+                        st.s1 += nv;
+                        st.s2 += (int64_t)nv * nv;
+                    }
+                }
+                if (g.row_stats) flush_row_stat(g, st, m, lq);
+            } else {
+                store4<KIND>(g, m, nf, v);
+            }
         }
     }
 }
@@ -289,11 +343,11 @@ mi_status validate(const char *fn, const int8_t *a, int lda, const uint8_t *w, v
 }
 
 GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ldo, int m, int n, int k, int shift,
-                   int32_t res_mult, int res_shift, const float *x_scale, float w_scale) {
+                   int32_t res_mult, int res_shift, const float *x_scale, float w_scale, int64_t *row_stats) {
     GemmArgs g{};
     g.a = a; g.w = reinterpret_cast<const uint32_t *>(w); g.out = out; g.x_scale = x_scale;
     g.lda = lda; g.ldo = ldo; g.M = m; g.N = n; g.K = k; g.kw = k / 16;
-    g.shift = shift; g.res_mult = res_mult; g.res_shift = res_shift; g.w_scale = w_scale;
+    g.shift = shift; g.res_mult = res_mult; g.res_shift = res_shift; g.w_scale = w_scale; g.row_stats = row_stats;
     return g;
 }
 
@@ -346,12 +400,16 @@ enum class Path { kAuto, kGemm, kGemv };
 
 mi_status bitlinear_impl(const char *fn, Path path, const int8_t *a, int lda, const uint8_t *w, void *out, int ldo,
                          int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                         const float *x_scale, float w_scale, void *stream) {
+                         const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
     clear_error();
     mi_status st = validate(fn, a, lda, w, out, ldo, kind, m, n, k, shift, res_shift, x_scale);
     if (st != MI_OK || (int64_t)m * n == 0) return st;
     if (path == Path::kGemv) MI_REQUIRE(m <= 64, MI_ERR_BAD_DIM, "%s: the GEMV path takes m <= 64 (m=%d)", fn, m);
-    const GemmArgs g = make_args(a, lda, w, out, ldo, m, n, k, shift, res_mult, res_shift, x_scale, w_scale);
+    if (row_stats) {
+        MI_REQUIRE(kind == MI_OUT_RESIDUAL, MI_ERR_BAD_ARG, "%s: row_stats only with RESIDUAL output", fn);
+        MI_REQUIRE(aligned(row_stats, 8), MI_ERR_BAD_ALIGNMENT, "%s: row_stats must be 8-byte aligned", fn);
+    }
+    const GemmArgs g = make_args(a, lda, w, out, ldo, m, n, k, shift, res_mult, res_shift, x_scale, w_scale, row_stats);
     const bool gemv = path == Path::kGemv || (path == Path::kAuto && m <= 64);
     hipError_t e = gemv ? launch_gemv(kind, g, as_stream(stream)) : launch_gemm(kind, g, as_stream(stream));
     if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
@@ -365,23 +423,23 @@ using namespace mi;
 
 extern "C" mi_status mi_bitlinear(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo, int kind,
                                   int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                                  const float *x_scale, float w_scale, void *stream) {
+                                  const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
     return bitlinear_impl("mi_bitlinear", Path::kAuto, a, lda, w_packed, out, ldo, kind, m, n, k, shift, res_mult,
-                          res_shift, x_scale, w_scale, stream);
+                          res_shift, x_scale, w_scale, row_stats, stream);
 }
 
 extern "C" mi_status mi_bitlinear_gemm(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
                                        int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                                       const float *x_scale, float w_scale, void *stream) {
+                                       const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
     return bitlinear_impl("mi_bitlinear_gemm", Path::kGemm, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
-                          res_mult, res_shift, x_scale, w_scale, stream);
+                          res_mult, res_shift, x_scale, w_scale, row_stats, stream);
 }
 
 extern "C" mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
                                        int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                                       const float *x_scale, float w_scale, void *stream) {
+                                       const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
     return bitlinear_impl("mi_bitlinear_gemv", Path::kGemv, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
-                          res_mult, res_shift, x_scale, w_scale, stream);
+                          res_mult, res_shift, x_scale, w_scale, row_stats, stream);
 }
 
 extern "C" mi_status mi_pack_ternary(const int8_t *w, uint8_t *packed, int n, int k, void *stream) {

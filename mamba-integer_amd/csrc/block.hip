@@ -1,6 +1,6 @@
 // Elementwise and row stages of the integer Mamba block on gfx950 (spec
 // mi-spec-1, rules 4.1, 4.3-4.4 and the model's embedding / greedy pick).
-#include "mi_common.hpp"
+#include "mi_mfma.hpp"
 
 namespace mi {
 namespace {
@@ -57,6 +57,46 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(const int32_t *r, co
     }
 }
 
+// One wave per row, one pass: the row stays in registers (16 int4 per lane,
+// dim <= 4096) while its sum and sum of squares are reduced.
+constexpr int kNormWaveMax = 16;
+
+__global__ __launch_bounds__(256) void norm_wave_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
+                                                        int tokens, int dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= tokens) return;
+    const int32_t *rr = r + row * dim;
+    int4 v[kNormWaveMax];
+    int64_t s1 = 0, s2 = 0;
+#pragma unroll
+    for (int j = 0; j < kNormWaveMax; ++j) {
+        const int i = 4 * lane + 256 * j;
+        v[j] = i < dim ? *reinterpret_cast<const int4 *>(rr + i) : make_int4(0, 0, 0, 0);
+        s1 += (int64_t)v[j].x + v[j].y + v[j].z + v[j].w;
+        s2 += (int64_t)v[j].x * v[j].x + (int64_t)v[j].y * v[j].y + (int64_t)v[j].z * v[j].z +
+              (int64_t)v[j].w * v[j].w;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += __shfl_xor(s1, off);
+        s2 += __shfl_xor(s2, off);
+    }
+    int64_t mu;
+    const int sh = norm_shift(s1, s2, dim, &mu);
+#pragma unroll
+    for (int j = 0; j < kNormWaveMax; ++j) {
+        const int i = 4 * lane + 256 * j;
+        if (i < dim) {
+            const int vv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            uint32_t o = 0;
+            for (int q = 0; q < 4; ++q)
+                o |= (uint32_t)((int)clamp64(rshr64((int64_t)(vv[q] - mu) * gamma[i + q], sh), -127, 127) & 255)
+                     << (8 * q);
+            *reinterpret_cast<uint32_t *>(out + row * dim + i) = o;
+        }
+    }
+}
+
 // --------------------------------------------------------------- embedding
 __global__ void embed_kernel(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -68,24 +108,62 @@ __global__ void embed_kernel(const int64_t *ids, const int8_t *emb, int32_t *r, 
     r[i] = (id >= 0 && id < vocab) ? (int32_t)emb[id * dim + c] * 16 : 0;
 }
 
-// ----------------------------------------------------- conv + squareplus
-// Exact squareplus of spec rule 4.4: a Newton step on the hardware
-// reciprocal-square-root estimate gives sqrt(v^2 + 2^22) to within a unit,
-// and two bounded integer corrections make it the exact floor.
-__device__ __forceinline__ int sqp_q(int32_t c) {
-    const int32_t v = clamp32(c, -51200, 51200);
-    const uint32_t av = (uint32_t)(v < 0 ? -v : v);
-    const uint32_t Y = av * av + (1u << 22);  // < 2^32
-    const float yf = (float)Y;
-    float rs = __builtin_amdgcn_rsqf(yf);
-    rs = rs * (1.5f - 0.5f * yf * rs * rs);
-    uint32_t s = (uint32_t)(yf * rs);
-    if (s > 65535u) s = 65535u;
-    for (int it = 0; it < 4 && (uint64_t)s * s > Y; ++it) --s;
-    for (int it = 0; it < 4 && (uint64_t)(s + 1) * (s + 1) <= Y; ++it) ++s;
-    return clamp32(rshr32(v + (int32_t)s, 7), -127, 127);
+// One block per token: r = emb[id] << 4, its row statistics into
+// stats[0][t] = (sum r, sum r^2), and stats[j][t] = 0 for the later layers
+// (their out_proj epilogues accumulate into them).
+__global__ __launch_bounds__(256) void embed_stats_kernel(const int64_t *ids, const int8_t *emb, int32_t *r,
+                                                          int tokens, int dim, int vocab, int64_t *stats,
+                                                          int stats_layers) {
+    __shared__ int64_t red[2][4];
+    const int64_t t = blockIdx.x;
+    const int64_t id = ids[t];
+    const bool ok = id >= 0 && id < vocab;
+    int64_t s1 = 0, s2 = 0;
+    for (int c = threadIdx.x; c < dim; c += 256) {
+        const int32_t v = ok ? (int32_t)emb[id * dim + c] * 16 : 0;
+        r[t * dim + c] = v;
+        s1 += v;
+        s2 += (int64_t)v * v;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += __shfl_xor(s1, off);
+        s2 += __shfl_xor(s2, off);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wave] = s1;
+        red[1][wave] = s2;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        stats[2 * t] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+        stats[2 * t + 1] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    }
+    for (int j = 1 + (int)threadIdx.x; j < stats_layers; j += 256) {
+        stats[((int64_t)j * tokens + t) * 2] = 0;
+        stats[((int64_t)j * tokens + t) * 2 + 1] = 0;
+    }
 }
 
+// Elementwise BitShiftNorm from precomputed row statistics: thread = 4 channels.
+__global__ __launch_bounds__(256) void norm_stats_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
+                                                         const int64_t *stats, int tokens, int dim) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int d4 = dim / 4;
+    if (i >= (int64_t)tokens * d4) return;
+    const int64_t t = i / d4;
+    const int c = (int)(i % d4) * 4;
+    int64_t mu;
+    const int sh = norm_shift(stats[2 * t], stats[2 * t + 1], dim, &mu);
+    const int4 v = *reinterpret_cast<const int4 *>(r + t * dim + c);
+    const int vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o = 0;
+    for (int q = 0; q < 4; ++q)
+        o |= (uint32_t)((int)clamp64(rshr64((int64_t)(vv[q] - mu) * gamma[c + q], sh), -127, 127) & 255) << (8 * q);
+    *reinterpret_cast<uint32_t *>(out + t * dim + c) = o;
+}
+
+// ----------------------------------------------------- conv + squareplus
 constexpr int kConvTT = 16;  // time steps per thread
 
 // Thread = (b, group of kConvTT steps, 4 channels).  The thread of step-group 0
@@ -146,16 +224,40 @@ __global__ __launch_bounds__(256) void conv_sqp_kernel(const int8_t *xz, int64_t
 }
 
 // ---------------------------------------------------------------- argmax
-__global__ __launch_bounds__(256) void argmax_kernel(const int32_t *logits, int64_t ld, int64_t *out, int cols) {
+// One block per row.  Each thread walks its columns in increasing order with
+// four independent 16-byte loads in flight, keeping the first maximum; the
+// block reduction prefers the larger value, then the smaller index.
+__global__ __launch_bounds__(256) void argmax_kernel(const int32_t *logits, int64_t ld, int64_t *out, int cols,
+                                                     bool vec) {
     __shared__ int32_t sv[256];
     __shared__ int32_t si[256];
     const int64_t row = blockIdx.x;
     const int32_t *lr = logits + row * ld;
     int32_t best = INT32_MIN;
     int32_t bi = 0x7fffffff;
-    for (int c = threadIdx.x; c < cols; c += 256) {
+    int cstart = 0;
+    if (vec) {
+        const int nv = cols / 4;
+        const int4 *lv = reinterpret_cast<const int4 *>(lr);
+        for (int v0 = threadIdx.x; v0 < nv; v0 += 1024) {
+            int4 q[4];
+            for (int u = 0; u < 4; ++u) {
+                const int v = v0 + 256 * u;
+                q[u] = v < nv ? lv[v] : make_int4(INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN);
+            }
+            for (int u = 0; u < 4; ++u) {
+                const int c = 4 * (v0 + 256 * u);
+                if (q[u].x > best) { best = q[u].x; bi = c; }
+                if (q[u].y > best) { best = q[u].y; bi = c + 1; }
+                if (q[u].z > best) { best = q[u].z; bi = c + 2; }
+                if (q[u].w > best) { best = q[u].w; bi = c + 3; }
+            }
+        }
+        cstart = 4 * nv;
+    }
+    for (int c = cstart + threadIdx.x; c < cols; c += 256) {
         const int32_t v = lr[c];
-        if (v > best) { best = v; bi = c; }  // strided scan keeps the first max of this thread
+        if (v > best || (v == best && c < bi)) { best = v; bi = c; }
     }
     sv[threadIdx.x] = best;
     si[threadIdx.x] = bi;
@@ -179,23 +281,41 @@ __global__ __launch_bounds__(256) void argmax_kernel(const int32_t *logits, int6
 using namespace mi;
 
 extern "C" mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
-                                      void *stream) {
+                                      const int64_t *row_stats, void *stream) {
     clear_error();
     MI_REQUIRE(tokens >= 0, MI_ERR_BAD_DIM, "mi_bitshift_norm: negative tokens");
     MI_REQUIRE(dim >= 1 && dim <= kNormThreads * kNormMaxPer, MI_ERR_BAD_DIM, "mi_bitshift_norm: dim=%d outside [1,%d]",
                dim, kNormThreads * kNormMaxPer);
     if (tokens == 0) return MI_OK;
     MI_REQUIRE(r && gamma && out, MI_ERR_NULL_POINTER, "mi_bitshift_norm: r, gamma and out are required");
-    hipLaunchKernelGGL(norm_kernel, dim3((unsigned)tokens), dim3(kNormThreads), 0, as_stream(stream), r, gamma, out, dim);
+    if (row_stats) {
+        MI_REQUIRE(dim % 4 == 0 && aligned(r, 16) && aligned(out, 4), MI_ERR_BAD_ALIGNMENT,
+                   "mi_bitshift_norm: with row_stats, dim %% 4 == 0 and aligned r/out are required");
+        const int64_t threads = (int64_t)tokens * (dim / 4);
+        hipLaunchKernelGGL(norm_stats_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, as_stream(stream), r,
+                           gamma, out, row_stats, tokens, dim);
+    } else if (dim % 4 == 0 && dim <= 256 * kNormWaveMax && aligned(r, 16) && aligned(out, 4)) {
+        hipLaunchKernelGGL(norm_wave_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, as_stream(stream), r,
+                           gamma, out, tokens, dim);
+    } else {
+        hipLaunchKernelGGL(norm_kernel, dim3((unsigned)tokens), dim3(kNormThreads), 0, as_stream(stream), r, gamma, out,
+                           dim);
+    }
     return check_launch("mi_bitshift_norm");
 }
 
 extern "C" mi_status mi_embed(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab,
-                              void *stream) {
+                              int64_t *row_stats, int stats_layers, void *stream) {
     clear_error();
     MI_REQUIRE(tokens >= 0 && dim >= 0 && vocab >= 0, MI_ERR_BAD_DIM, "mi_embed: negative size");
     if ((int64_t)tokens * dim == 0) return MI_OK;
     MI_REQUIRE(ids && emb && r, MI_ERR_NULL_POINTER, "mi_embed: ids, emb and r are required");
+    if (row_stats) {
+        MI_REQUIRE(stats_layers >= 1, MI_ERR_BAD_ARG, "mi_embed: stats_layers=%d must be >= 1", stats_layers);
+        hipLaunchKernelGGL(embed_stats_kernel, dim3((unsigned)tokens), dim3(256), 0, as_stream(stream), ids, emb, r,
+                           tokens, dim, vocab, row_stats, stats_layers);
+        return check_launch("mi_embed");
+    }
     const int64_t n = (int64_t)tokens * dim;
     hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), ids, emb, r,
                        tokens, dim, vocab);
@@ -231,7 +351,8 @@ extern "C" mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, 
     if (rows == 0) return MI_OK;
     MI_REQUIRE(cols >= 1, MI_ERR_BAD_DIM, "mi_argmax_i32: cols must be positive");
     MI_REQUIRE(logits && out, MI_ERR_NULL_POINTER, "mi_argmax_i32: logits and out are required");
+    const bool vec = ld % 4 == 0 && aligned(logits, 16);
     hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), logits, (int64_t)ld, out,
-                       cols);
+                       cols, vec);
     return check_launch("mi_argmax_i32");
 }

@@ -1,0 +1,372 @@
+// Fused decode-step stages of the integer Mamba block on gfx950 (spec
+// mi-spec-1, rules 4.1-4.12 at one token per sequence).
+//
+// A decode step at small batch is bound by the chain of dependent kernels,
+// not by bytes (the packed weights of the d768 x 24 model are 28.6 MB), so a
+// layer runs as four kernels instead of seven:
+//
+//   norm_gemv      BitShiftNorm of the residual rows recomputed inside every
+//                  block (rows <= 16, staged in LDS as int8), in_proj GEMV on
+//                  MFMA, and for the x half the depthwise conv step + squareplus
+//                  with the conv ring updated in place; the z half is stored.
+//   (x_proj GEMV)  bitlinear.hip
+//   dt_scan_step   dt_proj as a per-channel dot (v_dot4_i32_i8) fused with the
+//                  decay clamp, dt, the scan state update, y = C.h, the gate and
+//                  the requant of the out_proj input.
+//   (out_proj GEMV + residual) bitlinear.hip
+//
+// The same norm_gemv (INT32 output, no conv) computes the lm_head logits.
+#include "mi_mfma.hpp"
+
+namespace mi {
+namespace {
+
+constexpr int kMaxRows = 16;    // tokens per norm_gemv launch
+constexpr int kMaxNormK = 3072; // d_model limit of the LDS-staged rows
+
+struct NormGemvArgs {
+    const int32_t *r;       // [M][K] residual, Q8
+    const int64_t *row_stats;  // [M][2] (sum r, sum r^2) or null (computed here)
+    const int16_t *gamma;   // [K]
+    const uint32_t *w;      // [N][K/16] packed words
+    void *out;              // INT32: [M][ldo]; INT8: [M][ldo] (z half written)
+    int64_t ldo;
+    int M, N, K, kw;
+    int shift;
+    // conv epilogue for features n < conv_d
+    const int8_t *conv_w;   // [conv_d][4]
+    const int32_t *conv_b;  // [conv_d]
+    int8_t *conv_state;     // [M][3][conv_d]
+    int8_t *xs;             // [M][conv_d]
+    int conv_d;
+};
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Normalized int8 rows (spec rule 4.1) of r[0..M) into LDS a[16][pitch]: one
+// wave per row, the row statistics taken from row_stats or summed here in one
+// pass.
+__device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int m = wave; m < g.M; m += 4) {
+        const int32_t *row = g.r + (int64_t)m * g.K;
+        int64_t s1, s2;
+        if (g.row_stats) {
+            s1 = g.row_stats[2 * m];
+            s2 = g.row_stats[2 * m + 1];
+        } else {
+            s1 = 0;
+            s2 = 0;
+            for (int i = lane; i < g.K; i += 64) {
+                const int64_t v = row[i];
+                s1 += v;
+                s2 += v * v;
+            }
+            s1 = wave_sum64(s1);
+            s2 = wave_sum64(s2);
+        }
+        int64_t mu;
+        const int sh = norm_shift(s1, s2, g.K, &mu);
+        for (int i = 4 * lane; i < g.K; i += 256) {
+            const int4 v = *reinterpret_cast<const int4 *>(row + i);
+            const int vv[4] = {v.x, v.y, v.z, v.w};
+            uint32_t o = 0;
+            for (int q = 0; q < 4; ++q)
+                o |= (uint32_t)((int)clamp64(rshr64((int64_t)(vv[q] - mu) * g.gamma[i + q], sh), -127, 127) & 255)
+                     << (8 * q);
+            *reinterpret_cast<uint32_t *>(&a[m * pitch + i]) = o;
+        }
+    }
+}
+
+// Two block shapes.  Narrow (WIDE = false): 16 output features per block, the
+// 4 waves split K in 256-wide super-steps and reduce through LDS (in_proj:
+// 192 blocks at d768).  Wide: 64 features per block, each wave owns 16 of them
+// over the whole K, so the row normalization is shared by 4x more outputs
+// (lm_head: 500 blocks instead of 2000).  Every global load that does not
+// depend on the normalized rows (packed weights, conv ring, conv taps) is
+// issued before the rows are staged, so its latency overlaps the staging.
+constexpr int kMaxSuper = kMaxNormK / 256;
+
+template <int KIND, bool CONV, bool WIDE>
+__global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
+    extern __shared__ __align__(16) int8_t smem[];
+    const int pitch = g.K + 16;                       // conflict-free b128 row reads
+    int8_t *a = smem;                                 // [16][pitch]
+    v4i *red = reinterpret_cast<v4i *>(smem + kMaxRows * pitch);  // [3][64]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int n0 = WIDE ? blockIdx.x * 64 + wave * 16 : blockIdx.x * 16;
+    const int n = n0 + l16;
+    const int nsuper = (g.kw + 15) / 16;
+    constexpr int kPer = WIDE ? kMaxSuper : (kMaxSuper + 3) / 4;
+    const int s_first = WIDE ? 0 : wave, s_step = WIDE ? 1 : 4;
+
+    uint32_t wv[kPer][4];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int w0 = 16 * (s_first + i * s_step) + 4 * lq;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            wv[i][j] = (n < g.N && w0 + j < g.kw) ? g.w[(int64_t)n * g.kw + w0 + j] : 0u;
+    }
+    // conv operands of this lane's epilogue (token l16, features nf..nf+3)
+    const int m = l16;
+    const int nf = n0 + 4 * lq;
+    const bool epi = (WIDE || wave == 0) && m < g.M && nf < g.N;
+    const bool conv = CONV && epi && nf < g.conv_d;
+    uint32_t cs0 = 0, cs1 = 0, cs2 = 0, cw[4] = {0, 0, 0, 0};
+    int32_t cb[4] = {0, 0, 0, 0};
+    if (conv) {
+        const int8_t *st = g.conv_state + (int64_t)m * 3 * g.conv_d;
+        cs0 = *reinterpret_cast<const uint32_t *>(st + nf);
+        cs1 = *reinterpret_cast<const uint32_t *>(st + g.conv_d + nf);
+        cs2 = *reinterpret_cast<const uint32_t *>(st + 2 * g.conv_d + nf);
+        for (int r = 0; r < 4; ++r) {
+            cw[r] = *reinterpret_cast<const uint32_t *>(g.conv_w + (int64_t)(nf + r) * 4);
+            cb[r] = g.conv_b[nf + r];
+        }
+    }
+
+    stage_norm_rows(g, a, pitch);
+    __syncthreads();
+
+    v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int sidx = s_first + i * s_step;
+        if (sidx < nsuper) {
+            const int w0 = 16 * sidx + 4 * lq;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = 16 * (w0 + j);
+                v4i fa = v4i{0, 0, 0, 0};
+                if (k < g.K) fa = *reinterpret_cast<const v4i *>(&a[l16 * pitch + k]);
+                acc = mfma_i8(unpack16(wv[i][j]), fa, acc);
+            }
+        }
+    }
+    if (!WIDE) {
+        if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = acc + red[lane] + red[64 + lane] + red[128 + lane];
+    }
+    if (!epi) return;
+    if constexpr (KIND == MI_OUT_INT32) {
+        int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + nf;
+        for (int r = 0; r < 4 && nf + r < g.N; ++r) o[r] = acc[r];
+    } else {
+        int v[4];
+        for (int r = 0; r < 4; ++r) v[r] = clamp32(rshr32(acc[r], g.shift), -127, 127);
+        if (conv) {
+            // depthwise conv step (conv1d_step.cu:30-57) + squareplus on 4 channels
+            uint32_t xsw = 0, cur = 0;
+            for (int r = 0; r < 4; ++r) {
+                int32_t c = cb[r];
+                c += (int)(int8_t)(cw[r]) * (int)(int8_t)(cs0 >> (8 * r));
+                c += (int)(int8_t)(cw[r] >> 8) * (int)(int8_t)(cs1 >> (8 * r));
+                c += (int)(int8_t)(cw[r] >> 16) * (int)(int8_t)(cs2 >> (8 * r));
+                c += (int)(int8_t)(cw[r] >> 24) * v[r];
+                xsw |= (uint32_t)(sqp_q(c) & 255) << (8 * r);
+                cur |= (uint32_t)(v[r] & 255) << (8 * r);
+            }
+            int8_t *st = g.conv_state + (int64_t)m * 3 * g.conv_d;
+            *reinterpret_cast<uint32_t *>(g.xs + (int64_t)m * g.conv_d + nf) = xsw;
+            *reinterpret_cast<uint32_t *>(st + nf) = cs1;
+            *reinterpret_cast<uint32_t *>(st + g.conv_d + nf) = cs2;
+            *reinterpret_cast<uint32_t *>(st + 2 * g.conv_d + nf) = cur;
+        } else {
+            int8_t *o = (int8_t *)g.out + (int64_t)m * g.ldo + nf;
+            for (int r = 0; r < 4 && nf + r < g.N; ++r) o[r] = (int8_t)v[r];
+        }
+    }
+}
+
+// ------------------------------------------------------------ dt + scan step
+struct DtScanArgs {
+    const int8_t *xp;       // [M][xp_stride]: dt_raw at [0,R), B at [R,R+N), C at [R+N,R+2N)
+    int64_t xp_stride;
+    int R;
+    const uint32_t *w_dt;   // [D][R/16] words
+    int s_dt;
+    const int8_t *xs;       // [M][D]
+    const int8_t *z;        // [M][z_stride] (already offset to the z columns)
+    int64_t z_stride;
+    const int32_t *base;    // [D][N]
+    int k, s_y;
+    int32_t *h;             // [M][D][N] in place
+    int8_t *yo;             // [M][D]
+    int M, D, N;
+};
+
+constexpr int kMaxR = 256;
+constexpr int kMaxN = 64;
+
+// Thread quad per channel: lane g of the quad keeps states g, g+4, g+8, ...;
+// every lane computes the channel's dt_proj dot (48-wide at d768), the quad
+// sums y with two DPP adds, lane 0 gates and writes.
+__global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
+    __shared__ __align__(16) int8_t s_dt[kMaxR];
+    __shared__ int8_t s_bc[2 * kMaxN];
+    constexpr int kPerLane = kMaxN / 4;
+    const int m = blockIdx.y;
+    const int q = threadIdx.x & 3;
+    const int d = blockIdx.x * 64 + (threadIdx.x >> 2);
+    const bool active = d < g.D;
+    const int dd = active ? d : 0;
+    // loads that do not depend on the staged row: ternary dt_proj words, state, decays, xs, z
+    const int kw = g.R / 16;
+    uint32_t wdt[kMaxR / 16];
+#pragma unroll
+    for (int w = 0; w < kMaxR / 16; ++w) wdt[w] = w < kw ? g.w_dt[(int64_t)dd * kw + w] : 0u;
+    int32_t *hp = g.h + ((int64_t)m * g.D + dd) * g.N;
+    const int32_t *bp = g.base + (int64_t)dd * g.N;
+    int32_t hv[kPerLane], bv[kPerLane];
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+        const int n = q + 4 * i;
+        hv[i] = (active && n < g.N) ? hp[n] : 0;
+        bv[i] = (active && n < g.N) ? bp[n] : 0;
+    }
+    const int xsv = g.xs[(int64_t)m * g.D + dd];
+    const int zv = g.z[(int64_t)m * g.z_stride + dd];
+
+    const int8_t *row = g.xp + (int64_t)m * g.xp_stride;
+    for (int i = threadIdx.x; i < g.R; i += 256) s_dt[i] = row[i];
+    for (int i = threadIdx.x; i < 2 * g.N; i += 256) s_bc[i] = row[g.R + i];
+    __syncthreads();
+
+    int acc = 0;
+#pragma unroll
+    for (int w = 0; w < kMaxR / 16; ++w) {
+        if (w < kw) {
+            const v4i wt = unpack16(wdt[w]);
+            for (int j = 0; j < 4; ++j)
+                acc = __builtin_amdgcn_sdot4(wt[j], *reinterpret_cast<const int *>(&s_dt[16 * w + 4 * j]), acc, false);
+        }
+    }
+    const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
+    const int64_t xd = rshr64((int64_t)xsv * dt_q16(dm), 10);
+    int64_t y = 0;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+        const int n = q + 4 * i;
+        if (active && n < g.N) {
+            const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
+            const int32_t hn = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[n] * xd);
+            hp[n] = hn;
+            y += (int64_t)s_bc[g.N + n] * hn;
+        }
+    }
+    y += __shfl_xor(y, 1);
+    y += __shfl_xor(y, 2);
+    if (active && q == 0) {
+        const int64_t yg = ((int64_t)sat32_64(y) * gate_q15(zv)) >> 15;
+        g.yo[(int64_t)m * g.D + d] = (int8_t)clamp64(rshr64(yg, g.s_y), -127, 127);
+    }
+}
+
+mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma, const uint8_t *w, int m, int n,
+                          int k) {
+    MI_REQUIRE(m >= 0 && n >= 0 && k >= 0, MI_ERR_BAD_DIM, "%s: negative size", fn);
+    MI_REQUIRE(m <= kMaxRows, MI_ERR_BAD_DIM, "%s: m=%d exceeds %d tokens", fn, m, kMaxRows);
+    MI_REQUIRE(k % 16 == 0 && k <= kMaxNormK, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 16 and <= %d", fn, k,
+               kMaxNormK);
+    if ((int64_t)m * n == 0) return MI_OK;
+    MI_REQUIRE(r && gamma && w, MI_ERR_NULL_POINTER, "%s: r, gamma and w_packed are required", fn);
+    MI_REQUIRE(aligned(w, 4), MI_ERR_BAD_ALIGNMENT, "%s: w_packed must be 4-byte aligned", fn);
+    return MI_OK;
+}
+
+size_t norm_gemv_lds(int k) { return (size_t)kMaxRows * (k + 16) + 3 * 64 * sizeof(v4i); }
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                       const uint8_t *w_packed, void *out, int ldo, int kind, int m, int n, int k,
+                                       int shift, void *stream) {
+    clear_error();
+    mi_status st = check_norm_gemv("mi_norm_bitlinear", r, gamma, w_packed, m, n, k);
+    if (st != MI_OK || (int64_t)m * n == 0) return st;
+    MI_REQUIRE(kind == MI_OUT_INT8 || kind == MI_OUT_INT32, MI_ERR_BAD_ARG,
+               "mi_norm_bitlinear: kind %d (INT8 or INT32 only)", kind);
+    MI_REQUIRE(out && ldo >= n, MI_ERR_BAD_DIM, "mi_norm_bitlinear: out required with ldo >= n");
+    MI_REQUIRE(shift >= 0 && shift <= 30, MI_ERR_BAD_ARG, "mi_norm_bitlinear: shift=%d outside [0,30]", shift);
+    NormGemvArgs g{};
+    MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "mi_norm_bitlinear: r must be 16-byte aligned");
+    g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_packed);
+    g.out = out; g.ldo = ldo;
+    g.M = m; g.N = n; g.K = k; g.kw = k / 16; g.shift = shift;
+    // wide blocks (64 features) once there are enough of them to fill the GPU
+    const bool wide = n >= 16384;
+    const dim3 grid((unsigned)(wide ? (n + 63) / 64 : (n + 15) / 16));
+    const size_t lds = norm_gemv_lds(k);
+    hipStream_t hs = as_stream(stream);
+    if (kind == MI_OUT_INT32) {
+        if (wide) hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT32, false, true>), grid, dim3(256), lds, hs, g);
+        else hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT32, false, false>), grid, dim3(256), lds, hs, g);
+    } else {
+        if (wide) hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, false, true>), grid, dim3(256), lds, hs, g);
+        else hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, false, false>), grid, dim3(256), lds, hs, g);
+    }
+    return check_launch("mi_norm_bitlinear");
+}
+
+extern "C" mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                          const uint8_t *w_in, int s_in,
+                                          const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
+                                          int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream) {
+    clear_error();
+    mi_status st = check_norm_gemv("mi_norm_in_proj_conv", r, gamma, w_in, m, 2 * d_inner, d_model);
+    if (st != MI_OK || (int64_t)m * d_inner == 0) return st;
+    MI_REQUIRE(d_inner % 16 == 0, MI_ERR_BAD_DIM, "mi_norm_in_proj_conv: d_inner=%d must be a multiple of 16", d_inner);
+    MI_REQUIRE(conv_w && conv_b && conv_state && xs && xz, MI_ERR_NULL_POINTER,
+               "mi_norm_in_proj_conv: conv_w, conv_b, conv_state, xs and xz are required");
+    MI_REQUIRE(aligned(conv_w, 4) && aligned(conv_state, 4) && aligned(xs, 4), MI_ERR_BAD_ALIGNMENT,
+               "mi_norm_in_proj_conv: conv_w, conv_state and xs must be 4-byte aligned");
+    MI_REQUIRE(s_in >= 0 && s_in <= 30, MI_ERR_BAD_ARG, "mi_norm_in_proj_conv: s_in=%d outside [0,30]", s_in);
+    NormGemvArgs g{};
+    MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "mi_norm_in_proj_conv: r must be 16-byte aligned");
+    g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_in); g.out = xz;
+    g.ldo = 2 * (int64_t)d_inner;
+    g.M = m; g.N = 2 * d_inner; g.K = d_model; g.kw = d_model / 16; g.shift = s_in;
+    g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs; g.conv_d = d_inner;
+    hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, true, false>), dim3((unsigned)(2 * d_inner / 16)), dim3(256),
+                       norm_gemv_lds(d_model), as_stream(stream), g);
+    return check_launch("mi_norm_in_proj_conv");
+}
+
+extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const uint8_t *w_dt, int s_dt,
+                                     const int8_t *xs, const int8_t *z, int z_stride, int z_off, const int32_t *base,
+                                     int decay_shift, int s_y, int32_t *h_state, int8_t *yo, int m, int d_inner,
+                                     int nstate, void *stream) {
+    clear_error();
+    MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_dt_scan_step: negative size");
+    MI_REQUIRE(dt_rank >= 16 && dt_rank % 16 == 0 && dt_rank <= kMaxR, MI_ERR_BAD_DIM,
+               "mi_dt_scan_step: dt_rank=%d must be a multiple of 16 in [16,%d]", dt_rank, kMaxR);
+    MI_REQUIRE(nstate >= 1 && nstate <= kMaxN, MI_ERR_BAD_DIM, "mi_dt_scan_step: nstate=%d outside [1,%d]", nstate,
+               kMaxN);
+    MI_REQUIRE(dt_rank + 2 * nstate <= xp_stride, MI_ERR_BAD_DIM, "mi_dt_scan_step: xp_stride=%d too small", xp_stride);
+    MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride, MI_ERR_BAD_DIM, "mi_dt_scan_step: z columns exceed z_stride");
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG, "mi_dt_scan_step: decay_shift outside [1,30]");
+    MI_REQUIRE(s_dt >= 0 && s_dt <= 30 && s_y >= 0 && s_y <= 40, MI_ERR_BAD_ARG, "mi_dt_scan_step: shift out of range");
+    if ((int64_t)m * d_inner == 0) return MI_OK;
+    MI_REQUIRE(xp && w_dt && xs && z && base && h_state && yo, MI_ERR_NULL_POINTER,
+               "mi_dt_scan_step: a required pointer is NULL");
+    MI_REQUIRE(aligned(w_dt, 4), MI_ERR_BAD_ALIGNMENT, "mi_dt_scan_step: w_dt must be 4-byte aligned");
+    DtScanArgs g{};
+    g.xp = xp; g.xp_stride = xp_stride; g.R = dt_rank; g.w_dt = reinterpret_cast<const uint32_t *>(w_dt); g.s_dt = s_dt;
+    g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
+    g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
+    hipLaunchKernelGGL(dt_scan_step_kernel, dim3((unsigned)((d_inner + 63) / 64), (unsigned)m), dim3(256), 0,
+                       as_stream(stream), g);
+    return check_launch("mi_dt_scan_step");
+}

@@ -48,6 +48,21 @@ __host__ __device__ __forceinline__ uint64_t isqrt64(uint64_t v) {
     return s;
 }
 
+// BitShiftNorm parameters of one row (spec rule 4.1) from its exact row
+// statistics s1 = sum r, s2 = sum r^2: mu = floor(s1/dim) and
+// S = sum (r - mu)^2 = s2 - 2 mu s1 + dim mu^2 (exact in int64 for
+// |r| < 2^23, dim <= 8192); returns the output shift 12 + k of the threshold
+// table (mamba_integer_model.py:169-182 on var = S / (dim * 2^16)).
+__host__ __device__ __forceinline__ int norm_shift(int64_t s1, int64_t s2, int dim, int64_t *mu_out) {
+    const int64_t mu = s1 >= 0 ? s1 / dim : -((-s1 + dim - 1) / dim);
+    const int64_t S = s2 - 2 * mu * s1 + (int64_t)dim * mu * mu;
+    int kk = 0;
+    for (int j = 1; j <= 8; ++j) kk += S >= ((int64_t)dim << (2 * (j + 8)));
+    for (int j = 1; j <= 3; ++j) kk -= S < ((int64_t)dim << (2 * (8 - j)));
+    *mu_out = mu;
+    return 12 + kk;
+}
+
 // dt of spec rule 4.8 (mamba_integer_model.py:427) for dm in [-20, 20].
 __host__ __device__ inline int32_t dt_q16(int dm) {
     int64_t s = (int64_t)dm * 65536 +

@@ -1,0 +1,47 @@
+// Ternary unpack and the int8 MFMA used by every BitLinear kernel.
+#pragma once
+
+#include "mi_common.hpp"
+
+namespace mi {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// 16 ternary weights of one packed word -> 16 int8 in k order (4 dwords).
+// (word >> 2j) & 0x03030303 holds the 2-bit codes of weights 4j..4j+3 in byte
+// order; v_perm_b32 against the byte table {0x00, 0x01, 0xFE, 0xFF} (byte c =
+// value of code c, both permute sources equal) sign-extends all four at once.
+__device__ __forceinline__ v4i unpack16(uint32_t w) {
+    const uint32_t lut = 0xFFFE0100u;
+    v4i r;
+    r[0] = (int)__builtin_amdgcn_perm(lut, lut, w & 0x03030303u);
+    r[1] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 2) & 0x03030303u);
+    r[2] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 4) & 0x03030303u);
+    r[3] = (int)__builtin_amdgcn_perm(lut, lut, (w >> 6) & 0x03030303u);
+    return r;
+}
+
+// D(16x16) += A(16x64) * B(64x16), int8 in, int32 accumulate (gfx950).
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Exact squareplus of spec rule 4.4 on a conv output c (Q10) -> int8 (Q4): a
+// Newton step on the hardware reciprocal-square-root estimate gives
+// sqrt(v^2 + 2^22) within a unit; bounded integer corrections make it the
+// exact floor.
+__device__ __forceinline__ int sqp_q(int32_t c) {
+    const int32_t v = clamp32(c, -51200, 51200);
+    const uint32_t av = (uint32_t)(v < 0 ? -v : v);
+    const uint32_t Y = av * av + (1u << 22);  // < 2^32
+    const float yf = (float)Y;
+    float rs = __builtin_amdgcn_rsqf(yf);
+    rs = rs * (1.5f - 0.5f * yf * rs * rs);
+    uint32_t s = (uint32_t)(yf * rs);
+    if (s > 65535u) s = 65535u;
+    for (int it = 0; it < 4 && (uint64_t)s * s > Y; ++it) --s;
+    for (int it = 0; it < 4 && (uint64_t)(s + 1) * (s + 1) <= Y; ++it) ++s;
+    return clamp32(rshr32(v + (int32_t)s, 7), -127, 127);
+}
+
+}  // namespace mi

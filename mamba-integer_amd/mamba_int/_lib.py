@@ -30,14 +30,17 @@ SIGNATURES = {
     "mi_ssd_chunked_scan": [P, P, P, P, I, P, P, P, P, I, I, I, I, I, I, P],
     "mi_pack_ternary": [P, P, I, I, P],
     "mi_act_quant_f32": [P, P, P, I, I, P],
-    "mi_bitlinear": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P],
-    "mi_bitlinear_gemm": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P],
-    "mi_bitlinear_gemv": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P],
-    "mi_bitshift_norm": [P, P, P, I, I, P],
-    "mi_embed": [P, P, P, I, I, I, P],
+    "mi_bitlinear": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
+    "mi_bitlinear_gemm": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
+    "mi_bitlinear_gemv": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
+    "mi_bitshift_norm": [P, P, P, I, I, P, P],
+    "mi_embed": [P, P, P, I, I, I, P, I, P],
     "mi_conv_squareplus": [P, I, P, P, P, P, P, I, I, I, P],
     "mi_block_scan": [P, P, P, I, I, P, I, I, P, I, I, P, P, P, I, I, I, I, P],
     "mi_argmax_i32": [P, I, P, I, I, P],
+    "mi_norm_bitlinear": [P, P, P, P, P, I, I, I, I, I, I, P],
+    "mi_norm_in_proj_conv": [P, P, P, P, I, P, P, P, P, P, I, I, I, P],
+    "mi_dt_scan_step": [P, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
 }
 
 

@@ -66,6 +66,8 @@ class _Workspace:
         self.xp = torch.empty((T, dims.xp_width), dtype=torch.int8, device=device)
         self.dm = torch.empty((T, D), dtype=torch.int8, device=device)
         self.yo = torch.empty((T, D), dtype=torch.int8, device=device)
+        # row statistics (sum r, sum r^2) of the residual entering layer i (i = n_layer: the head)
+        self.stats = torch.empty((dims.n_layer + 1, T, 2), dtype=torch.int64, device=device)
 
 
 class IntegerMambaRunner:
@@ -92,6 +94,7 @@ class IntegerMambaRunner:
         # optional (before, after) callables around every fused scan launch
         # (the bench times that kernel with events on the launch stream)
         self.scan_timer = None
+        self._stats_valid = False
 
     # ------------------------------------------------------------ plumbing
     def _workspace(self, T: int) -> _Workspace:
@@ -109,11 +112,15 @@ class IntegerMambaRunner:
 
     # ---------------------------------------------------------------- layers
     def _layer(self, ly: DeviceLayer, ws: _Workspace, B: int, L: int, conv_state: torch.Tensor,
-               h_state: torch.Tensor, fresh: bool) -> None:
+               h_state: torch.Tensor, fresh: bool, stats_in: Optional[torch.Tensor],
+               stats_out: Optional[torch.Tensor]) -> None:
+        """A layer over [B, L] tokens (prefill).  stats_in: row statistics of ws.r
+        (None: the norm reduces the rows itself); stats_out: zeroed buffer that
+        receives the statistics of the updated residual (or None)."""
         dims = self.dims
         D, N, R, d = dims.d_inner, dims.d_state, dims.dt_rank, dims.d_model
         T = B * L
-        ops.bitshift_norm(ws.r, ly.gamma, out=ws.a)
+        ops.bitshift_norm(ws.r, ly.gamma, out=ws.a, row_stats=stats_in)
         ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
         ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
                             state_out=conv_state, out=ws.xs, batch=B)
@@ -127,18 +134,44 @@ class IntegerMambaRunner:
         if self.scan_timer is not None:
             self.scan_timer[1]()
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                      res_shift=ly.res_shift)
+                      res_shift=ly.res_shift, row_stats=stats_out)
 
-    def _head(self, r_rows: torch.Tensor) -> torch.Tensor:
-        a = ops.bitshift_norm(r_rows, self.gamma_f)
-        return ops.bitlinear(a, self.w_head, ops.OUT_INT32, self.dims.vocab_size)
+    def _fused_decode_ok(self, B: int) -> bool:
+        return B <= 16 and self.dims.d_model <= 3072 and self.dims.d_state <= 64 and self.dims.dt_rank <= 256
+
+    def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
+                      h_state: torch.Tensor, li: int) -> None:
+        """One token per sequence through a layer in four kernels (fused stages)."""
+        dims = self.dims
+        D, R, d = dims.d_inner, dims.dt_rank, dims.d_model
+        ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
+                              row_stats=ws.stats[li])
+        ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+        ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
+        ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                      res_shift=ly.res_shift, row_stats=ws.stats[li + 1])
+
+    def _head(self, r_rows: torch.Tensor, stats: Optional[torch.Tensor],
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if r_rows.shape[0] <= 16 and self.dims.d_model <= 3072:
+            return ops.norm_bitlinear(r_rows, self.gamma_f, self.w_head, ops.OUT_INT32, self.dims.vocab_size,
+                                      out=out, row_stats=stats)
+        a = ops.bitshift_norm(r_rows, self.gamma_f, row_stats=stats)
+        return ops.bitlinear(a, self.w_head, ops.OUT_INT32, self.dims.vocab_size, out=out)
 
     def _run(self, ids: torch.Tensor, state: DecodeState, fresh: bool) -> _Workspace:
         B, L = ids.shape
         ws = self._workspace(B * L)
-        ops.embed(ids.reshape(-1).contiguous(), self.emb, out=ws.r)
+        ops.embed(ids.reshape(-1).contiguous(), self.emb, out=ws.r, row_stats=ws.stats)
+        decode = L == 1 and not fresh and self._fused_decode_ok(B)
         for i, ly in enumerate(self.layers):
-            self._layer(ly, ws, B, L, state.conv[i], state.h[i], fresh)
+            if decode:
+                self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
+            else:
+                # prefill: the norm of layer 0 uses the embedding's row statistics; later
+                # norms reduce their rows (atomics over 16k-row tiles cost more than they save)
+                self._layer(ly, ws, B, L, state.conv[i], state.h[i], fresh, ws.stats[0] if i == 0 else None, None)
+        self._stats_valid = decode
         return ws
 
     # ------------------------------------------------------------ public API
@@ -148,7 +181,7 @@ class IntegerMambaRunner:
         B, L = ids.shape
         state = self.new_state(B)
         ws = self._run(ids, state, fresh=True)
-        return self._head(ws.r).view(B, L, -1)
+        return self._head(ws.r, ws.stats[-1] if self._stats_valid else None).view(B, L, -1)
 
     @torch.no_grad()
     def prefill(self, ids: torch.Tensor, state: Optional[DecodeState] = None
@@ -160,13 +193,14 @@ class IntegerMambaRunner:
             state = self.new_state(B)
         ws = self._run(ids, state, fresh=fresh)
         last = ws.r.view(B, L, -1)[:, -1, :].contiguous()
-        return self._head(last), state
+        last_stats = ws.stats[-1].view(B, L, 2)[:, -1, :].contiguous() if self._stats_valid else None
+        return self._head(last, last_stats), state
 
     @torch.no_grad()
     def decode_step(self, tokens: torch.Tensor, state: DecodeState) -> torch.Tensor:
         """One recurrent step for tokens [B] int64; updates `state` in place."""
         ws = self._run(tokens.view(-1, 1), state, fresh=False)
-        return self._head(ws.r)
+        return self._head(ws.r, ws.stats[-1] if self._stats_valid else None)
 
     @torch.no_grad()
     def generate(self, ids: torch.Tensor, n_new: int, use_graph: bool = True) -> torch.Tensor:
@@ -193,46 +227,49 @@ class IntegerMambaRunner:
         step = self._decode_graph(B, state)
         step.tok_in.copy_(tok)
         for i in range(1, n_new):
-            step.graph.replay()
-            out[:, i] = step.tok_out
-            step.tok_in.copy_(step.tok_out)
+            step.graph.replay()          # embed(tok) ... argmax -> tok
+            out[:, i] = step.tok_in
         # hand the state back to the caller's tensors
         for i in range(len(self.layers)):
             state.conv[i].copy_(step.state.conv[i])
             state.h[i].copy_(step.state.h[i])
         return out
 
+    def _decode_body(self, ws: _Workspace, state: DecodeState, tok: torch.Tensor, logits: torch.Tensor,
+                     tok_out: torch.Tensor) -> None:
+        """embed -> layers -> head -> argmax for one token per sequence (graph body)."""
+        B = tok.shape[0]
+        ops.embed(tok, self.emb, out=ws.r, row_stats=ws.stats)
+        fused = self._fused_decode_ok(B)
+        for i, ly in enumerate(self.layers):
+            if fused:
+                self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
+            else:
+                self._layer(ly, ws, B, 1, state.conv[i], state.h[i], False, ws.stats[i], ws.stats[i + 1])
+        self._head(ws.r, ws.stats[-1], out=logits)
+        ops.argmax(logits, out=tok_out)
+
     def _decode_graph(self, B: int, state: DecodeState):
         """Captures embed -> layers -> head -> argmax for batch B as one HIP graph."""
         g = self._graphs.get(B)
         if g is None:
-            tok_in = torch.zeros((B,), dtype=torch.int64, device=self.device)
+            tok_in = torch.zeros((B,), dtype=torch.int64, device=self.device)  # read by embed, rewritten by argmax
             gstate = self.new_state(B)
             # warm the workspaces outside capture (allocation happens here)
             ws = self._workspace(B)
-            head_a = torch.empty((B, self.dims.d_model), dtype=torch.int8, device=self.device)
             logits = torch.empty((B, self.dims.vocab_size), dtype=torch.int32, device=self.device)
-            tok_out = torch.empty((B,), dtype=torch.int64, device=self.device)
+            tok_out = tok_in
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
                 # one eager step first: every kernel is loaded before capture
-                ops.embed(tok_in, self.emb, out=ws.r)
-                for i, ly in enumerate(self.layers):
-                    self._layer(ly, ws, B, 1, gstate.conv[i], gstate.h[i], fresh=False)
-                ops.bitshift_norm(ws.r, self.gamma_f, out=head_a)
-                ops.bitlinear(head_a, self.w_head, ops.OUT_INT32, self.dims.vocab_size, out=logits)
-                ops.argmax(logits, out=tok_out)
+                self._decode_body(ws, gstate, tok_in, logits, tok_out)
+                tok_in.zero_()
             side.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.stream(side):
                 with torch.cuda.graph(graph, stream=side):
-                    ops.embed(tok_in, self.emb, out=ws.r)
-                    for i, ly in enumerate(self.layers):
-                        self._layer(ly, ws, B, 1, gstate.conv[i], gstate.h[i], fresh=False)
-                    ops.bitshift_norm(ws.r, self.gamma_f, out=head_a)
-                    ops.bitlinear(head_a, self.w_head, ops.OUT_INT32, self.dims.vocab_size, out=logits)
-                    ops.argmax(logits, out=tok_out)
+                    self._decode_body(ws, gstate, tok_in, logits, tok_out)
             torch.cuda.current_stream().wait_stream(side)
 
             class _G:

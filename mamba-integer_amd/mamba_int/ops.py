@@ -117,7 +117,8 @@ _ENTRY = {"auto": "mi_bitlinear", "gemm": "mi_bitlinear_gemm", "gemv": "mi_bitli
 def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Optional[int] = None,
               shift: int = 0, out: Optional[torch.Tensor] = None, res_mult: int = 0, res_shift: int = 0,
               x_scale: Optional[torch.Tensor] = None, w_scale: float = 0.0, path: str = "auto",
-              lda: Optional[int] = None, m: Optional[int] = None) -> torch.Tensor:
+              lda: Optional[int] = None, m: Optional[int] = None,
+              row_stats: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out = kind(a[:, :k] @ W^T).  a int8 [m, lda] (a row-strided view is passed by
     its storage with ``lda``); RESIDUAL updates ``out`` (int32 [m, n]) in place."""
     if a.dtype != torch.int8 or not a.is_cuda:
@@ -137,25 +138,30 @@ def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Opt
     _req(out, _OUT_DTYPE[kind], "out")
     _lib.call(_ENTRY[path], _ptr(a), lda, _ptr(w_packed), _ptr(out), out.shape[-1], kind, m, n, k,
               shift, int(res_mult), res_shift, _ptr(_opt(x_scale, torch.float32, "x_scale")),
-              ctypes.c_float(w_scale), _stream())
+              ctypes.c_float(w_scale), _ptr(_opt(row_stats, torch.int64, "row_stats")), _stream())
     return out
 
 
 # ---------------------------------------------------------------- block ops
-def bitshift_norm(r: torch.Tensor, gamma: torch.Tensor, out=None) -> torch.Tensor:
+def bitshift_norm(r: torch.Tensor, gamma: torch.Tensor, out=None, row_stats=None) -> torch.Tensor:
     _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma")
     T, d = r.shape
     o = out if out is not None else torch.empty((T, d), dtype=torch.int8, device=r.device)
-    _lib.call("mi_bitshift_norm", _ptr(r), _ptr(gamma), _ptr(o), T, d, _stream())
+    _lib.call("mi_bitshift_norm", _ptr(r), _ptr(gamma), _ptr(o), T, d,
+              _ptr(_opt(row_stats, torch.int64, "row_stats")), _stream())
     return o
 
 
-def embed(ids: torch.Tensor, emb: torch.Tensor, out=None) -> torch.Tensor:
+def embed(ids: torch.Tensor, emb: torch.Tensor, out=None, row_stats=None) -> torch.Tensor:
+    """r = emb[ids] << 4; with row_stats (int64 [layers, T, 2]) also the row
+    statistics of r into layer 0 and zeros into the other layers."""
     _req(ids, torch.int64, "ids"); _req(emb, torch.int8, "emb")
     V, d = emb.shape
     T = ids.numel()
     r = out if out is not None else torch.empty((T, d), dtype=torch.int32, device=ids.device)
-    _lib.call("mi_embed", _ptr(ids), _ptr(emb), _ptr(r), T, d, V, _stream())
+    layers = 0 if row_stats is None else row_stats.shape[0]
+    _lib.call("mi_embed", _ptr(ids), _ptr(emb), _ptr(r), T, d, V,
+              _ptr(_opt(row_stats, torch.int64, "row_stats")), layers, _stream())
     return r
 
 
@@ -195,3 +201,41 @@ def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
     o = out if out is not None else torch.empty((rows,), dtype=torch.int64, device=logits.device)
     _lib.call("mi_argmax_i32", _ptr(logits), cols, _ptr(o), rows, cols, _stream())
     return o
+
+
+# ------------------------------------------------------ fused decode stages
+def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int,
+                   shift: int = 0, out=None, row_stats=None) -> torch.Tensor:
+    """BitShiftNorm of r (int32 [m, k], m <= 16) fused into the BitLinear GEMV (INT8 or INT32 out)."""
+    _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma"); _req(w_packed, torch.uint8, "w_packed")
+    m, k = r.shape
+    o = out if out is not None else torch.empty((m, n), dtype=_OUT_DTYPE[kind], device=r.device)
+    _req(o, _OUT_DTYPE[kind], "out")
+    _lib.call("mi_norm_bitlinear", _ptr(r), _ptr(_opt(row_stats, torch.int64, "row_stats")), _ptr(gamma),
+              _ptr(w_packed), _ptr(o), o.shape[-1], kind, m, n, k, shift, _stream())
+    return o
+
+
+def norm_in_proj_conv(r, gamma, w_in, s_in: int, conv_w, conv_b, conv_state, xs, xz, row_stats=None) -> None:
+    """Decode stage: norm + in_proj GEMV + conv step + squareplus (x half -> xs, conv_state
+    updated in place), z half -> xz[:, d_inner:]."""
+    _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma"); _req(w_in, torch.uint8, "w_in")
+    _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
+    _req(conv_state, torch.int8, "conv_state"); _req(xs, torch.int8, "xs"); _req(xz, torch.int8, "xz")
+    m, d = r.shape
+    D = conv_w.shape[0]
+    _lib.call("mi_norm_in_proj_conv", _ptr(r), _ptr(_opt(row_stats, torch.int64, "row_stats")), _ptr(gamma),
+              _ptr(w_in), s_in, _ptr(conv_w), _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), m, d, D,
+              _stream())
+
+
+def dt_scan_step(xp, dt_rank: int, w_dt, s_dt: int, xs, z, z_off: int, base, decay_shift: int, s_y: int,
+                 h_state, yo) -> None:
+    """Decode stage: dt_proj + decay + dt + scan state update + y + gate + requant -> yo."""
+    for t, nm in ((xp, "xp"), (xs, "xs"), (z, "z"), (yo, "yo")):
+        _req(t, torch.int8, nm)
+    _req(w_dt, torch.uint8, "w_dt"); _req(base, torch.int32, "base"); _req(h_state, torch.int32, "h_state")
+    m = xs.shape[0]
+    D, N = base.shape
+    _lib.call("mi_dt_scan_step", _ptr(xp), xp.shape[-1], dt_rank, _ptr(w_dt), s_dt, _ptr(xs), _ptr(z),
+              z.shape[-1], z_off, _ptr(base), decay_shift, s_y, _ptr(h_state), _ptr(yo), m, D, N, _stream())

@@ -99,7 +99,7 @@ class MambaIntegerBlock(nn.Module):
         ws = run._workspace(B * L)
         ws.r.copy_(hidden_states.reshape(B * L, d))
         st = run.new_state(B)
-        run._layer(run.layers[0], ws, B, L, st.conv[0], st.h[0], fresh=True)
+        run._layer(run.layers[0], ws, B, L, st.conv[0], st.h[0], True, None, None)
         return ws.r.clone().view(B, L, d)
 
 

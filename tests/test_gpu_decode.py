@@ -1,0 +1,112 @@
+"""GPU parity of the fused decode stages against the unfused oracle ops."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import i8
+
+pytestmark = pytest.mark.gpu
+
+
+def T(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def H(t):
+    return t.cpu().numpy()
+
+
+def _resid(rng, m, d):
+    r = rng.integers(-(2**23) + 1, 2**23, size=(m, d), dtype=np.int32)
+    r[0] >>= 10
+    return r
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 80, 64), (8, 3072, 768), (16, 300, 256), (5, 32000, 768), (8, 64, 3072)])
+def test_norm_bitlinear(cuda, m, n, k):
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m + n + k)
+    r = _resid(rng, m, k)
+    g = rng.integers(100, 400, size=k, dtype=np.int16)
+    wp = pack_ternary(rng.integers(-1, 2, size=(n, k), dtype=np.int8))
+    a = O.bitshift_norm(r, g)
+    got = H(ops.norm_bitlinear(T(r), T(g), T(wp), ops.OUT_INT32, n))
+    assert np.array_equal(got, O.bitlinear(a, wp, O.OUT_INT32))
+    got8 = H(ops.norm_bitlinear(T(r), T(g), T(wp), ops.OUT_INT8, n, shift=4))
+    assert np.array_equal(got8, O.bitlinear(a, wp, O.OUT_INT8, 4))
+
+
+@pytest.mark.parametrize("m,d,D", [(8, 768, 1536), (1, 128, 256), (16, 256, 512)])
+def test_norm_in_proj_conv(cuda, m, d, D):
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m * d + D)
+    r = _resid(rng, m, d)
+    g = np.full(d, 256, np.int16)
+    wp = pack_ternary(rng.integers(-1, 2, size=(2 * D, d), dtype=np.int8))
+    cw = i8(rng, D, 4)
+    cb = rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, m, 3, D)
+    xz_ref = O.bitlinear(O.bitshift_norm(r, g), wp, O.OUT_INT8, 4)
+    xs_ref, st_ref = O.conv_squareplus(xz_ref.reshape(m, 1, 2 * D), D, cw, cb, st)
+    stg = T(st)
+    xs = torch.zeros((m, D), dtype=torch.int8, device="cuda")
+    xz = torch.zeros((m, 2 * D), dtype=torch.int8, device="cuda")
+    ops.norm_in_proj_conv(T(r), T(g), T(wp), 4, T(cw), T(cb), stg, xs, xz)
+    assert np.array_equal(H(xs), xs_ref[:, 0])
+    assert np.array_equal(H(stg), st_ref)
+    assert np.array_equal(H(xz)[:, D:], xz_ref[:, D:])
+
+
+@pytest.mark.parametrize("m,D,N,R", [(8, 1536, 16, 48), (1, 256, 16, 16), (16, 512, 32, 32), (3, 100, 8, 16)])
+def test_dt_scan_step(cuda, m, D, N, R):
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m + D + N + R)
+    W = (R + 2 * N + 15) // 16 * 16
+    xp = i8(rng, m, W)
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    xs = rng.integers(0, 128, size=(m, D), dtype=np.int8)
+    z = i8(rng, m, 2 * D, lo=-128)
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    h0 = rng.integers(-(2**22), 2**22, size=(m, D, N), dtype=np.int32)
+    dm = O.bitlinear(np.ascontiguousarray(xp[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs.reshape(m, 1, D), dm.reshape(m, 1, D), xp.reshape(m, 1, W), R,
+                                 z.reshape(m, 1, 2 * D), D, base, 15, 13, h_state=h0)
+    hg = T(h0)
+    yo = T(np.zeros((m, D), np.int8))
+    ops.dt_scan_step(T(xp), R, T(wdt), 2, T(xs), T(z), D, T(base), 15, 13, hg, yo)
+    assert np.array_equal(H(yo), yo_ref[:, 0])
+    assert np.array_equal(H(hg), h_ref)
+
+
+def test_row_stats_paths(cuda):
+    """Embed row statistics, the RESIDUAL epilogue's atomics (GEMV and GEMM) and
+    the stats-driven norms equal the reducing norm."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(17)
+    V, d, D = 300, 256, 512
+    emb = i8(rng, V, d)
+    for T_ in (8, 300):
+        ids = rng.integers(0, V, size=T_).astype(np.int64)
+        stats = torch.full((3, T_, 2), 7, dtype=torch.int64, device="cuda")
+        r = ops.embed(T(ids), T(emb), row_stats=stats)
+        r0 = H(r).astype(np.int64)
+        assert np.array_equal(H(stats[0]), np.stack([r0.sum(1), (r0 * r0).sum(1)], 1))
+        assert not H(stats[1:]).any()
+        a = i8(rng, T_, D)
+        wp = pack_ternary(rng.integers(-1, 2, size=(d, D), dtype=np.int8))
+        ops.bitlinear(T(a), T(wp), ops.OUT_RESIDUAL, d, out=r, res_mult=4719, res_shift=16, row_stats=stats[1])
+        r1 = H(r).astype(np.int64)
+        assert np.array_equal(r1, O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0.astype(np.int32), res_mult=4719,
+                                              res_shift=16))
+        assert np.array_equal(H(stats[1]), np.stack([r1.sum(1), (r1 * r1).sum(1)], 1))
+        g = rng.integers(100, 400, size=d, dtype=np.int16)
+        ref = O.bitshift_norm(r1.astype(np.int32), g)
+        assert np.array_equal(H(ops.bitshift_norm(r, T(g), row_stats=stats[1])), ref)
+        assert np.array_equal(H(ops.bitshift_norm(r, T(g))), ref)
+        if T_ <= 16:
+            wh = pack_ternary(rng.integers(-1, 2, size=(40, d), dtype=np.int8))
+            got = H(ops.norm_bitlinear(r, T(g), T(wh), ops.OUT_INT32, 40, row_stats=stats[1]))
+            assert np.array_equal(got, O.bitlinear(ref, wh, O.OUT_INT32))
