@@ -1,0 +1,97 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+that include/mamba_int.h declares, and rejects bad arguments before anything
+is enqueued (no call here reaches the device)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO, PKG
+
+HEADER = os.path.join(REPO, "include", "mamba_int.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:mi_status|const char \*)\s*(mi_\w+)\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "mi_dyadic_scan" in names and "mi_bitlinear" in names and len(names) >= 18
+
+
+def test_library_exports_every_declared_symbol():
+    from mamba_int import _lib
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), name
+    bound = set(_lib.SIGNATURES) | {"mi_version", "mi_last_error_string"}
+    assert set(declared()) == bound
+
+
+def test_version_names_spec_and_arch():
+    from mamba_int import _lib
+    v = _lib.version()
+    assert "mi-spec-1" in v and "gfx950" in v
+
+
+def _fake(n=64):
+    return ctypes.c_void_p(0x100000)  # never dereferenced: every call below fails validation
+
+
+@pytest.mark.parametrize("call,status,needle", [
+    (("mi_dyadic_scan", None, None, None, None, 15, None, None, None, 1, 4, 16, 0, None), 2, "nstate"),
+    (("mi_dyadic_scan", None, None, None, None, 0, None, None, None, 1, 4, 16, 16, None), 4, "decay_shift"),
+    (("mi_dyadic_scan", None, None, None, None, 15, None, None, None, 1, 4, 16, 16, None), 1, "required"),
+    (("mi_ssd_chunked_scan", None, None, None, None, 15, None, None, None, None, 1, 8, 2, 16, 16, 0, None), 4, "chunk"),
+    (("mi_bitlinear", None, 16, None, None, 16, 1, 4, 4, 17, 0, 0, 0, None, ctypes.c_float(0), None, None), 2, "multiple of 16"),
+    (("mi_bitlinear", None, 16, None, None, 16, 9, 4, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 4, "kind"),
+    (("mi_bitlinear_gemv", "A16", 16, "W4", "O16", 16, 1, 100, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 2, "m <= 64"),
+    (("mi_bitlinear", "A16", 8, "W4", "O16", 16, 1, 4, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 3, "lda"),
+    (("mi_bitlinear", "A16", 16, "W4", "O16", 16, 4, 4, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 1, "x_scale"),
+    (("mi_bitshift_norm", None, None, None, 4, 0, None, None), 2, "dim"),
+    (("mi_conv_squareplus", None, 16, None, None, None, None, None, 1, 4, 18, None), 2, "multiple of 4"),
+    (("mi_block_scan", None, None, None, 48, 16, None, 32, 16, None, 14, 13, None, None, None, 1, 4, 16, 16, None), 4, "decay_shift"),
+    (("mi_norm_bitlinear", None, None, None, None, None, 16, 1, 17, 16, 64, 0, None), 2, "m=17"),
+    (("mi_dt_scan_step", None, 80, 40, None, 2, None, None, 32, 16, None, 15, 13, None, None, 1, 16, 16, None), 2, "dt_rank"),
+    (("mi_argmax_i32", None, 10, None, 1, 20, None), 2, "ld"),
+])
+def test_argument_validation(call, status, needle):
+    from mamba_int import _lib
+    args = []
+    for a in call[1:]:
+        if a == "A16" or a == "O16":
+            args.append(ctypes.c_void_p(0x100000))
+        elif a == "W4":
+            args.append(ctypes.c_void_p(0x100004))
+        else:
+            args.append(a)
+    st = _lib.raw(call[0], *args)
+    assert st == status, (_lib.last_error(), st)
+    assert needle in _lib.last_error()
+
+
+def test_zero_sizes_are_noops():
+    from mamba_int import _lib
+    assert _lib.raw("mi_dyadic_scan", None, None, None, None, 15, None, None, None, 0, 4, 16, 16, None) == 0
+    assert _lib.raw("mi_bitlinear", None, 16, None, None, 16, 1, 0, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None,
+                    None) == 0
+    assert _lib.last_error() == ""
+
+
+def test_ops_reject_host_tensors():
+    import torch
+    from mamba_int import ops
+    with pytest.raises(ValueError):
+        ops.bitshift_norm(torch.zeros(2, 16, dtype=torch.int32), torch.zeros(16, dtype=torch.int16))
+
+
+def test_product_does_not_import_the_oracle():
+    for root, _, files in os.walk(PKG):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(root, f)).read()
+                assert not re.search(r"^\s*(import|from)\s+oracle", src, flags=re.M), f
+                assert "liboracle" not in src, f
