@@ -176,7 +176,8 @@ mi_status mi_conv_squareplus(const int8_t *xz, int xz_stride, const int8_t *conv
  * columns [b_off, b_off+nstate) and C at [b_off+nstate, b_off+2*nstate);
  * z int8 [batch,len,z_stride] at column z_off; base int32 [d_inner,nstate] in
  * [0,32000]; yo int8 [batch,len,d_inner]; h_in / h_out int32
- * [batch,d_inner,nstate] nullable.  decay_shift == 15; nstate in [1,64]. */
+ * [batch,d_inner,nstate] nullable.  decay_shift == 15; nstate in [1,64];
+ * s_y in [0,30]. */
 mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int8_t *xp, int xp_stride,
                         int b_off, const int8_t *z, int z_stride, int z_off,
                         const int32_t *base, int decay_shift, int s_y, int8_t *yo,

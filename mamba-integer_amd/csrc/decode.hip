@@ -357,7 +357,7 @@ extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_ran
     MI_REQUIRE(dt_rank + 2 * nstate <= xp_stride, MI_ERR_BAD_DIM, "mi_dt_scan_step: xp_stride=%d too small", xp_stride);
     MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride, MI_ERR_BAD_DIM, "mi_dt_scan_step: z columns exceed z_stride");
     MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG, "mi_dt_scan_step: decay_shift outside [1,30]");
-    MI_REQUIRE(s_dt >= 0 && s_dt <= 30 && s_y >= 0 && s_y <= 40, MI_ERR_BAD_ARG, "mi_dt_scan_step: shift out of range");
+    MI_REQUIRE(s_dt >= 0 && s_dt <= 30 && s_y >= 0 && s_y <= 30, MI_ERR_BAD_ARG, "mi_dt_scan_step: shift out of range");
     if ((int64_t)m * d_inner == 0) return MI_OK;
     MI_REQUIRE(xp && w_dt && xs && z && base && h_state && yo, MI_ERR_NULL_POINTER,
                "mi_dt_scan_step: a required pointer is NULL");

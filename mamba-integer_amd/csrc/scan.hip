@@ -453,6 +453,11 @@ __global__ __launch_bounds__(256) void scan_elem_kernel(const int32_t *u, const 
 }
 
 }  // namespace
+
+hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z, const int8_t *bsrc,
+                             const int8_t *csrc, const int32_t *base, int8_t *yo, const int32_t *h_in, int32_t *h_out,
+                             int64_t x_row, int64_t z_row, int64_t bc_row, int B, int L, int D, int N, int s_y,
+                             hipStream_t st);
 }  // namespace mi
 
 using namespace mi;
@@ -514,7 +519,7 @@ extern "C" mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int
     MI_REQUIRE(batch >= 0 && len >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_block_scan: negative size");
     MI_REQUIRE(nstate >= 1 && nstate <= 64, MI_ERR_BAD_DIM, "mi_block_scan: nstate=%d outside [1,64]", nstate);
     MI_REQUIRE(decay_shift == 15, MI_ERR_BAD_ARG, "mi_block_scan: decay_shift=%d, the model path uses 15", decay_shift);
-    MI_REQUIRE(s_y >= 0 && s_y <= 40, MI_ERR_BAD_ARG, "mi_block_scan: s_y=%d outside [0,40]", s_y);
+    MI_REQUIRE(s_y >= 0 && s_y <= 30, MI_ERR_BAD_ARG, "mi_block_scan: s_y=%d outside [0,30]", s_y);
     MI_REQUIRE(b_off >= 0 && b_off + 2 * nstate <= xp_stride, MI_ERR_BAD_DIM,
                "mi_block_scan: B/C columns [%d,%d) exceed xp_stride=%d", b_off, b_off + 2 * nstate, xp_stride);
     MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride, MI_ERR_BAD_DIM,
@@ -530,7 +535,12 @@ extern "C" mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int
     const bool fast = len > 0 && fast_shape(nstate, d_inner, decay_shift, kModeModel) && aligned(xs, 16) && aligned(dm, 16) &&
                       aligned(a.z, 16) && aligned(a.bsrc, 16) && aligned(a.csrc, 16) && aligned(yo, 16) &&
                       xp_stride % 16 == 0 && z_stride % 16 == 0;
-    hipError_t e = launch_scan<kModeModel>(a, nstate, fast, as_stream(stream));
+    hipError_t e;
+    if (fast && nstate != 128 && !getenv("MI_MODEL_SCAN_V1"))
+        e = launch_model_scan(xs, dm, a.z, a.bsrc, a.csrc, base, yo, h_in, h_out, d_inner, z_stride, xp_stride, batch,
+                              len, d_inner, nstate, s_y, as_stream(stream));
+    else
+        e = launch_scan<kModeModel>(a, nstate, fast, as_stream(stream));
     if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_block_scan: launch failed: %s", hipGetErrorString(e));
     return MI_OK;
 }
