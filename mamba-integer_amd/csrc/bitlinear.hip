@@ -106,8 +106,11 @@ constexpr int kBM = 128, kBN = 128, kBK = 128;
 constexpr int kApitch = kBK + 16;       // bytes per staged activation row (bank-conflict free b128 reads)
 constexpr int kWpitch = kBK / 16 + 4;   // words per staged weight row (conflict free b32 reads)
 
+// Three blocks (12 waves) per CU: 768 blocks of the 4096 x 3072 x 768 problem
+// then run in one round and each block's global-load latency hides behind the
+// other two blocks' MFMA work.
 template <int KIND>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemm_kernel(GemmArgs g) {
     __shared__ __align__(16) int8_t sA[2][kBM * kApitch];
     __shared__ __align__(16) uint32_t sW[2][kBN * kWpitch];
 
@@ -193,6 +196,131 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
             st.s2 += e.s2;
         }
         if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
+    }
+}
+
+// ------------------------------------------------ prefill GEMM, 32x32 MFMA
+// v_mfma_i32_32x32x32_i8 sustains more of the int8 rate than the 16x16x64
+// form.  Operands: lane l holds 16 consecutive k (group l/32) of row l%32 in
+// both A (weights) and B (tokens); result register r of lane l is
+// (n = 8*(r/4) + 4*(l/32) + r%4, m = l%32), so registers 4q..4q+3 are four
+// consecutive features of one token.  Block tile 128(n) x 128(m), 4 waves of
+// 64x64 (2x2 MFMAs per 32-wide k step), K staged 128 at a time, packed
+// weights kept packed in LDS (pitch 10 words: conflict-free b32 reads by 32
+// rows x 2 k-groups).
+typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int kW32pitch = kBK / 16 + 2;
+
+__device__ __forceinline__ void flush_row_stat32(const GemmArgs &g, RowStat st, int m, int lh) {
+    st.s1 += __shfl_xor(st.s1, 32);
+    st.s2 += __shfl_xor(st.s2, 32);
+    if (lh == 0 && m < g.M) {
+        atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m), (unsigned long long)st.s1);
+        atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m + 1), (unsigned long long)st.s2);
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemm32_kernel(GemmArgs g) {
+    __shared__ __align__(16) int8_t sA[2][kBM * kApitch];
+    __shared__ __align__(16) uint32_t sW[2][kBN * kW32pitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    const int mtiles = (g.M + kBM - 1) / kBM;
+    const int m0 = (blockIdx.x % mtiles) * kBM;
+    const int n0 = (blockIdx.x / mtiles) * kBN;
+
+    uint4 ra[4];
+    uint32_t rw[4];
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            const int row = i >> 3, c16 = i & 7;
+            const int m = m0 + row, k = k0 + c16 * 16;
+            ra[j] = (m < g.M && k < g.K) ? *reinterpret_cast<const uint4 *>(g.a + (int64_t)m * g.lda + k)
+                                         : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            const int row = i >> 3, c = i & 7;
+            const int n = n0 + row, kw = (k0 >> 4) + c;
+            rw[j] = (n < g.N && kw < g.kw) ? g.w[(int64_t)n * g.kw + kw] : 0u;
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            const int row = i >> 3, c16 = i & 7;
+            *reinterpret_cast<uint4 *>(&sA[buf][row * kApitch + c16 * 16]) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = tid + 256 * j;
+            const int row = i >> 3, c = i & 7;
+            sW[buf][row * kW32pitch + c] = rw[j];
+        }
+    };
+
+    v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int nk = (g.K + kBK - 1) / kBK;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
+#pragma unroll
+        for (int ks = 0; ks < kBK / 32; ++ks) {
+            v4i fw[2], fa[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = wn * 64 + i * 32 + l32;
+                fw[i] = unpack16(sW[buf][row * kW32pitch + ks * 2 + lh]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int row = wm * 64 + j * 32 + l32;
+                fa[j] = *reinterpret_cast<const v4i *>(&sA[buf][row * kApitch + ks * 32 + lh * 16]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[i], fa[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int m = m0 + wm * 64 + j * 32 + l32;
+        RowStat st{0, 0};
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v4i v = v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                const RowStat e = store4<KIND>(g, m, n0 + wn * 64 + i * 32 + 8 * q + 4 * lh, v);
+                st.s1 += e.s1;
+                st.s2 += e.s2;
+            }
+        if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat32(g, st, m, lh);
     }
 }
 
@@ -354,7 +482,10 @@ GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ld
 template <int KIND>
 hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
     const int blocks = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);
-    hipLaunchKernelGGL(gemm_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
+    if (getenv("MI_GEMM16"))
+        hipLaunchKernelGGL(gemm_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL(gemm32_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
     return hipGetLastError();
 }
 
