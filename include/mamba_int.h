@@ -227,6 +227,16 @@ mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const ui
                           int decay_shift, int s_y, int32_t *h_state, int8_t *yo, int m, int d_inner,
                           int nstate, void *stream);
 
+/* x_proj (INT8, shift s_x) fused in front of mi_dt_scan_step: each block
+ * computes the dt_rank + 2*nstate x_proj outputs of its token from xs int8
+ * [m,d_inner] (16-byte aligned) and w_x packed [dt_rank+2*nstate,
+ * d_inner/4] (8-byte aligned), then runs the dt_proj + scan step + gate of
+ * mi_dt_scan_step.  dt_rank + 2*nstate <= 256; d_inner % 32 == 0. */
+mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x, int s_x, int dt_rank,
+                                const uint8_t *w_dt, int s_dt, const int8_t *z, int z_stride, int z_off,
+                                const int32_t *base, int decay_shift, int s_y, int32_t *h_state,
+                                int8_t *yo, int m, int d_inner, int nstate, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -191,6 +191,8 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
 struct DtScanArgs {
     const int8_t *xp;       // [M][xp_stride]: dt_raw at [0,R), B at [R,R+N), C at [R+N,R+2N)
     int64_t xp_stride;
+    const uint32_t *w_x;    // fused x_proj: [R+2N][D/16] words (xp unused)
+    int s_x;
     int R;
     const uint32_t *w_dt;   // [D][R/16] words
     int s_dt;
@@ -206,13 +208,76 @@ struct DtScanArgs {
 
 constexpr int kMaxR = 256;
 constexpr int kMaxN = 64;
+constexpr int kMaxXTiles = 16;   // fused x_proj: R + 2N <= 256
 
 // Thread quad per channel: lane g of the quad keeps states g, g+4, g+8, ...;
 // every lane computes the channel's dt_proj dot (48-wide at d768), the quad
 // sums y with two DPP adds, lane 0 gates and writes.
+// x_proj outputs of token m (the block's own copy): 16x16x64 MFMA with the
+// ternary rows as the A operand and the token in column 0 of B (the other
+// columns zero).  Each of the 16 lane groups (4 waves x 4 k-groups) owns a
+// contiguous run of packed words, so every lane reads 8-byte pairs of words
+// of its row and all loads of a chunk are issued before the first MFMA; the
+// word -> k-group assignment is the same for A and B, so the dot products are
+// unchanged.  Column-0 lanes leave per-wave partial sums in s_xacc.
+template <int NT>
+__device__ __forceinline__ void xproj_token(const DtScanArgs &g, int m, int32_t (*s_xacc)[16 * kMaxXTiles]) {
+    constexpr int CW = (64 / NT) >= 8 ? 8 : ((64 / NT) & ~1);
+    static_assert(CW >= 2 && CW % 2 == 0, "chunk of word pairs");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int NX = g.R + 2 * g.N;
+    const int kwx = g.D / 16;               // even: d_inner % 32 == 0
+    const int wpg = 2 * ((kwx + 31) / 32);  // words per lane group, even
+    const int w0 = (wave * 4 + lq) * wpg;
+    const int w1 = min(w0 + wpg, kwx);
+    const int8_t *xrow = g.xs + (int64_t)m * g.D;
+    v4i acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
+    // the trip count is the same for every lane (MFMA reads all 64 lanes, so
+    // no lane may skip it); words past a group's run load as zeros
+    for (int c0 = 0; c0 < wpg; c0 += CW) {
+        uint2 wv[NT][CW / 2];
+        v4i fa[CW];
+#pragma unroll
+        for (int p = 0; p < CW / 2; ++p) {
+            const int w = w0 + c0 + 2 * p;
+            const bool ok = w < w1;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int n = 16 * t + l16;
+                wv[t][p] = (ok && n < NX) ? *reinterpret_cast<const uint2 *>(g.w_x + (int64_t)n * kwx + w)
+                                          : make_uint2(0u, 0u);
+            }
+            const bool xa = ok && l16 == 0;
+            fa[2 * p] = xa ? *reinterpret_cast<const v4i *>(xrow + 16 * w) : v4i{0, 0, 0, 0};
+            fa[2 * p + 1] = xa ? *reinterpret_cast<const v4i *>(xrow + 16 * w + 16) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int p = 0; p < CW / 2; ++p)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = mfma_i8(unpack16(wv[t][p].x), fa[2 * p], acc[t]);
+                acc[t] = mfma_i8(unpack16(wv[t][p].y), fa[2 * p + 1], acc[t]);
+            }
+    }
+    // column-0 lanes (l16 == 0) hold features 16t + 4lq + r
+    if (l16 == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s_xacc[wave][16 * t + 4 * lq + r] = acc[t][r];
+    }
+}
+
+// XNT > 0: the block first computes the x_proj outputs of its token itself
+// (XNT tiles of 16 features, the x_proj weights come from L2), so the
+// separate x_proj GEMV kernel and its launch leave the decode chain.
+template <int XNT>
 __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_dt[kMaxR];
     __shared__ int8_t s_bc[2 * kMaxN];
+    __shared__ int32_t s_xacc[XNT ? 4 : 1][XNT ? 16 * kMaxXTiles : 1];
     constexpr int kPerLane = kMaxN / 4;
     const int m = blockIdx.y;
     const int q = threadIdx.x & 3;
@@ -236,9 +301,21 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     const int xsv = g.xs[(int64_t)m * g.D + dd];
     const int zv = g.z[(int64_t)m * g.z_stride + dd];
 
-    const int8_t *row = g.xp + (int64_t)m * g.xp_stride;
-    for (int i = threadIdx.x; i < g.R; i += 256) s_dt[i] = row[i];
-    for (int i = threadIdx.x; i < 2 * g.N; i += 256) s_bc[i] = row[g.R + i];
+    if constexpr (XNT > 0) {
+        xproj_token<XNT>(g, m, s_xacc);
+        __syncthreads();
+        const int NX = g.R + 2 * g.N;
+        for (int i = threadIdx.x; i < NX; i += 256) {
+            const int v = s_xacc[0][i] + s_xacc[1][i] + s_xacc[2][i] + s_xacc[3][i];
+            const int8_t q8 = (int8_t)clamp32(rshr32(v, g.s_x), -127, 127);
+            if (i < g.R) s_dt[i] = q8;
+            else s_bc[i - g.R] = q8;
+        }
+    } else {
+        const int8_t *row = g.xp + (int64_t)m * g.xp_stride;
+        for (int i = threadIdx.x; i < g.R; i += 256) s_dt[i] = row[i];
+        for (int i = threadIdx.x; i < 2 * g.N; i += 256) s_bc[i] = row[g.R + i];
+    }
     __syncthreads();
 
     int acc = 0;
@@ -366,7 +443,51 @@ extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_ran
     g.xp = xp; g.xp_stride = xp_stride; g.R = dt_rank; g.w_dt = reinterpret_cast<const uint32_t *>(w_dt); g.s_dt = s_dt;
     g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
-    hipLaunchKernelGGL(dt_scan_step_kernel, dim3((unsigned)((d_inner + 63) / 64), (unsigned)m), dim3(256), 0,
+    hipLaunchKernelGGL(dt_scan_step_kernel<0>, dim3((unsigned)((d_inner + 63) / 64), (unsigned)m), dim3(256), 0,
                        as_stream(stream), g);
     return check_launch("mi_dt_scan_step");
+}
+
+extern "C" mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x, int s_x, int dt_rank,
+                                           const uint8_t *w_dt, int s_dt, const int8_t *z, int z_stride, int z_off,
+                                           const int32_t *base, int decay_shift, int s_y, int32_t *h_state,
+                                           int8_t *yo, int m, int d_inner, int nstate, void *stream) {
+    clear_error();
+    MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_xproj_dt_scan_step: negative size");
+    MI_REQUIRE(d_inner % 32 == 0, MI_ERR_BAD_DIM, "mi_xproj_dt_scan_step: d_inner=%d must be a multiple of 32",
+               d_inner);
+    MI_REQUIRE(dt_rank >= 16 && dt_rank % 16 == 0 && dt_rank <= kMaxR, MI_ERR_BAD_DIM,
+               "mi_xproj_dt_scan_step: dt_rank=%d must be a multiple of 16 in [16,%d]", dt_rank, kMaxR);
+    MI_REQUIRE(nstate >= 1 && nstate <= kMaxN, MI_ERR_BAD_DIM, "mi_xproj_dt_scan_step: nstate=%d outside [1,%d]",
+               nstate, kMaxN);
+    MI_REQUIRE(dt_rank + 2 * nstate <= 16 * kMaxXTiles, MI_ERR_BAD_DIM,
+               "mi_xproj_dt_scan_step: dt_rank + 2*nstate = %d exceeds %d", dt_rank + 2 * nstate, 16 * kMaxXTiles);
+    MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride, MI_ERR_BAD_DIM,
+               "mi_xproj_dt_scan_step: z columns exceed z_stride");
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG, "mi_xproj_dt_scan_step: decay_shift outside [1,30]");
+    MI_REQUIRE(s_x >= 0 && s_x <= 30 && s_dt >= 0 && s_dt <= 30 && s_y >= 0 && s_y <= 30, MI_ERR_BAD_ARG,
+               "mi_xproj_dt_scan_step: shift out of range");
+    if ((int64_t)m * d_inner == 0) return MI_OK;
+    MI_REQUIRE(xs && w_x && w_dt && z && base && h_state && yo, MI_ERR_NULL_POINTER,
+               "mi_xproj_dt_scan_step: a required pointer is NULL");
+    MI_REQUIRE(aligned(xs, 16) && aligned(w_x, 8) && aligned(w_dt, 4), MI_ERR_BAD_ALIGNMENT,
+               "mi_xproj_dt_scan_step: xs must be 16-byte aligned, w_x 8-byte and w_dt 4-byte aligned");
+    DtScanArgs g{};
+    g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.s_x = s_x; g.R = dt_rank;
+    g.w_dt = reinterpret_cast<const uint32_t *>(w_dt); g.s_dt = s_dt;
+    g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
+    g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
+    const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
+    hipStream_t hs = as_stream(stream);
+    const int ntiles = (dt_rank + 2 * nstate + 15) / 16;
+    if (ntiles <= 2) hipLaunchKernelGGL(dt_scan_step_kernel<2>, grid, dim3(256), 0, hs, g);
+    else if (ntiles == 3) hipLaunchKernelGGL(dt_scan_step_kernel<3>, grid, dim3(256), 0, hs, g);
+    else if (ntiles == 4) hipLaunchKernelGGL(dt_scan_step_kernel<4>, grid, dim3(256), 0, hs, g);
+    else if (ntiles == 5) hipLaunchKernelGGL(dt_scan_step_kernel<5>, grid, dim3(256), 0, hs, g);
+    else if (ntiles == 6) hipLaunchKernelGGL(dt_scan_step_kernel<6>, grid, dim3(256), 0, hs, g);
+    else if (ntiles <= 8) hipLaunchKernelGGL(dt_scan_step_kernel<8>, grid, dim3(256), 0, hs, g);
+    else if (ntiles <= 10) hipLaunchKernelGGL(dt_scan_step_kernel<10>, grid, dim3(256), 0, hs, g);
+    else if (ntiles <= 12) hipLaunchKernelGGL(dt_scan_step_kernel<12>, grid, dim3(256), 0, hs, g);
+    else hipLaunchKernelGGL(dt_scan_step_kernel<16>, grid, dim3(256), 0, hs, g);
+    return check_launch("mi_xproj_dt_scan_step");
 }

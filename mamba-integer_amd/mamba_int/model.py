@@ -141,13 +141,17 @@ class IntegerMambaRunner:
 
     def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
                       h_state: torch.Tensor, li: int) -> None:
-        """One token per sequence through a layer in four kernels (fused stages)."""
+        """One token per sequence through a layer in three kernels (fused stages)."""
         dims = self.dims
         D, R, d = dims.d_inner, dims.dt_rank, dims.d_model
         ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
                               row_stats=ws.stats[li])
-        ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
-        ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
+        if dims.xp_width <= 256:
+            ops.xproj_dt_scan_step(ws.xs, ly.w_x, ly.s_x, R, ly.w_dt, ly.s_dt, ws.xz, D, ly.base, ly.k, ly.s_y,
+                                   h_state, ws.yo)
+        else:
+            ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+            ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
                       res_shift=ly.res_shift, row_stats=ws.stats[li + 1])
 

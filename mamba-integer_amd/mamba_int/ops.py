@@ -239,3 +239,16 @@ def dt_scan_step(xp, dt_rank: int, w_dt, s_dt: int, xs, z, z_off: int, base, dec
     D, N = base.shape
     _lib.call("mi_dt_scan_step", _ptr(xp), xp.shape[-1], dt_rank, _ptr(w_dt), s_dt, _ptr(xs), _ptr(z),
               z.shape[-1], z_off, _ptr(base), decay_shift, s_y, _ptr(h_state), _ptr(yo), m, D, N, _stream())
+
+
+def xproj_dt_scan_step(xs, w_x, s_x: int, dt_rank: int, w_dt, s_dt: int, z, z_off: int, base,
+                       decay_shift: int, s_y: int, h_state, yo) -> None:
+    """Decode stage: x_proj + dt_proj + decay + dt + scan state update + y + gate + requant."""
+    for t, nm in ((xs, "xs"), (z, "z"), (yo, "yo")):
+        _req(t, torch.int8, nm)
+    _req(w_x, torch.uint8, "w_x"); _req(w_dt, torch.uint8, "w_dt")
+    _req(base, torch.int32, "base"); _req(h_state, torch.int32, "h_state")
+    m = xs.shape[0]
+    D, N = base.shape
+    _lib.call("mi_xproj_dt_scan_step", _ptr(xs), _ptr(w_x), s_x, dt_rank, _ptr(w_dt), s_dt, _ptr(z),
+              z.shape[-1], z_off, _ptr(base), decay_shift, s_y, _ptr(h_state), _ptr(yo), m, D, N, _stream())

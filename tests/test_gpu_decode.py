@@ -110,3 +110,27 @@ def test_row_stats_paths(cuda):
             wh = pack_ternary(rng.integers(-1, 2, size=(40, d), dtype=np.int8))
             got = H(ops.norm_bitlinear(r, T(g), T(wh), ops.OUT_INT32, 40, row_stats=stats[1]))
             assert np.array_equal(got, O.bitlinear(ref, wh, O.OUT_INT32))
+
+
+@pytest.mark.parametrize("m,D,N,R", [(8, 1536, 16, 48), (1, 256, 16, 16), (16, 512, 32, 32), (3, 96, 8, 16),
+                                     (8, 4096, 16, 128), (2, 160, 64, 112), (4, 2048, 64, 64)])
+def test_xproj_dt_scan_step(cuda, m, D, N, R):
+    """x_proj fused in front of the scan step equals x_proj GEMV + unfused ops."""
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m * 7 + D + N + R)
+    NX = R + 2 * N
+    xs = rng.integers(0, 128, size=(m, D), dtype=np.int8)
+    wx = pack_ternary(rng.integers(-1, 2, size=(NX, D), dtype=np.int8))
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    z = i8(rng, m, 2 * D, lo=-128)
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    h0 = rng.integers(-(2**22), 2**22, size=(m, D, N), dtype=np.int32)
+    xp = O.bitlinear(xs, wx, O.OUT_INT8, 5)
+    dm = O.bitlinear(np.ascontiguousarray(xp[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs.reshape(m, 1, D), dm.reshape(m, 1, D), xp.reshape(m, 1, NX), R,
+                                 z.reshape(m, 1, 2 * D), D, base, 15, 13, h_state=h0)
+    hg = T(h0)
+    yo = T(np.zeros((m, D), np.int8))
+    ops.xproj_dt_scan_step(T(xs), T(wx), 5, R, T(wdt), 2, T(z), D, T(base), 15, 13, hg, yo)
+    assert np.array_equal(H(yo), yo_ref[:, 0])
+    assert np.array_equal(H(hg), h_ref)
