@@ -197,7 +197,7 @@ mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, i
  * unfused ops, bit for bit. */
 
 /* BitShiftNorm of r (int32 [m,k], m <= 16, k % 16 == 0, k <= 3072, r 16-byte
- * aligned; row statistics from row_stats when non-null) fused into
+ * and gamma 8-byte aligned; row statistics from row_stats when non-null) fused into
  * the BitLinear GEMV: out[m, n] = INT8 (sat8(rshr(acc, shift))) or INT32 acc,
  * out row stride ldo.  Replaces BitShiftNorm.forward + BitLinear.forward for
  * one token per sequence (the lm_head path of MambaIntegerModel.forward,
@@ -210,7 +210,8 @@ mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, const in
  * r int32 [m,d_model]; w_in packed [2*d_inner, d_model/4]; the x half goes
  * through the conv with conv_state int8 [m,3,d_inner] updated in place and
  * lands in xs int8 [m,d_inner]; the z half is written to xz int8
- * [m,2*d_inner] at columns [d_inner, 2*d_inner).  m <= 16, d_model <= 3072. */
+ * [m,2*d_inner] at columns [d_inner, 2*d_inner).  m <= 16, d_model <= 3072;
+ * alignment as mi_norm_bitlinear. */
 mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
                                const uint8_t *w_in, int s_in,
                                const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
@@ -236,6 +237,26 @@ mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x, int s_x, i
                                 const uint8_t *w_dt, int s_dt, const int8_t *z, int z_stride, int z_off,
                                 const int32_t *base, int decay_shift, int s_y, int32_t *h_state,
                                 int8_t *yo, int m, int d_inner, int nstate, void *stream);
+
+/* mi_norm_in_proj_conv that also starts x_proj (self.x_proj,
+ * mamba_integer_model.py:379,414): the block owning channels [16b, 16b+16)
+ * of the x half writes the exact int32 partial
+ *   xpart[i, b, n] = sum over those channels c of w_x[n, c] * xs[i, c]
+ * into xpart int32 [m, d_inner/16, nx], w_x packed [nx, d_inner/4]
+ * (4-byte aligned), nx = dt_rank + 2*nstate <= 256. */
+mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                     const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
+                                     int8_t *conv_state, int8_t *xs, int8_t *xz, const uint8_t *w_x, int nx,
+                                     int32_t *xpart, int m, int d_model, int d_inner, void *stream);
+
+/* mi_dt_scan_step with x_proj finished from those partials:
+ * xp[i, n] = sat8(rshr(sum over b < nblk of xpart[i, b, n], s_x)), then
+ * dt_rank, B and C as in mi_dt_scan_step.  nblk = d_inner/16 for the
+ * partials of mi_norm_in_proj_conv_xpart. */
+mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s_x, int dt_rank, const uint8_t *w_dt,
+                                int s_dt, const int8_t *xs, const int8_t *z, int z_stride, int z_off,
+                                const int32_t *base, int decay_shift, int s_y, int32_t *h_state, int8_t *yo,
+                                int m, int d_inner, int nstate, void *stream);
 
 #ifdef __cplusplus
 }

@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kMaxRows = 16;    // tokens per norm_gemv launch
 constexpr int kMaxNormK = 3072; // d_model limit of the LDS-staged rows
+constexpr int kMaxXTiles = 16;  // x_proj outputs (dt_rank + 2*nstate) <= 256
 
 struct NormGemvArgs {
     const int32_t *r;       // [M][K] residual, Q8
@@ -39,6 +40,11 @@ struct NormGemvArgs {
     int8_t *conv_state;     // [M][3][conv_d]
     int8_t *xs;             // [M][conv_d]
     int conv_d;
+    // x_proj partials of the x-blocks (optional): xpart[m][blk][nx] =
+    // sum over the block's 16 channels c of w_x[n][c] * xs[m][c]
+    const uint32_t *w_x;    // [nx][conv_d/16] words
+    int nx;
+    int32_t *xpart;
 };
 
 __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
@@ -46,28 +52,75 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
     return v;
 }
 
-// Normalized int8 rows (spec rule 4.1) of r[0..M) into LDS a[16][pitch]: one
-// wave per row, the row statistics taken from row_stats or summed here in one
-// pass.
+// Normalized int8 rows (spec rule 4.1) of r[0..M) into LDS a[16][pitch].
+// With row_stats: every thread normalizes 4-element groups of the flattened
+// [M][K] rows; the loads of a whole chunk of groups are issued before the
+// first wait, and threads 0..M-1 turn the row statistics into (mu, shift) in
+// LDS meanwhile.  Without: one wave per row sums the row in one pass.
 __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (g.row_stats) {
+        // rows padded to a power of two Mp; TPR = 256/Mp threads per row, each
+        // with its row's (mu, shift) in registers and groups tr, tr+TPR, ...
+        const int Mp = g.M <= 1 ? 1 : g.M <= 2 ? 2 : g.M <= 4 ? 4 : g.M <= 8 ? 8 : 16;
+        const int TPR = 256 / Mp;
+        const int m = (int)threadIdx.x / TPR, tr = (int)threadIdx.x - m * TPR;
+        const int mr = min(m, g.M - 1);
+        const int K4 = g.K / 4;
+        constexpr int kC = 8;
+        int4 rv[kC];
+        uint2 gv[kC];
+        const int32_t *row = g.r + (int64_t)mr * g.K;
+        auto load_chunk = [&](int j0) {
+#pragma unroll
+            for (int c = 0; c < kC; ++c) {
+                const int grp = min(tr + (j0 + c) * TPR, K4 - 1);
+                rv[c] = *reinterpret_cast<const int4 *>(row + 4 * grp);
+                gv[c] = *reinterpret_cast<const uint2 *>(g.gamma + 4 * grp);
+            }
+        };
+        load_chunk(0);
+        int64_t mu64;
+        const int sh = norm_shift(g.row_stats[2 * mr], g.row_stats[2 * mr + 1], g.K, &mu64);
+        const int32_t mu = (int32_t)mu64;
+        const int64_t rnd = (int64_t)1 << (sh - 1);
+        const int ngrp = (K4 + TPR - 1) / TPR;
+        for (int j0 = 0; j0 < ngrp; j0 += kC) {
+            if (j0 > 0) load_chunk(j0);
+#pragma unroll
+            for (int c = 0; c < kC; ++c) {
+                const int grp = tr + (j0 + c) * TPR;
+                if (m < g.M && grp < K4) {
+                    const int vv[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
+                    const int gg[4] = {(int16_t)(gv[c].x & 0xFFFF), (int16_t)(gv[c].x >> 16),
+                                       (int16_t)(gv[c].y & 0xFFFF), (int16_t)(gv[c].y >> 16)};
+                    uint32_t o = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        // |r - mu| < 2^24 and |gamma| < 2^15, so the rounded
+                        // quotient (shift >= 9) fits 32 bits: the low word of
+                        // the 64-bit shift is the exact value
+                        const int64_t p = (int64_t)(vv[q] - mu) * gg[q] + rnd;
+                        const int32_t v = (int32_t)__builtin_amdgcn_alignbit((uint32_t)((uint64_t)p >> 32),
+                                                                             (uint32_t)p, (uint32_t)sh);
+                        o |= (uint32_t)(min(max(v, -127), 127) & 255) << (8 * q);
+                    }
+                    *reinterpret_cast<uint32_t *>(&a[m * pitch + 4 * grp]) = o;
+                }
+            }
+        }
+        return;
+    }
     for (int m = wave; m < g.M; m += 4) {
         const int32_t *row = g.r + (int64_t)m * g.K;
-        int64_t s1, s2;
-        if (g.row_stats) {
-            s1 = g.row_stats[2 * m];
-            s2 = g.row_stats[2 * m + 1];
-        } else {
-            s1 = 0;
-            s2 = 0;
-            for (int i = lane; i < g.K; i += 64) {
-                const int64_t v = row[i];
-                s1 += v;
-                s2 += v * v;
-            }
-            s1 = wave_sum64(s1);
-            s2 = wave_sum64(s2);
+        int64_t s1 = 0, s2 = 0;
+        for (int i = lane; i < g.K; i += 64) {
+            const int64_t v = row[i];
+            s1 += v;
+            s2 += v * v;
         }
+        s1 = wave_sum64(s1);
+        s2 = wave_sum64(s2);
         int64_t mu;
         const int sh = norm_shift(s1, s2, g.K, &mu);
         for (int i = 4 * lane; i < g.K; i += 256) {
@@ -132,6 +185,16 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
         }
     }
 
+    // x_proj words of this block's 16 channels (x-blocks, wave 0)
+    const bool xpart = CONV && !WIDE && g.xpart != nullptr && n0 < g.conv_d;
+    uint32_t wx[kMaxXTiles];
+    if (xpart && wave == 0) {
+        const int xkw = g.conv_d / 16;
+#pragma unroll
+        for (int t = 0; t < kMaxXTiles; ++t)
+            wx[t] = 16 * t < g.nx ? g.w_x[(int64_t)min(16 * t + l16, g.nx - 1) * xkw + n0 / 16] : 0u;
+    }
+
     stage_norm_rows(g, a, pitch);
     __syncthreads();
 
@@ -155,6 +218,48 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
         __syncthreads();
         if (wave != 0) return;
         acc = acc + red[lane] + red[64 + lane] + red[128 + lane];
+    }
+    if constexpr (CONV && !WIDE) {
+        if (xpart) {
+            // conv + squareplus for every lane of wave 0 (zeros where idle),
+            // then the block's x_proj partial: one MFMA per 16 x_proj rows with
+            // K = this block's 16 channels (lane group lq carries channels
+            // 4lq..4lq+3 in its first dword, the other k slots are zero)
+            uint32_t xsw = 0, cur = 0;
+            if (conv) {
+                for (int r = 0; r < 4; ++r) {
+                    const int v = clamp32(rshr32(acc[r], g.shift), -127, 127);
+                    int32_t c = cb[r];
+                    c += (int)(int8_t)(cw[r]) * (int)(int8_t)(cs0 >> (8 * r));
+                    c += (int)(int8_t)(cw[r] >> 8) * (int)(int8_t)(cs1 >> (8 * r));
+                    c += (int)(int8_t)(cw[r] >> 16) * (int)(int8_t)(cs2 >> (8 * r));
+                    c += (int)(int8_t)(cw[r] >> 24) * v;
+                    xsw |= (uint32_t)(sqp_q(c) & 255) << (8 * r);
+                    cur |= (uint32_t)(v & 255) << (8 * r);
+                }
+                int8_t *st = g.conv_state + (int64_t)m * 3 * g.conv_d;
+                *reinterpret_cast<uint32_t *>(g.xs + (int64_t)m * g.conv_d + nf) = xsw;
+                *reinterpret_cast<uint32_t *>(st + nf) = cs1;
+                *reinterpret_cast<uint32_t *>(st + g.conv_d + nf) = cs2;
+                *reinterpret_cast<uint32_t *>(st + 2 * g.conv_d + nf) = cur;
+            }
+            const v4i fb = v4i{(int)xsw, 0, 0, 0};
+            const uint32_t lut = 0xFFFE0100u;
+            const int nblk = g.conv_d / 16;
+            int32_t *dst = g.xpart + ((int64_t)m * nblk + blockIdx.x) * g.nx;
+#pragma unroll
+            for (int t = 0; t < kMaxXTiles; ++t) {
+                if (16 * t < g.nx) {
+                    const v4i fa = v4i{(int)__builtin_amdgcn_perm(lut, lut, (wx[t] >> (2 * lq)) & 0x03030303u), 0, 0, 0};
+                    const v4i d = mfma_i8(fa, fb, v4i{0, 0, 0, 0});
+                    // lane (token l16, group lq) holds rows 16t + 4lq + r
+                    if (m < g.M)
+                        for (int r = 0; r < 4; ++r)
+                            if (16 * t + 4 * lq + r < g.nx) dst[16 * t + 4 * lq + r] = d[r];
+                }
+            }
+            return;
+        }
     }
     if (!epi) return;
     if constexpr (KIND == MI_OUT_INT32) {
@@ -193,6 +298,9 @@ struct DtScanArgs {
     int64_t xp_stride;
     const uint32_t *w_x;    // fused x_proj: [R+2N][D/16] words (xp unused)
     int s_x;
+    bool x_c16;             // w_x rows are whole 16-word chunks, 16-byte aligned
+    const int32_t *xpart;   // x_proj partials [M][nblk][R+2N] (XNT < 0)
+    int nblk;
     int R;
     const uint32_t *w_dt;   // [D][R/16] words
     int s_dt;
@@ -208,7 +316,6 @@ struct DtScanArgs {
 
 constexpr int kMaxR = 256;
 constexpr int kMaxN = 64;
-constexpr int kMaxXTiles = 16;   // fused x_proj: R + 2N <= 256
 
 // Thread quad per channel: lane g of the quad keeps states g, g+4, g+8, ...;
 // every lane computes the channel's dt_proj dot (48-wide at d768), the quad
@@ -237,31 +344,86 @@ __device__ __forceinline__ void xproj_token(const DtScanArgs &g, int m, int32_t 
     // the trip count is the same for every lane (MFMA reads all 64 lanes, so
     // no lane may skip it); words past a group's run load as zeros
     for (int c0 = 0; c0 < wpg; c0 += CW) {
+        // every load is unconditional, from a clamped in-bounds address (a
+        // divergent load would make the compiler wait on it before the next
+        // one): rows past NX feed result rows nobody reads, and words past
+        // the group's run meet a zero B operand
         uint2 wv[NT][CW / 2];
-        v4i fa[CW];
+        v4i xv[CW];
 #pragma unroll
         for (int p = 0; p < CW / 2; ++p) {
-            const int w = w0 + c0 + 2 * p;
-            const bool ok = w < w1;
+            const int wc = min(w0 + c0 + 2 * p, kwx - 2);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const int n = 16 * t + l16;
-                wv[t][p] = (ok && n < NX) ? *reinterpret_cast<const uint2 *>(g.w_x + (int64_t)n * kwx + w)
-                                          : make_uint2(0u, 0u);
+                const int n = min(16 * t + l16, NX - 1);
+                wv[t][p] = *reinterpret_cast<const uint2 *>(g.w_x + (int64_t)n * kwx + wc);
             }
-            const bool xa = ok && l16 == 0;
-            fa[2 * p] = xa ? *reinterpret_cast<const v4i *>(xrow + 16 * w) : v4i{0, 0, 0, 0};
-            fa[2 * p + 1] = xa ? *reinterpret_cast<const v4i *>(xrow + 16 * w + 16) : v4i{0, 0, 0, 0};
+            xv[2 * p] = *reinterpret_cast<const v4i *>(xrow + 16 * wc);
+            xv[2 * p + 1] = *reinterpret_cast<const v4i *>(xrow + 16 * wc + 16);
         }
 #pragma unroll
-        for (int p = 0; p < CW / 2; ++p)
+        for (int p = 0; p < CW / 2; ++p) {
+            const bool xa = l16 == 0 && w0 + c0 + 2 * p < w1;
+            const v4i f0 = xa ? xv[2 * p] : v4i{0, 0, 0, 0};
+            const v4i f1 = xa ? xv[2 * p + 1] : v4i{0, 0, 0, 0};
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                acc[t] = mfma_i8(unpack16(wv[t][p].x), fa[2 * p], acc[t]);
-                acc[t] = mfma_i8(unpack16(wv[t][p].y), fa[2 * p + 1], acc[t]);
+                acc[t] = mfma_i8(unpack16(wv[t][p].x), f0, acc[t]);
+                acc[t] = mfma_i8(unpack16(wv[t][p].y), f1, acc[t]);
             }
+        }
     }
     // column-0 lanes (l16 == 0) hold features 16t + 4lq + r
+    if (l16 == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s_xacc[wave][16 * t + 4 * lq + r] = acc[t][r];
+    }
+}
+
+// Coalesced variant for d_inner % 256 == 0 (the packed row is a whole number
+// of 16-word chunks): wave v takes chunks v, v+4, ...; in a chunk, lane
+// (l16, lq) reads words [4lq, 4lq+4) of row 16t+l16 as one 16-byte load, so
+// one load instruction covers 64 contiguous bytes of each of 16 rows, and the
+// four words feed four MFMA k-steps.  Two chunks' loads are in flight at once.
+template <int NT>
+__device__ __forceinline__ void xproj_token_c16(const DtScanArgs &g, int m, int32_t (*s_xacc)[16 * kMaxXTiles]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int NX = g.R + 2 * g.N;
+    const int kwx = g.D / 16;
+    const int nchunk = kwx / 16;
+    const int8_t *xrow = g.xs + (int64_t)m * g.D;
+    v4i acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
+    for (int c0 = wave; c0 < nchunk; c0 += 8) {
+        v4i wv[2][NT];
+        v4i xv[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            // a second chunk past the end re-reads the first (in bounds) and meets a zero B operand
+            const int c = c0 + 4 * u < nchunk ? c0 + 4 * u : c0;
+            const int w = 16 * c + 4 * lq;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int n = min(16 * t + l16, NX - 1);
+                wv[u][t] = *reinterpret_cast<const v4i *>(g.w_x + (int64_t)n * kwx + w);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[u][j] = *reinterpret_cast<const v4i *>(xrow + 16 * (w + j));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const bool xa = l16 == 0 && c0 + 4 * u < nchunk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const v4i f = xa ? xv[u][j] : v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_i8(unpack16((uint32_t)wv[u][t][j]), f, acc[t]);
+            }
+        }
+    }
     if (l16 == 0) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -273,17 +435,25 @@ __device__ __forceinline__ void xproj_token(const DtScanArgs &g, int m, int32_t 
 // XNT > 0: the block first computes the x_proj outputs of its token itself
 // (XNT tiles of 16 features, the x_proj weights come from L2), so the
 // separate x_proj GEMV kernel and its launch leave the decode chain.
-template <int XNT>
+// NPL > 0 (nstate == 4*NPL): lane q of a channel owns the contiguous states
+// [q*NPL, q*NPL+NPL), read and written as int4; NPL == 0: lane q owns states
+// q, q+4, ... (any nstate <= 64).  Every load is issued unconditionally from
+// an in-bounds address before the first wait.
+template <int XNT, int NPL>
 __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_dt[kMaxR];
     __shared__ int8_t s_bc[2 * kMaxN];
-    __shared__ int32_t s_xacc[XNT ? 4 : 1][XNT ? 16 * kMaxXTiles : 1];
-    constexpr int kPerLane = kMaxN / 4;
+    __shared__ int32_t s_xacc[XNT ? 4 : 1][XNT ? 16 * kMaxXTiles : 1];  // XNT < 0: row 0 only
+    __shared__ int32_t s_dtq[41];    // dt_q16(dm) for dm in [-20, 20]
+    __shared__ int32_t s_gate[256];  // gate_q15(z) for z in [-128, 127] (the block has 256 threads)
+    if (threadIdx.x < 41) s_dtq[threadIdx.x] = dt_q16((int)threadIdx.x - 20);
+    s_gate[threadIdx.x] = gate_q15((int)threadIdx.x - 128);
+    constexpr int kPerLane = NPL > 0 ? NPL : kMaxN / 4;
     const int m = blockIdx.y;
     const int q = threadIdx.x & 3;
     const int d = blockIdx.x * 64 + (threadIdx.x >> 2);
     const bool active = d < g.D;
-    const int dd = active ? d : 0;
+    const int dd = active ? d : g.D - 1;
     // loads that do not depend on the staged row: ternary dt_proj words, state, decays, xs, z
     const int kw = g.R / 16;
     uint32_t wdt[kMaxR / 16];
@@ -292,17 +462,63 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     int32_t *hp = g.h + ((int64_t)m * g.D + dd) * g.N;
     const int32_t *bp = g.base + (int64_t)dd * g.N;
     int32_t hv[kPerLane], bv[kPerLane];
+    if constexpr (NPL > 0) {
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int n = q + 4 * i;
-        hv[i] = (active && n < g.N) ? hp[n] : 0;
-        bv[i] = (active && n < g.N) ? bp[n] : 0;
+        for (int c = 0; c < NPL / 4; ++c) {
+            const int4 h4 = *reinterpret_cast<const int4 *>(hp + q * NPL + 4 * c);
+            const int4 b4 = *reinterpret_cast<const int4 *>(bp + q * NPL + 4 * c);
+            hv[4 * c] = h4.x; hv[4 * c + 1] = h4.y; hv[4 * c + 2] = h4.z; hv[4 * c + 3] = h4.w;
+            bv[4 * c] = b4.x; bv[4 * c + 1] = b4.y; bv[4 * c + 2] = b4.z; bv[4 * c + 3] = b4.w;
+        }
+    } else {
+        const int nq = (g.N + 3) >> 2;  // same for every lane
+#pragma unroll
+        for (int i = 0; i < kPerLane; ++i) {
+            if (i < nq) {
+                const int n = min(q + 4 * i, g.N - 1);
+                hv[i] = hp[n];
+                bv[i] = bp[n];
+            } else {
+                hv[i] = 0;
+                bv[i] = 0;
+            }
+        }
     }
     const int xsv = g.xs[(int64_t)m * g.D + dd];
     const int zv = g.z[(int64_t)m * g.z_stride + dd];
 
-    if constexpr (XNT > 0) {
-        xproj_token<XNT>(g, m, s_xacc);
+    if constexpr (XNT < 0) {
+        // x_proj from the producer's per-block partials: thread (sub, n) sums
+        // blocks sub, sub+S, ... of output n (32 loads in flight), the S
+        // sub-sums meet in LDS
+        const int NX = g.R + 2 * g.N;
+        const int S = max(1, 256 / NX);
+        const int sub = threadIdx.x / NX;
+        const int n = (int)threadIdx.x - sub * NX;
+        if (sub < S) {
+            const int nb = g.nblk;
+            const int32_t *pp = g.xpart + (int64_t)m * nb * NX + n;
+            int32_t sum = 0;
+            for (int b0 = sub; b0 < nb; b0 += 32 * S) {
+                int32_t v[32];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) v[u] = pp[(int64_t)min(b0 + u * S, nb - 1) * NX];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) sum += b0 + u * S < nb ? v[u] : 0;
+            }
+            s_xacc[0][sub * NX + n] = sum;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < NX; i += 256) {
+            int v = 0;
+            for (int k = 0; k < S; ++k) v += s_xacc[0][k * NX + i];
+            const int8_t q8 = (int8_t)clamp32(rshr32(v, g.s_x), -127, 127);
+            if (i < g.R) s_dt[i] = q8;
+            else s_bc[i - g.R] = q8;
+        }
+    } else if constexpr (XNT > 0) {
+        if (g.x_c16) xproj_token_c16<(XNT > 0 ? XNT : 1)>(g, m, s_xacc);
+        else xproj_token<(XNT > 0 ? XNT : 1)>(g, m, s_xacc);
         __syncthreads();
         const int NX = g.R + 2 * g.N;
         for (int i = threadIdx.x; i < NX; i += 256) {
@@ -328,24 +544,54 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
         }
     }
     const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
-    const int64_t xd = rshr64((int64_t)xsv * dt_q16(dm), 10);
+    const int64_t xd = rshr64((int64_t)xsv * s_dtq[dm + 20], 10);
     int64_t y = 0;
+    if constexpr (NPL > 0) {
+        int32_t hn[NPL];
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int n = q + 4 * i;
-        if (active && n < g.N) {
+        for (int i = 0; i < NPL; ++i) {
+            const int n = q * NPL + i;
             const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
-            const int32_t hn = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[n] * xd);
-            hp[n] = hn;
-            y += (int64_t)s_bc[g.N + n] * hn;
+            hn[i] = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[n] * xd);
+            y += (int64_t)s_bc[g.N + n] * hn[i];
+        }
+        if (active) {
+#pragma unroll
+            for (int c = 0; c < NPL / 4; ++c)
+                *reinterpret_cast<int4 *>(hp + q * NPL + 4 * c) =
+                    make_int4(hn[4 * c], hn[4 * c + 1], hn[4 * c + 2], hn[4 * c + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kPerLane; ++i) {
+            const int n = q + 4 * i;
+            if (active && n < g.N) {
+                const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
+                const int32_t hn = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[n] * xd);
+                hp[n] = hn;
+                y += (int64_t)s_bc[g.N + n] * hn;
+            }
         }
     }
     y += __shfl_xor(y, 1);
     y += __shfl_xor(y, 2);
     if (active && q == 0) {
-        const int64_t yg = ((int64_t)sat32_64(y) * gate_q15(zv)) >> 15;
+        const int64_t yg = ((int64_t)sat32_64(y) * s_gate[zv + 128]) >> 15;
         g.yo[(int64_t)m * g.D + d] = (int8_t)clamp64(rshr64(yg, g.s_y), -127, 127);
     }
+}
+
+template <int NPL>
+void launch_xproj_scan(int ntiles, dim3 grid, hipStream_t hs, const DtScanArgs &g) {
+    if (ntiles <= 2) hipLaunchKernelGGL((dt_scan_step_kernel<2, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles == 3) hipLaunchKernelGGL((dt_scan_step_kernel<3, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles == 4) hipLaunchKernelGGL((dt_scan_step_kernel<4, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles == 5) hipLaunchKernelGGL((dt_scan_step_kernel<5, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles == 6) hipLaunchKernelGGL((dt_scan_step_kernel<6, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles <= 8) hipLaunchKernelGGL((dt_scan_step_kernel<8, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles <= 10) hipLaunchKernelGGL((dt_scan_step_kernel<10, NPL>), grid, dim3(256), 0, hs, g);
+    else if (ntiles <= 12) hipLaunchKernelGGL((dt_scan_step_kernel<12, NPL>), grid, dim3(256), 0, hs, g);
+    else hipLaunchKernelGGL((dt_scan_step_kernel<16, NPL>), grid, dim3(256), 0, hs, g);
 }
 
 mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma, const uint8_t *w, int m, int n,
@@ -356,7 +602,8 @@ mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma
                kMaxNormK);
     if ((int64_t)m * n == 0) return MI_OK;
     MI_REQUIRE(r && gamma && w, MI_ERR_NULL_POINTER, "%s: r, gamma and w_packed are required", fn);
-    MI_REQUIRE(aligned(w, 4), MI_ERR_BAD_ALIGNMENT, "%s: w_packed must be 4-byte aligned", fn);
+    MI_REQUIRE(aligned(w, 4) && aligned(gamma, 8), MI_ERR_BAD_ALIGNMENT,
+               "%s: w_packed must be 4-byte aligned, gamma 8-byte aligned", fn);
     return MI_OK;
 }
 
@@ -397,28 +644,60 @@ extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stat
     return check_launch("mi_norm_bitlinear");
 }
 
-extern "C" mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                          const uint8_t *w_in, int s_in,
-                                          const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
-                                          int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream) {
+namespace mi {
+namespace {
+mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                 const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
+                                 int8_t *conv_state, int8_t *xs, int8_t *xz, const uint8_t *w_x, int nx,
+                                 int32_t *xpart, int m, int d_model, int d_inner, void *stream) {
     clear_error();
-    mi_status st = check_norm_gemv("mi_norm_in_proj_conv", r, gamma, w_in, m, 2 * d_inner, d_model);
+    mi_status st = check_norm_gemv(fn, r, gamma, w_in, m, 2 * d_inner, d_model);
     if (st != MI_OK || (int64_t)m * d_inner == 0) return st;
-    MI_REQUIRE(d_inner % 16 == 0, MI_ERR_BAD_DIM, "mi_norm_in_proj_conv: d_inner=%d must be a multiple of 16", d_inner);
+    MI_REQUIRE(d_inner % 16 == 0, MI_ERR_BAD_DIM, "%s: d_inner=%d must be a multiple of 16", fn, d_inner);
     MI_REQUIRE(conv_w && conv_b && conv_state && xs && xz, MI_ERR_NULL_POINTER,
-               "mi_norm_in_proj_conv: conv_w, conv_b, conv_state, xs and xz are required");
+               "%s: conv_w, conv_b, conv_state, xs and xz are required", fn);
     MI_REQUIRE(aligned(conv_w, 4) && aligned(conv_state, 4) && aligned(xs, 4), MI_ERR_BAD_ALIGNMENT,
-               "mi_norm_in_proj_conv: conv_w, conv_state and xs must be 4-byte aligned");
-    MI_REQUIRE(s_in >= 0 && s_in <= 30, MI_ERR_BAD_ARG, "mi_norm_in_proj_conv: s_in=%d outside [0,30]", s_in);
+               "%s: conv_w, conv_state and xs must be 4-byte aligned", fn);
+    MI_REQUIRE(s_in >= 0 && s_in <= 30, MI_ERR_BAD_ARG, "%s: s_in=%d outside [0,30]", fn, s_in);
+    MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "%s: r must be 16-byte aligned", fn);
+    if (xpart) {
+        MI_REQUIRE(w_x, MI_ERR_NULL_POINTER, "%s: w_x is required with xpart", fn);
+        MI_REQUIRE(nx >= 1 && nx <= 16 * kMaxXTiles, MI_ERR_BAD_DIM, "%s: nx=%d outside [1,%d]", fn, nx,
+                   16 * kMaxXTiles);
+        MI_REQUIRE(aligned(w_x, 4), MI_ERR_BAD_ALIGNMENT, "%s: w_x must be 4-byte aligned", fn);
+    }
     NormGemvArgs g{};
-    MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "mi_norm_in_proj_conv: r must be 16-byte aligned");
     g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_in); g.out = xz;
     g.ldo = 2 * (int64_t)d_inner;
     g.M = m; g.N = 2 * d_inner; g.K = d_model; g.kw = d_model / 16; g.shift = s_in;
     g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs; g.conv_d = d_inner;
+    g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.nx = nx; g.xpart = xpart;
     hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, true, false>), dim3((unsigned)(2 * d_inner / 16)), dim3(256),
                        norm_gemv_lds(d_model), as_stream(stream), g);
-    return check_launch("mi_norm_in_proj_conv");
+    return check_launch(fn);
+}
+}  // namespace
+}  // namespace mi
+
+extern "C" mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                          const uint8_t *w_in, int s_in,
+                                          const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
+                                          int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream) {
+    return norm_in_proj_conv_impl("mi_norm_in_proj_conv", r, row_stats, gamma, w_in, s_in, conv_w, conv_b,
+                                  conv_state, xs, xz, nullptr, 0, nullptr, m, d_model, d_inner, stream);
+}
+
+extern "C" mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                                const uint8_t *w_in, int s_in, const int8_t *conv_w,
+                                                const int32_t *conv_b, int8_t *conv_state, int8_t *xs, int8_t *xz,
+                                                const uint8_t *w_x, int nx, int32_t *xpart, int m, int d_model,
+                                                int d_inner, void *stream) {
+    if (!xpart) {
+        mi::clear_error();
+        return mi::fail(MI_ERR_NULL_POINTER, "mi_norm_in_proj_conv_xpart: xpart is required");
+    }
+    return norm_in_proj_conv_impl("mi_norm_in_proj_conv_xpart", r, row_stats, gamma, w_in, s_in, conv_w, conv_b,
+                                  conv_state, xs, xz, w_x, nx, xpart, m, d_model, d_inner, stream);
 }
 
 extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const uint8_t *w_dt, int s_dt,
@@ -443,9 +722,47 @@ extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_ran
     g.xp = xp; g.xp_stride = xp_stride; g.R = dt_rank; g.w_dt = reinterpret_cast<const uint32_t *>(w_dt); g.s_dt = s_dt;
     g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
-    hipLaunchKernelGGL(dt_scan_step_kernel<0>, dim3((unsigned)((d_inner + 63) / 64), (unsigned)m), dim3(256), 0,
-                       as_stream(stream), g);
+    const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
+    const bool vec = nstate == 16 && aligned(h_state, 16) && aligned(base, 16);
+    if (vec) hipLaunchKernelGGL((dt_scan_step_kernel<0, 4>), grid, dim3(256), 0, as_stream(stream), g);
+    else hipLaunchKernelGGL((dt_scan_step_kernel<0, 0>), grid, dim3(256), 0, as_stream(stream), g);
     return check_launch("mi_dt_scan_step");
+}
+
+extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s_x, int dt_rank,
+                                           const uint8_t *w_dt, int s_dt, const int8_t *xs, const int8_t *z,
+                                           int z_stride, int z_off, const int32_t *base, int decay_shift, int s_y,
+                                           int32_t *h_state, int8_t *yo, int m, int d_inner, int nstate,
+                                           void *stream) {
+    clear_error();
+    MI_REQUIRE(m >= 0 && d_inner >= 0 && nblk >= 1, MI_ERR_BAD_DIM, "mi_xpart_dt_scan_step: bad size");
+    MI_REQUIRE(dt_rank >= 16 && dt_rank % 16 == 0 && dt_rank <= kMaxR, MI_ERR_BAD_DIM,
+               "mi_xpart_dt_scan_step: dt_rank=%d must be a multiple of 16 in [16,%d]", dt_rank, kMaxR);
+    MI_REQUIRE(nstate >= 1 && nstate <= kMaxN, MI_ERR_BAD_DIM, "mi_xpart_dt_scan_step: nstate=%d outside [1,%d]",
+               nstate, kMaxN);
+    MI_REQUIRE(dt_rank + 2 * nstate <= 16 * kMaxXTiles, MI_ERR_BAD_DIM,
+               "mi_xpart_dt_scan_step: dt_rank + 2*nstate = %d exceeds %d", dt_rank + 2 * nstate, 16 * kMaxXTiles);
+    MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride, MI_ERR_BAD_DIM,
+               "mi_xpart_dt_scan_step: z columns exceed z_stride");
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG,
+               "mi_xpart_dt_scan_step: decay_shift outside [1,30]");
+    MI_REQUIRE(s_x >= 0 && s_x <= 30 && s_dt >= 0 && s_dt <= 30 && s_y >= 0 && s_y <= 30, MI_ERR_BAD_ARG,
+               "mi_xpart_dt_scan_step: shift out of range");
+    if ((int64_t)m * d_inner == 0) return MI_OK;
+    MI_REQUIRE(xpart && w_dt && xs && z && base && h_state && yo, MI_ERR_NULL_POINTER,
+               "mi_xpart_dt_scan_step: a required pointer is NULL");
+    MI_REQUIRE(aligned(w_dt, 4), MI_ERR_BAD_ALIGNMENT, "mi_xpart_dt_scan_step: w_dt must be 4-byte aligned");
+    DtScanArgs g{};
+    g.xpart = xpart; g.nblk = nblk; g.s_x = s_x; g.R = dt_rank;
+    g.w_dt = reinterpret_cast<const uint32_t *>(w_dt); g.s_dt = s_dt;
+    g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
+    g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
+    const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
+    if (nstate == 16 && aligned(h_state, 16) && aligned(base, 16))
+        hipLaunchKernelGGL((dt_scan_step_kernel<-1, 4>), grid, dim3(256), 0, as_stream(stream), g);
+    else
+        hipLaunchKernelGGL((dt_scan_step_kernel<-1, 0>), grid, dim3(256), 0, as_stream(stream), g);
+    return check_launch("mi_xpart_dt_scan_step");
 }
 
 extern "C" mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x, int s_x, int dt_rank,
@@ -474,20 +791,14 @@ extern "C" mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x,
                "mi_xproj_dt_scan_step: xs must be 16-byte aligned, w_x 8-byte and w_dt 4-byte aligned");
     DtScanArgs g{};
     g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.s_x = s_x; g.R = dt_rank;
+    g.x_c16 = d_inner % 256 == 0 && aligned(w_x, 16);
     g.w_dt = reinterpret_cast<const uint32_t *>(w_dt); g.s_dt = s_dt;
     g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
     const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
     hipStream_t hs = as_stream(stream);
     const int ntiles = (dt_rank + 2 * nstate + 15) / 16;
-    if (ntiles <= 2) hipLaunchKernelGGL(dt_scan_step_kernel<2>, grid, dim3(256), 0, hs, g);
-    else if (ntiles == 3) hipLaunchKernelGGL(dt_scan_step_kernel<3>, grid, dim3(256), 0, hs, g);
-    else if (ntiles == 4) hipLaunchKernelGGL(dt_scan_step_kernel<4>, grid, dim3(256), 0, hs, g);
-    else if (ntiles == 5) hipLaunchKernelGGL(dt_scan_step_kernel<5>, grid, dim3(256), 0, hs, g);
-    else if (ntiles == 6) hipLaunchKernelGGL(dt_scan_step_kernel<6>, grid, dim3(256), 0, hs, g);
-    else if (ntiles <= 8) hipLaunchKernelGGL(dt_scan_step_kernel<8>, grid, dim3(256), 0, hs, g);
-    else if (ntiles <= 10) hipLaunchKernelGGL(dt_scan_step_kernel<10>, grid, dim3(256), 0, hs, g);
-    else if (ntiles <= 12) hipLaunchKernelGGL(dt_scan_step_kernel<12>, grid, dim3(256), 0, hs, g);
-    else hipLaunchKernelGGL(dt_scan_step_kernel<16>, grid, dim3(256), 0, hs, g);
+    if (nstate == 16 && aligned(h_state, 16) && aligned(base, 16)) launch_xproj_scan<4>(ntiles, grid, hs, g);
+    else launch_xproj_scan<0>(ntiles, grid, hs, g);
     return check_launch("mi_xproj_dt_scan_step");
 }

@@ -42,6 +42,8 @@ SIGNATURES = {
     "mi_norm_in_proj_conv": [P, P, P, P, I, P, P, P, P, P, I, I, I, P],
     "mi_dt_scan_step": [P, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
     "mi_xproj_dt_scan_step": [P, P, I, I, P, I, P, I, I, P, I, I, P, P, I, I, I, P],
+    "mi_norm_in_proj_conv_xpart": [P, P, P, P, I, P, P, P, P, P, P, I, P, I, I, I, P],
+    "mi_xpart_dt_scan_step": [P, I, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
 }
 
 

@@ -68,6 +68,10 @@ class _Workspace:
         self.yo = torch.empty((T, D), dtype=torch.int8, device=device)
         # row statistics (sum r, sum r^2) of the residual entering layer i (i = n_layer: the head)
         self.stats = torch.empty((dims.n_layer + 1, T, 2), dtype=torch.int64, device=device)
+        # x_proj partials of the decode chain (one row per 16 channels of d_inner)
+        nx = dims.dt_rank + 2 * dims.d_state
+        self.xpart = (torch.empty((T, D // 16, nx), dtype=torch.int32, device=device)
+                      if T <= 16 and (D // 16) * nx <= 8192 else None)
 
 
 class IntegerMambaRunner:
@@ -144,6 +148,15 @@ class IntegerMambaRunner:
         """One token per sequence through a layer in three kernels (fused stages)."""
         dims = self.dims
         D, R, d = dims.d_inner, dims.dt_rank, dims.d_model
+        if ws.xpart is not None:
+            # x_proj partials from the in_proj blocks, summed by the scan step
+            ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
+                                  row_stats=ws.stats[li], w_x=ly.w_x, xpart=ws.xpart)
+            ops.xpart_dt_scan_step(ws.xpart, ly.s_x, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y,
+                                   h_state, ws.yo)
+            ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                          res_shift=ly.res_shift, row_stats=ws.stats[li + 1])
+            return
         ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
                               row_stats=ws.stats[li])
         if dims.xp_width <= 256:

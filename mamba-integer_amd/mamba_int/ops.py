@@ -216,16 +216,42 @@ def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor,
     return o
 
 
-def norm_in_proj_conv(r, gamma, w_in, s_in: int, conv_w, conv_b, conv_state, xs, xz, row_stats=None) -> None:
+def norm_in_proj_conv(r, gamma, w_in, s_in: int, conv_w, conv_b, conv_state, xs, xz, row_stats=None,
+                      w_x=None, xpart=None) -> None:
     """Decode stage: norm + in_proj GEMV + conv step + squareplus (x half -> xs, conv_state
-    updated in place), z half -> xz[:, d_inner:]."""
+    updated in place), z half -> xz[:, d_inner:].  With w_x and xpart [m, d_inner/16, nx]
+    int32, also the per-16-channel x_proj partials."""
     _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma"); _req(w_in, torch.uint8, "w_in")
     _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
     _req(conv_state, torch.int8, "conv_state"); _req(xs, torch.int8, "xs"); _req(xz, torch.int8, "xz")
     m, d = r.shape
     D = conv_w.shape[0]
-    _lib.call("mi_norm_in_proj_conv", _ptr(r), _ptr(_opt(row_stats, torch.int64, "row_stats")), _ptr(gamma),
-              _ptr(w_in), s_in, _ptr(conv_w), _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), m, d, D,
+    stats = _ptr(_opt(row_stats, torch.int64, "row_stats"))
+    if xpart is None:
+        _lib.call("mi_norm_in_proj_conv", _ptr(r), stats, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
+                  _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), m, d, D, _stream())
+        return
+    _req(xpart, torch.int32, "xpart"); _req(w_x, torch.uint8, "w_x")
+    if tuple(xpart.shape[:2]) != (m, D // 16):
+        raise ValueError(f"xpart must be [m, d_inner/16, nx], got {tuple(xpart.shape)}")
+    _lib.call("mi_norm_in_proj_conv_xpart", _ptr(r), stats, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
+              _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), _ptr(w_x), xpart.shape[-1], _ptr(xpart), m, d, D,
+              _stream())
+
+
+def xpart_dt_scan_step(xpart, s_x: int, dt_rank: int, w_dt, s_dt: int, xs, z, z_off: int, base,
+                       decay_shift: int, s_y: int, h_state, yo) -> None:
+    """Decode stage: x_proj from per-block partials + dt_proj + decay + dt + scan step + gate -> yo."""
+    for t, nm in ((xs, "xs"), (z, "z"), (yo, "yo")):
+        _req(t, torch.int8, nm)
+    _req(xpart, torch.int32, "xpart"); _req(w_dt, torch.uint8, "w_dt")
+    _req(base, torch.int32, "base"); _req(h_state, torch.int32, "h_state")
+    m = xs.shape[0]
+    D, N = base.shape
+    if xpart.shape[0] != m or xpart.shape[-1] != dt_rank + 2 * N:
+        raise ValueError(f"xpart must be [m, nblk, dt_rank + 2*d_state], got {tuple(xpart.shape)}")
+    _lib.call("mi_xpart_dt_scan_step", _ptr(xpart), xpart.shape[1], s_x, dt_rank, _ptr(w_dt), s_dt, _ptr(xs),
+              _ptr(z), z.shape[-1], z_off, _ptr(base), decay_shift, s_y, _ptr(h_state), _ptr(yo), m, D, N,
               _stream())
 
 

@@ -134,3 +134,56 @@ def test_xproj_dt_scan_step(cuda, m, D, N, R):
     ops.xproj_dt_scan_step(T(xs), T(wx), 5, R, T(wdt), 2, T(z), D, T(base), 15, 13, hg, yo)
     assert np.array_equal(H(yo), yo_ref[:, 0])
     assert np.array_equal(H(hg), h_ref)
+
+
+@pytest.mark.parametrize("m,d,D,N,R,stats", [(8, 768, 1536, 16, 48, True), (1, 128, 256, 16, 16, False),
+                                             (16, 256, 512, 32, 32, True), (3, 64, 96, 8, 16, True),
+                                             (5, 512, 1024, 64, 128, False)])
+def test_xpart_decode_chain(cuda, m, d, D, N, R, stats):
+    """norm + in_proj + conv with x_proj partials, then the scan step from those
+    partials, equals the unfused oracle chain (norm, in_proj, conv, x_proj,
+    dt_proj, block scan)."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m * d + D + N + R)
+    NX = R + 2 * N
+    r = _resid(rng, m, d)
+    g = rng.integers(100, 400, size=d, dtype=np.int16)
+    wp = pack_ternary(rng.integers(-1, 2, size=(2 * D, d), dtype=np.int8))
+    cw = i8(rng, D, 4)
+    cb = rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, m, 3, D)
+    wx_t = rng.integers(-1, 2, size=(NX, D), dtype=np.int8)
+    wx = pack_ternary(wx_t)
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    h0 = rng.integers(-(2**22), 2**22, size=(m, D, N), dtype=np.int32)
+    # oracle chain
+    xz_ref = O.bitlinear(O.bitshift_norm(r, g), wp, O.OUT_INT8, 4)
+    xs_ref, st_ref = O.conv_squareplus(xz_ref.reshape(m, 1, 2 * D), D, cw, cb, st)
+    xs_ref = xs_ref[:, 0]
+    part_ref = np.einsum("nbc,ibc->ibn", wx_t.reshape(NX, D // 16, 16).astype(np.int64),
+                         xs_ref.reshape(m, D // 16, 16).astype(np.int64))
+    xp = O.bitlinear(xs_ref, wx, O.OUT_INT8, 5)
+    dm = O.bitlinear(np.ascontiguousarray(xp[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs_ref.reshape(m, 1, D), dm.reshape(m, 1, D), xp.reshape(m, 1, NX), R,
+                                 xz_ref.reshape(m, 1, 2 * D), D, base, 15, 13, h_state=h0)
+    # device chain
+    rs = None
+    if stats:
+        r64 = r.astype(np.int64)
+        rs = T(np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+    stg = T(st)
+    xs = torch.zeros((m, D), dtype=torch.int8, device="cuda")
+    xz = torch.zeros((m, 2 * D), dtype=torch.int8, device="cuda")
+    xpart = torch.full((m, D // 16, NX), 7, dtype=torch.int32, device="cuda")
+    ops.norm_in_proj_conv(T(r), T(g), T(wp), 4, T(cw), T(cb), stg, xs, xz, row_stats=rs, w_x=T(wx), xpart=xpart)
+    assert np.array_equal(H(xs), xs_ref)
+    assert np.array_equal(H(stg), st_ref)
+    assert np.array_equal(H(xz)[:, D:], xz_ref[:, D:])
+    assert np.array_equal(H(xpart), part_ref)
+    hg = T(h0)
+    yo = T(np.zeros((m, D), np.int8))
+    ops.xpart_dt_scan_step(xpart, 5, R, T(wdt), 2, xs, xz, D, T(base), 15, 13, hg, yo)
+    assert np.array_equal(H(yo), yo_ref[:, 0])
+    assert np.array_equal(H(hg), h_ref)
