@@ -414,6 +414,74 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
     }
 }
 
+// ------------------------------------------- decode RESIDUAL GEMV, m <= 16
+// The out_proj of one decode step (a few tokens): 16 features per block, 8
+// waves taking 16-word chunks of K (c, c+8, ...).  In a chunk, lane (row
+// l16, group lq) reads words [16c+4lq, 16c+4lq+4) of weight row n0+l16 in one
+// 16-byte load and the 64 activation bytes of the same k of token l16, so
+// every load is issued before the first MFMA and none is conditional: a
+// token or feature index past the end is clamped, and its results are not
+// stored.  The residual each output overwrites is read at kernel start.
+// Requires kw % 16 == 0, 16-byte aligned w, a and lda.
+__global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g) {
+    __shared__ int32_t red[8][64][4];
+    __shared__ int32_t s_new[16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int nchunk = g.kw / 16;
+    // output element of threads 0..255: token l16, feature n0 + 4lq + wave
+    const int en = n0 + 4 * lq + (wave & 3);
+    const bool eok = tid < 256 && l16 < g.M && en < g.N;
+    int32_t *rp = (int32_t *)g.out + (int64_t)min(l16, g.M - 1) * g.ldo + min(en, g.N - 1);
+    const int32_t rold = *rp;
+    const uint32_t *wrow = g.w + (int64_t)min(n0 + l16, g.N - 1) * g.kw;
+    const int8_t *arow = g.a + (int64_t)min(l16, g.M - 1) * g.lda;
+    v4i acc = v4i{0, 0, 0, 0};
+    for (int c0 = wave; c0 < nchunk; c0 += 16) {
+        v4i wv[2], xv[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = c0 + 8 * u < nchunk ? c0 + 8 * u : c0;
+            const int w = 16 * c + 4 * lq;
+            wv[u] = *reinterpret_cast<const v4i *>(wrow + w);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[u][j] = *reinterpret_cast<const v4i *>(arow + 16 * (w + j));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (c0 + 8 * u < nchunk)  // same for the whole wave
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc = mfma_i8(unpack16((uint32_t)wv[u][j]), xv[u][j], acc);
+    }
+    *reinterpret_cast<v4i *>(&red[wave][lane][0]) = acc;
+    __syncthreads();
+    if (tid < 256) {
+        const int r = wave;  // register r of the MFMA result = feature 4lq + r
+        int32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) v += red[w][lane][r];
+        const int64_t delta = rshr64((int64_t)v * g.res_mult, g.res_shift);
+        const int32_t nv = (int32_t)clamp64((int64_t)rold + delta, -kResidualLimit, kResidualLimit);
+        if (eok) *rp = nv;
+        s_new[l16][4 * lq + r] = eok ? nv : 0;
+    }
+    if (g.row_stats) {
+        __syncthreads();
+        if (tid < g.M) {
+            int64_t s1 = 0, s2 = 0;
+#pragma unroll
+            for (int f = 0; f < 16; ++f) {
+                const int64_t v = s_new[tid][f];
+                s1 += v;
+                s2 += v * v;
+            }
+            atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)tid), (unsigned long long)s1);
+            atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)tid + 1),
+                      (unsigned long long)s2);
+        }
+    }
+}
+
 // ------------------------------------------------------------ helpers
 __global__ void pack_ternary_kernel(const int8_t *w, uint32_t *p, int64_t words, int kw) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -512,6 +580,11 @@ hipError_t launch_gemv_mt(const GemmArgs &g, hipStream_t st) {
 
 template <int KIND>
 hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
+    if (KIND == MI_OUT_RESIDUAL && g.M <= 16 && g.kw % 16 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
+        g.lda % 16 == 0) {
+        hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((g.N + 15) / 16)), dim3(512), 0, st, g);
+        return hipGetLastError();
+    }
     if (g.M <= 16) return launch_gemv_mt<1, KIND>(g, st);
     if (g.M <= 32) return launch_gemv_mt<2, KIND>(g, st);
     return launch_gemv_mt<4, KIND>(g, st);

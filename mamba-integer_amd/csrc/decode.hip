@@ -57,13 +57,21 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 // [M][K] rows; the loads of a whole chunk of groups are issued before the
 // first wait, and threads 0..M-1 turn the row statistics into (mu, shift) in
 // LDS meanwhile.  Without: one wave per row sums the row in one pass.
-__device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch) {
+// Threads per row of the stats-driven staging: rows padded to a power of two
+// Mp, TPR = 256/Mp threads each.
+__device__ __forceinline__ int norm_tpr(int M) {
+    const int Mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
+    return 256 / Mp;
+}
+
+// (s1, s2): the row statistics of this thread's row min(threadIdx.x / TPR,
+// M - 1), loaded by the caller ahead of its other loads (used with row_stats).
+__device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, int64_t s1, int64_t s2) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (g.row_stats) {
-        // rows padded to a power of two Mp; TPR = 256/Mp threads per row, each
-        // with its row's (mu, shift) in registers and groups tr, tr+TPR, ...
-        const int Mp = g.M <= 1 ? 1 : g.M <= 2 ? 2 : g.M <= 4 ? 4 : g.M <= 8 ? 8 : 16;
-        const int TPR = 256 / Mp;
+        // TPR threads per row, each with its row's (mu, shift) in registers
+        // and groups tr, tr+TPR, ...
+        const int TPR = norm_tpr(g.M);
         const int m = (int)threadIdx.x / TPR, tr = (int)threadIdx.x - m * TPR;
         const int mr = min(m, g.M - 1);
         const int K4 = g.K / 4;
@@ -81,7 +89,7 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch) {
         };
         load_chunk(0);
         int64_t mu64;
-        const int sh = norm_shift(g.row_stats[2 * mr], g.row_stats[2 * mr + 1], g.K, &mu64);
+        const int sh = norm_shift(s1, s2, g.K, &mu64);
         const int32_t mu = (int32_t)mu64;
         const int64_t rnd = (int64_t)1 << (sh - 1);
         const int ngrp = (K4 + TPR - 1) / TPR;
@@ -113,16 +121,16 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch) {
     }
     for (int m = wave; m < g.M; m += 4) {
         const int32_t *row = g.r + (int64_t)m * g.K;
-        int64_t s1 = 0, s2 = 0;
+        int64_t t1 = 0, t2 = 0;
         for (int i = lane; i < g.K; i += 64) {
             const int64_t v = row[i];
-            s1 += v;
-            s2 += v * v;
+            t1 += v;
+            t2 += v * v;
         }
-        s1 = wave_sum64(s1);
-        s2 = wave_sum64(s2);
+        t1 = wave_sum64(t1);
+        t2 = wave_sum64(t2);
         int64_t mu;
-        const int sh = norm_shift(s1, s2, g.K, &mu);
+        const int sh = norm_shift(t1, t2, g.K, &mu);
         for (int i = 4 * lane; i < g.K; i += 256) {
             const int4 v = *reinterpret_cast<const int4 *>(row + i);
             const int vv[4] = {v.x, v.y, v.z, v.w};
@@ -149,10 +157,17 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
     extern __shared__ __align__(16) int8_t smem[];
     const int pitch = g.K + 16;                       // conflict-free b128 row reads
     int8_t *a = smem;                                 // [16][pitch]
-    v4i *red = reinterpret_cast<v4i *>(smem + kMaxRows * pitch);  // [3][64]
+    v4i *red = reinterpret_cast<v4i *>(smem + kMaxRows * pitch);  // [4][64]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lq = lane >> 4;
+    // the row statistics of this thread's staging row, before any other load
+    int64_t rs1 = 0, rs2 = 0;
+    if (g.row_stats) {
+        const int mr = min(tid / norm_tpr(g.M), g.M - 1);
+        rs1 = g.row_stats[2 * mr];
+        rs2 = g.row_stats[2 * mr + 1];
+    }
     const int n0 = WIDE ? blockIdx.x * 64 + wave * 16 : blockIdx.x * 16;
     const int n = n0 + l16;
     const int nsuper = (g.kw + 15) / 16;
@@ -171,9 +186,23 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
     const int m = l16;
     const int nf = n0 + 4 * lq;
     const bool epi = (WIDE || wave == 0) && m < g.M && nf < g.N;
-    const bool conv = CONV && epi && nf < g.conv_d;
+    const bool conv = CONV && WIDE && epi && nf < g.conv_d;
     uint32_t cs0 = 0, cs1 = 0, cs2 = 0, cw[4] = {0, 0, 0, 0};
     int32_t cb[4] = {0, 0, 0, 0};
+    // narrow conv kernel: every thread owns one output (token l16, feature
+    // n0 + 4lq + wave) of an x-block and prefetches that channel's operands
+    const bool xblk = CONV && !WIDE && n0 < g.conv_d;
+    int ecs0 = 0, ecs1 = 0, ecs2 = 0, ecb = 0;
+    uint32_t ecw = 0;
+    if (xblk) {
+        const int ch = nf + wave;  // < conv_d: conv_d % 16 == 0
+        const int8_t *st = g.conv_state + (int64_t)min(m, g.M - 1) * 3 * g.conv_d + ch;
+        ecs0 = st[0];
+        ecs1 = st[g.conv_d];
+        ecs2 = st[2 * g.conv_d];
+        ecw = *reinterpret_cast<const uint32_t *>(g.conv_w + (int64_t)ch * 4);
+        ecb = g.conv_b[ch];
+    }
     if (conv) {
         const int8_t *st = g.conv_state + (int64_t)m * 3 * g.conv_d;
         cs0 = *reinterpret_cast<const uint32_t *>(st + nf);
@@ -195,7 +224,7 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
             wx[t] = 16 * t < g.nx ? g.w_x[(int64_t)min(16 * t + l16, g.nx - 1) * xkw + n0 / 16] : 0u;
     }
 
-    stage_norm_rows(g, a, pitch);
+    stage_norm_rows(g, a, pitch, rs1, rs2);
     __syncthreads();
 
     v4i acc = v4i{0, 0, 0, 0};
@@ -213,53 +242,76 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
             }
         }
     }
+    if constexpr (CONV && !WIDE) {
+        // all four waves finish the block: thread (wave, lane) takes output
+        // (token l16, feature n0 + 4lq + wave), the MFMA result register
+        // `wave` summed over the four waves' partial products
+        red[wave * 64 + lane] = acc;
+        __syncthreads();
+        const int32_t v = red[lane][wave] + red[64 + lane][wave] + red[128 + lane][wave] + red[192 + lane][wave];
+        const int q = clamp32(rshr32(v, g.shift), -127, 127);
+        const int fe = nf + wave;
+        const bool ok = m < g.M && fe < g.N;
+        if (!xblk) {
+            if (ok) reinterpret_cast<int8_t *>(g.out)[(int64_t)m * g.ldo + fe] = (int8_t)q;  // z half
+            return;
+        }
+        // depthwise conv step (conv1d_step.cu:30-57) + squareplus of one channel
+        int xsv = 0;
+        if (ok) {
+            const int32_t c = ecb + (int)(int8_t)ecw * ecs0 + (int)(int8_t)(ecw >> 8) * ecs1 +
+                              (int)(int8_t)(ecw >> 16) * ecs2 + (int)(int8_t)(ecw >> 24) * q;
+            xsv = sqp_q(c);
+            g.xs[(int64_t)m * g.conv_d + fe] = (int8_t)xsv;
+            int8_t *st = g.conv_state + (int64_t)m * 3 * g.conv_d + fe;
+            st[0] = (int8_t)ecs1;
+            st[g.conv_d] = (int8_t)ecs2;
+            st[2 * g.conv_d] = (int8_t)q;
+        }
+        if (!xpart) return;
+        // the block's x_proj partial: one MFMA per 16 x_proj rows with K = the
+        // block's 16 channels (lane group lq carries channels 4lq..4lq+3 in
+        // its first dword, the other k slots are zero)
+        __shared__ uint32_t s_xs[16][4];
+        reinterpret_cast<int8_t *>(&s_xs[m][lq])[wave] = (int8_t)xsv;
+        __syncthreads();
+        if (wave != 0) return;
+        const v4i fb = v4i{(int)s_xs[l16][lq], 0, 0, 0};
+        const uint32_t lut = 0xFFFE0100u;
+        const int nblk = g.conv_d / 16;
+        int32_t *dst = g.xpart + ((int64_t)m * nblk + blockIdx.x) * g.nx;
+        // every product first, then the stores back to back (a store between
+        // two MFMAs would make the next wait on its completion)
+        v4i d[kMaxXTiles];
+#pragma unroll
+        for (int t = 0; t < kMaxXTiles; ++t) {
+            if (16 * t < g.nx) {
+                const v4i fa = v4i{(int)__builtin_amdgcn_perm(lut, lut, (wx[t] >> (2 * lq)) & 0x03030303u), 0, 0, 0};
+                d[t] = mfma_i8(fa, fb, v4i{0, 0, 0, 0});
+            }
+        }
+        // lane (token l16, group lq) holds rows 16t + 4lq + r
+        if (m < g.M) {
+#pragma unroll
+            for (int t = 0; t < kMaxXTiles; ++t) {
+                const int row = 16 * t + 4 * lq;
+                if (16 * t < g.nx) {
+                    if ((g.nx & 3) == 0 && row + 3 < g.nx) {
+                        *reinterpret_cast<v4i *>(dst + row) = d[t];
+                    } else {
+                        for (int r = 0; r < 4; ++r)
+                            if (row + r < g.nx) dst[row + r] = d[t][r];
+                    }
+                }
+            }
+        }
+        return;
+    }
     if (!WIDE) {
         if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
         __syncthreads();
         if (wave != 0) return;
         acc = acc + red[lane] + red[64 + lane] + red[128 + lane];
-    }
-    if constexpr (CONV && !WIDE) {
-        if (xpart) {
-            // conv + squareplus for every lane of wave 0 (zeros where idle),
-            // then the block's x_proj partial: one MFMA per 16 x_proj rows with
-            // K = this block's 16 channels (lane group lq carries channels
-            // 4lq..4lq+3 in its first dword, the other k slots are zero)
-            uint32_t xsw = 0, cur = 0;
-            if (conv) {
-                for (int r = 0; r < 4; ++r) {
-                    const int v = clamp32(rshr32(acc[r], g.shift), -127, 127);
-                    int32_t c = cb[r];
-                    c += (int)(int8_t)(cw[r]) * (int)(int8_t)(cs0 >> (8 * r));
-                    c += (int)(int8_t)(cw[r] >> 8) * (int)(int8_t)(cs1 >> (8 * r));
-                    c += (int)(int8_t)(cw[r] >> 16) * (int)(int8_t)(cs2 >> (8 * r));
-                    c += (int)(int8_t)(cw[r] >> 24) * v;
-                    xsw |= (uint32_t)(sqp_q(c) & 255) << (8 * r);
-                    cur |= (uint32_t)(v & 255) << (8 * r);
-                }
-                int8_t *st = g.conv_state + (int64_t)m * 3 * g.conv_d;
-                *reinterpret_cast<uint32_t *>(g.xs + (int64_t)m * g.conv_d + nf) = xsw;
-                *reinterpret_cast<uint32_t *>(st + nf) = cs1;
-                *reinterpret_cast<uint32_t *>(st + g.conv_d + nf) = cs2;
-                *reinterpret_cast<uint32_t *>(st + 2 * g.conv_d + nf) = cur;
-            }
-            const v4i fb = v4i{(int)xsw, 0, 0, 0};
-            const uint32_t lut = 0xFFFE0100u;
-            const int nblk = g.conv_d / 16;
-            int32_t *dst = g.xpart + ((int64_t)m * nblk + blockIdx.x) * g.nx;
-#pragma unroll
-            for (int t = 0; t < kMaxXTiles; ++t) {
-                if (16 * t < g.nx) {
-                    const v4i fa = v4i{(int)__builtin_amdgcn_perm(lut, lut, (wx[t] >> (2 * lq)) & 0x03030303u), 0, 0, 0};
-                    const v4i d = mfma_i8(fa, fb, v4i{0, 0, 0, 0});
-                    // lane (token l16, group lq) holds rows 16t + 4lq + r
-                    if (m < g.M)
-                        for (int r = 0; r < 4; ++r)
-                            if (16 * t + 4 * lq + r < g.nx) dst[16 * t + 4 * lq + r] = d[r];
-                }
-            }
-            return;
-        }
     }
     if (!epi) return;
     if constexpr (KIND == MI_OUT_INT32) {
@@ -607,7 +659,7 @@ mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma
     return MI_OK;
 }
 
-size_t norm_gemv_lds(int k) { return (size_t)kMaxRows * (k + 16) + 3 * 64 * sizeof(v4i); }
+size_t norm_gemv_lds(int k) { return (size_t)kMaxRows * (k + 16) + 4 * 64 * sizeof(v4i); }
 
 }  // namespace
 }  // namespace mi
@@ -664,7 +716,8 @@ mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t
         MI_REQUIRE(w_x, MI_ERR_NULL_POINTER, "%s: w_x is required with xpart", fn);
         MI_REQUIRE(nx >= 1 && nx <= 16 * kMaxXTiles, MI_ERR_BAD_DIM, "%s: nx=%d outside [1,%d]", fn, nx,
                    16 * kMaxXTiles);
-        MI_REQUIRE(aligned(w_x, 4), MI_ERR_BAD_ALIGNMENT, "%s: w_x must be 4-byte aligned", fn);
+        MI_REQUIRE(aligned(w_x, 4) && aligned(xpart, 16), MI_ERR_BAD_ALIGNMENT,
+                   "%s: w_x must be 4-byte and xpart 16-byte aligned", fn);
     }
     NormGemvArgs g{};
     g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_in); g.out = xz;

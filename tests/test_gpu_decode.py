@@ -187,3 +187,23 @@ def test_xpart_decode_chain(cuda, m, d, D, N, R, stats):
     ops.xpart_dt_scan_step(xpart, 5, R, T(wdt), 2, xs, xz, D, T(base), 15, 13, hg, yo)
     assert np.array_equal(H(yo), yo_ref[:, 0])
     assert np.array_equal(H(hg), h_ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 768, 1536), (1, 768, 1536), (16, 100, 512), (3, 2048, 4096), (5, 20, 256),
+                                   (16, 64, 256 * 13)])
+def test_decode_residual_gemv(cuda, m, n, k):
+    """The decode out_proj (RESIDUAL, m <= 16, K a multiple of 256): residual
+    update and the atomically added row statistics of the new rows."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m * n + k)
+    a = i8(rng, m, k)
+    wp = pack_ternary(rng.integers(-1, 2, size=(n, k), dtype=np.int8))
+    r0 = rng.integers(-(2**23) + 1, 2**23, size=(m, n), dtype=np.int32)
+    ref = O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0, res_mult=4719, res_shift=16)
+    rt = T(r0)
+    stats = torch.zeros((m, 2), dtype=torch.int64, device="cuda")
+    ops.bitlinear(T(a), T(wp), ops.OUT_RESIDUAL, n, out=rt, res_mult=4719, res_shift=16, row_stats=stats)
+    assert np.array_equal(H(rt), ref)
+    r64 = ref.astype(np.int64)
+    assert np.array_equal(H(stats), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
