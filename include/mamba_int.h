@@ -258,6 +258,25 @@ mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s_x, int dt_
                                 const int32_t *base, int decay_shift, int s_y, int32_t *h_state, int8_t *yo,
                                 int m, int d_inner, int nstate, void *stream);
 
+/* ------------------------------------------------ greedy pick */
+/* The generation loop's argmax (scripts/inference.py:147-161, torch.argmax
+ * over the last logits) fused into the lm_head: mi_norm_bitlinear (INT32)
+ * in 64-output blocks, each block also writing for every row i its partial
+ * key keys[i, b] = max over its outputs j of (logit << 32 | 0x7FFFFFFF - j),
+ * so the largest key of a row names its first maximal index.  keys int64
+ * [m, ceil(n/64)]; logits int32 [m, ldo] or NULL (then not stored). */
+mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                   const uint8_t *w_packed, int32_t *logits, int ldo, int64_t *keys, int m,
+                                   int n, int k, void *stream);
+
+/* ids[i] = the index the largest of keys[i, 0:nkeys] names (int64 out). */
+mi_status mi_argmax_keys(const int64_t *keys, int nkeys, int64_t *ids, int rows, void *stream);
+
+/* mi_argmax_keys, then mi_embed (with row statistics) of the picked ids;
+ * the ids are written to ids. */
+mi_status mi_embed_argmax(const int64_t *keys, int nkeys, int64_t *ids, const int8_t *emb, int32_t *r,
+                          int tokens, int dim, int vocab, int64_t *row_stats, int stats_layers, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -145,6 +145,62 @@ __global__ __launch_bounds__(256) void embed_stats_kernel(const int64_t *ids, co
     }
 }
 
+// Greedy pick of row t from per-block partial keys (logit << 32 | 0x7FFFFFFF -
+// index): the largest key, decoded to its index, returned to every thread.
+__device__ int64_t block_pick(const int64_t *keys, int nkeys) {
+    __shared__ int64_t s_best[4];
+    int64_t best = INT64_MIN;
+    for (int i = threadIdx.x; i < nkeys; i += 256) best = max(best, keys[i]);
+    for (int off = 32; off > 0; off >>= 1) best = max(best, (int64_t)__shfl_xor(best, off));
+    if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    best = max(max(s_best[0], s_best[1]), max(s_best[2], s_best[3]));
+    return 0x7FFFFFFF - (int64_t)(uint32_t)(best & 0xFFFFFFFF);
+}
+
+__global__ __launch_bounds__(256) void argmax_keys_kernel(const int64_t *keys, int nkeys, int64_t *ids) {
+    const int64_t t = blockIdx.x;
+    const int64_t id = block_pick(keys + t * nkeys, nkeys);
+    if (threadIdx.x == 0) ids[t] = id;
+}
+
+// Greedy pick of the previous step's logits, then the embedding row of the
+// picked id with its row statistics (embed_stats_kernel of that id).
+__global__ __launch_bounds__(256) void embed_argmax_kernel(const int64_t *keys, int nkeys, int64_t *ids,
+                                                           const int8_t *emb, int32_t *r, int tokens, int dim,
+                                                           int vocab, int64_t *stats, int stats_layers) {
+    __shared__ int64_t red[2][4];
+    const int64_t t = blockIdx.x;
+    const int64_t id = block_pick(keys + t * nkeys, nkeys);
+    if (threadIdx.x == 0) ids[t] = id;
+    const bool ok = id >= 0 && id < vocab;
+    int64_t s1 = 0, s2 = 0;
+    for (int c = threadIdx.x; c < dim; c += 256) {
+        const int32_t v = ok ? (int32_t)emb[id * dim + c] * 16 : 0;
+        r[t * dim + c] = v;
+        s1 += v;
+        s2 += (int64_t)v * v;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += __shfl_xor(s1, off);
+        s2 += __shfl_xor(s2, off);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wave] = s1;
+        red[1][wave] = s2;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        stats[2 * t] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+        stats[2 * t + 1] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    }
+    for (int j = 1 + (int)threadIdx.x; j < stats_layers; j += 256) {
+        stats[((int64_t)j * tokens + t) * 2] = 0;
+        stats[((int64_t)j * tokens + t) * 2 + 1] = 0;
+    }
+}
+
 // Elementwise BitShiftNorm from precomputed row statistics: thread = 4 channels.
 __global__ __launch_bounds__(256) void norm_stats_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
                                                          const int64_t *stats, int tokens, int dim) {
@@ -355,4 +411,27 @@ extern "C" mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, 
     hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), logits, (int64_t)ld, out,
                        cols, vec);
     return check_launch("mi_argmax_i32");
+}
+
+extern "C" mi_status mi_argmax_keys(const int64_t *keys, int nkeys, int64_t *ids, int rows, void *stream) {
+    clear_error();
+    MI_REQUIRE(rows >= 0 && nkeys >= 1, MI_ERR_BAD_DIM, "mi_argmax_keys: rows=%d, nkeys=%d", rows, nkeys);
+    if (rows == 0) return MI_OK;
+    MI_REQUIRE(keys && ids, MI_ERR_NULL_POINTER, "mi_argmax_keys: keys and ids are required");
+    hipLaunchKernelGGL(argmax_keys_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), keys, nkeys, ids);
+    return check_launch("mi_argmax_keys");
+}
+
+extern "C" mi_status mi_embed_argmax(const int64_t *keys, int nkeys, int64_t *ids, const int8_t *emb, int32_t *r,
+                                     int tokens, int dim, int vocab, int64_t *row_stats, int stats_layers,
+                                     void *stream) {
+    clear_error();
+    MI_REQUIRE(tokens >= 0 && dim >= 0 && vocab >= 0 && nkeys >= 1, MI_ERR_BAD_DIM, "mi_embed_argmax: bad size");
+    if ((int64_t)tokens * dim == 0) return MI_OK;
+    MI_REQUIRE(keys && ids && emb && r && row_stats, MI_ERR_NULL_POINTER,
+               "mi_embed_argmax: keys, ids, emb, r and row_stats are required");
+    MI_REQUIRE(stats_layers >= 1, MI_ERR_BAD_ARG, "mi_embed_argmax: stats_layers=%d must be >= 1", stats_layers);
+    hipLaunchKernelGGL(embed_argmax_kernel, dim3((unsigned)tokens), dim3(256), 0, as_stream(stream), keys, nkeys, ids,
+                       emb, r, tokens, dim, vocab, row_stats, stats_layers);
+    return check_launch("mi_embed_argmax");
 }

@@ -45,6 +45,9 @@ struct NormGemvArgs {
     const uint32_t *w_x;    // [nx][conv_d/16] words
     int nx;
     int32_t *xpart;
+    // greedy-pick partials of the wide INT32 kernel (optional): keys[m][block]
+    // = largest (logit << 32 | 0x7FFFFFFF - index) over the block's outputs
+    int64_t *keys;
 };
 
 __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
@@ -312,6 +315,25 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
         __syncthreads();
         if (wave != 0) return;
         acc = acc + red[lane] + red[64 + lane] + red[128 + lane];
+    }
+    if constexpr (WIDE && KIND == MI_OUT_INT32) {
+        if (g.keys) {
+            // the larger logit wins; among equal logits the smaller index
+            __shared__ int64_t s_key[4][16];
+            int64_t best = INT64_MIN;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (nf + r < g.N)
+                    best = max(best, (int64_t)(((uint64_t)(int64_t)acc[r] << 32) | (uint32_t)(0x7FFFFFFF - (nf + r))));
+            best = max(best, (int64_t)__shfl_xor(best, 16));
+            best = max(best, (int64_t)__shfl_xor(best, 32));
+            if (lq == 0) s_key[wave][l16] = best;
+            __syncthreads();
+            if (tid < g.M)
+                g.keys[(int64_t)tid * gridDim.x + blockIdx.x] =
+                    max(max(s_key[0][tid], s_key[1][tid]), max(s_key[2][tid], s_key[3][tid]));
+            if (g.out == nullptr) return;
+        }
     }
     if (!epi) return;
     if constexpr (KIND == MI_OUT_INT32) {
@@ -694,6 +716,24 @@ extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stat
         else hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, false, false>), grid, dim3(256), lds, hs, g);
     }
     return check_launch("mi_norm_bitlinear");
+}
+
+extern "C" mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
+                                              const uint8_t *w_packed, int32_t *logits, int ldo, int64_t *keys, int m,
+                                              int n, int k, void *stream) {
+    clear_error();
+    mi_status st = check_norm_gemv("mi_norm_bitlinear_argmax", r, gamma, w_packed, m, n, k);
+    if (st != MI_OK || (int64_t)m * n == 0) return st;
+    MI_REQUIRE(keys, MI_ERR_NULL_POINTER, "mi_norm_bitlinear_argmax: keys is required");
+    MI_REQUIRE(!logits || ldo >= n, MI_ERR_BAD_DIM, "mi_norm_bitlinear_argmax: ldo=%d < n=%d", ldo, n);
+    MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "mi_norm_bitlinear_argmax: r must be 16-byte aligned");
+    NormGemvArgs g{};
+    g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_packed);
+    g.out = logits; g.ldo = ldo; g.keys = keys;
+    g.M = m; g.N = n; g.K = k; g.kw = k / 16; g.shift = 0;
+    hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT32, false, true>), dim3((unsigned)((n + 63) / 64)), dim3(256),
+                       norm_gemv_lds(k), as_stream(stream), g);
+    return check_launch("mi_norm_bitlinear_argmax");
 }
 
 namespace mi {

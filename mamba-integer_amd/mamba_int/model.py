@@ -94,7 +94,7 @@ class IntegerMambaRunner:
         self.gamma_f = _dev(params.gamma_f, dv)
         self.w_head = _dev(params.w_head, dv)
         self._ws: Dict[int, _Workspace] = {}
-        self._graphs: Dict[int, tuple] = {}
+        self._graphs: Dict[object, object] = {}
         # optional (before, after) callables around every fused scan launch
         # (the bench times that kernel with events on the launch stream)
         self.scan_timer = None
@@ -241,6 +241,9 @@ class IntegerMambaRunner:
                 tok = ops.argmax(logits)
                 out[:, i] = tok
             return out
+        if self._chain_ok(B):
+            self._decode_chain_loop(tok, state, out)
+            return out
         step = self._decode_graph(B, state)
         step.tok_in.copy_(tok)
         for i in range(1, n_new):
@@ -251,6 +254,87 @@ class IntegerMambaRunner:
             state.conv[i].copy_(step.state.conv[i])
             state.h[i].copy_(step.state.h[i])
         return out
+
+    # ------------------------------------------------- multi-step decode graphs
+    GRAPH_STEPS = 16
+
+    def _chain_ok(self, B: int) -> bool:
+        """The fused chain (three kernels per layer, argmax fused into the head) fits batch B."""
+        return self._fused_decode_ok(B) and self.dims.d_model <= 3072 and self._workspace(B).xpart is not None
+
+    def _decode_chain(self, ws: _Workspace, state: DecodeState, hist: torch.Tensor, keys: torch.Tensor) -> None:
+        """len(hist) greedy steps.  Step 0 embeds hist[-1] (the previous pick); step j > 0
+        picks from step j-1's head keys, writing the pick to hist[j-1], and embeds it;
+        the last step's pick goes to hist[-1]."""
+        S = hist.shape[0]
+        V = self.dims.vocab_size
+        for j in range(S):
+            if j == 0:
+                ops.embed(hist[S - 1], self.emb, out=ws.r, row_stats=ws.stats)
+            else:
+                ops.embed_argmax(keys, hist[j - 1], self.emb, ws.r, ws.stats)
+            for i, ly in enumerate(self.layers):
+                self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
+            ops.norm_bitlinear_argmax(ws.r, self.gamma_f, self.w_head, V, keys, row_stats=ws.stats[-1])
+        ops.argmax_keys(keys, out=hist[S - 1])
+
+    def _chain_graph(self, B: int, S: int):
+        """HIP graph of S chained greedy steps for batch B (state, workspace and keys shared
+        by every S; hist [S, B] of its own)."""
+        g = self._graphs.get((B, S))
+        if g is not None:
+            return g
+        shared = self._graphs.get((B, "shared"))
+        if shared is None:
+            nk = (self.dims.vocab_size + 63) // 64
+            shared = (self.new_state(B), torch.empty((B, nk), dtype=torch.int64, device=self.device))
+            self._graphs[(B, "shared")] = shared
+        gstate, keys = shared
+        ws = self._workspace(B)
+        hist = torch.zeros((S, B), dtype=torch.int64, device=self.device)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            # one eager pass first: every kernel is loaded before capture
+            self._decode_chain(ws, gstate, hist, keys)
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                self._decode_chain(ws, gstate, hist, keys)
+        torch.cuda.current_stream().wait_stream(side)
+        g = (graph, hist, gstate)
+        self._graphs[(B, S)] = g
+        return g
+
+    def _decode_chain_loop(self, tok: torch.Tensor, state: DecodeState, out: torch.Tensor) -> None:
+        """Fills out[:, 1:] by replaying chain graphs of GRAPH_STEPS steps (and one of the
+        remainder), starting from pick `tok` and `state`; the state is handed back."""
+        B, n_new = out.shape
+        if n_new <= 1:
+            return
+        # every graph this run replays is captured first: capture runs an eager
+        # pass over the shared graph state, which must not happen mid-run
+        sizes = [min(self.GRAPH_STEPS, n_new - i) for i in range(1, n_new, self.GRAPH_STEPS)]
+        for S in set(sizes):
+            self._chain_graph(B, S)
+        gstate = self._chain_graph(B, sizes[0])[2]
+        for li in range(len(self.layers)):
+            gstate.conv[li].copy_(state.conv[li])
+            gstate.h[li].copy_(state.h[li])
+        i = 1
+        prev = tok
+        for S in sizes:
+            graph, hist, _ = self._chain_graph(B, S)
+            if prev.data_ptr() != hist[S - 1].data_ptr():
+                hist[S - 1].copy_(prev)
+            graph.replay()
+            out[:, i:i + S] = hist.t()
+            prev = hist[S - 1]
+            i += S
+        for li in range(len(self.layers)):
+            state.conv[li].copy_(gstate.conv[li])
+            state.h[li].copy_(gstate.h[li])
 
     def _decode_body(self, ws: _Workspace, state: DecodeState, tok: torch.Tensor, logits: torch.Tensor,
                      tok_out: torch.Tensor) -> None:

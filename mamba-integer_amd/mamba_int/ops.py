@@ -278,3 +278,39 @@ def xproj_dt_scan_step(xs, w_x, s_x: int, dt_rank: int, w_dt, s_dt: int, z, z_of
     D, N = base.shape
     _lib.call("mi_xproj_dt_scan_step", _ptr(xs), _ptr(w_x), s_x, dt_rank, _ptr(w_dt), s_dt, _ptr(z),
               z.shape[-1], z_off, _ptr(base), decay_shift, s_y, _ptr(h_state), _ptr(yo), m, D, N, _stream())
+
+
+def norm_bitlinear_argmax(r, gamma, w_packed, n: int, keys, logits=None, row_stats=None) -> None:
+    """lm_head (norm + INT32 GEMV) writing per-64-output partial argmax keys [m, ceil(n/64)]
+    and, when given, the logits."""
+    _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma"); _req(w_packed, torch.uint8, "w_packed")
+    _req(keys, torch.int64, "keys")
+    m, k = r.shape
+    if tuple(keys.shape) != (m, (n + 63) // 64):
+        raise ValueError(f"keys must be [{m}, {(n + 63) // 64}], got {tuple(keys.shape)}")
+    ldo = 0
+    if logits is not None:
+        _req(logits, torch.int32, "logits")
+        ldo = logits.stride(0)
+    _lib.call("mi_norm_bitlinear_argmax", _ptr(r), _ptr(_opt(row_stats, torch.int64, "row_stats")), _ptr(gamma),
+              _ptr(w_packed), _ptr(logits) if logits is not None else None, ldo, _ptr(keys), m, n, k, _stream())
+
+
+def argmax_keys(keys, out=None) -> torch.Tensor:
+    """ids [rows] int64 from the partial keys of norm_bitlinear_argmax."""
+    _req(keys, torch.int64, "keys")
+    rows, nk = keys.shape
+    out = torch.empty((rows,), dtype=torch.int64, device=keys.device) if out is None else out
+    _req(out, torch.int64, "out")
+    _lib.call("mi_argmax_keys", _ptr(keys), nk, _ptr(out), rows, _stream())
+    return out
+
+
+def embed_argmax(keys, ids_out, emb, r, row_stats) -> None:
+    """Greedy pick from partial keys, then the embedding (with row statistics) of the picks."""
+    _req(keys, torch.int64, "keys"); _req(ids_out, torch.int64, "ids_out"); _req(emb, torch.int8, "emb")
+    _req(r, torch.int32, "r"); _req(row_stats, torch.int64, "row_stats")
+    T, nk = keys.shape
+    V, d = emb.shape
+    _lib.call("mi_embed_argmax", _ptr(keys), nk, _ptr(ids_out), _ptr(emb), _ptr(r), T, d, V, _ptr(row_stats),
+              row_stats.shape[0], _stream())

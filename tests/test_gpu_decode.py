@@ -207,3 +207,42 @@ def test_decode_residual_gemv(cuda, m, n, k):
     assert np.array_equal(H(rt), ref)
     r64 = ref.astype(np.int64)
     assert np.array_equal(H(stats), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 32000, 768), (1, 500, 128), (16, 1000, 256), (3, 64, 3072)])
+def test_lm_head_argmax_keys(cuda, m, n, k):
+    """lm_head with the fused greedy pick: logits, the picked ids (first maximal
+    index: every weight row is duplicated, so every logit value occurs at least
+    twice) and the embedding of the picks equal the oracle's."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m + n + k)
+    r = _resid(rng, m, k)
+    g = rng.integers(100, 400, size=k, dtype=np.int16)
+    half = rng.integers(-1, 2, size=((n + 1) // 2, k), dtype=np.int8)
+    w = np.repeat(half, 2, axis=0)[:n]
+    wp = pack_ternary(w)
+    logits_ref = O.bitlinear(O.bitshift_norm(r, g), wp, O.OUT_INT32)
+    ids_ref = np.argmax(logits_ref, axis=1)
+    r64 = r.astype(np.int64)
+    stats = T(np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+    keys = torch.empty((m, (n + 63) // 64), dtype=torch.int64, device="cuda")
+    logits = torch.zeros((m, n), dtype=torch.int32, device="cuda")
+    ops.norm_bitlinear_argmax(T(r), T(g), T(wp), n, keys, logits=logits, row_stats=stats)
+    assert np.array_equal(H(logits), logits_ref)
+    assert np.array_equal(H(ops.argmax_keys(keys)), ids_ref)
+    keys2 = torch.empty_like(keys)
+    ops.norm_bitlinear_argmax(T(r), T(g), T(wp), n, keys2, row_stats=stats)  # logits not stored
+    assert np.array_equal(H(keys2), H(keys))
+    # embedding of the picks, with the row statistics of layer 0 and zeroed later layers
+    V, d = n, 64
+    emb = i8(rng, V, d)
+    ids = torch.full((m,), -1, dtype=torch.int64, device="cuda")
+    rr = torch.empty((m, d), dtype=torch.int32, device="cuda")
+    st = torch.full((3, m, 2), 5, dtype=torch.int64, device="cuda")
+    ops.embed_argmax(keys, ids, T(emb), rr, st)
+    assert np.array_equal(H(ids), ids_ref)
+    er = O.embed(ids_ref, emb).astype(np.int64)
+    assert np.array_equal(H(rr), er)
+    assert np.array_equal(H(st)[0], np.stack([er.sum(1), (er * er).sum(1)], 1))
+    assert not H(st)[1:].any()

@@ -104,3 +104,24 @@ def test_dropin_model_api(cuda):
     out = m.generate(ids, 5)
     assert out.shape == (2, 25)
     assert np.array_equal(H(out[:, 20:]), O.OracleModel(m.params).generate(ids.cpu().numpy(), 5))
+
+
+def test_chained_decode_graphs_long_generation(cuda):
+    """Greedy generation through the chained multi-step graphs (16 steps per
+    replay, argmax fused into the head, a remainder graph) equals the oracle's,
+    and the state handed back continues the sequence exactly."""
+    from mamba_int.model import IntegerMambaRunner
+    p = _small()
+    ids = np.random.default_rng(4).integers(0, 500, size=(3, 12))
+    om = O.OracleModel(p)
+    run = IntegerMambaRunner(p)
+    ref = om.generate(ids, 40)
+    got = H(run.generate(T(ids), 40, use_graph=True))
+    assert np.array_equal(got, ref)
+    assert np.array_equal(H(run.generate(T(ids), 40, use_graph=True)), ref)
+    # state continuity: 20 + 20 steps through decode_loop equals 40 in one go
+    lg, st = run.prefill(T(ids))
+    first = H(run.decode_loop(lg, st, 20))
+    lg2 = run.decode_step(T(first[:, -1]), st)
+    second = H(run.decode_loop(lg2, st, 20))
+    assert np.array_equal(np.concatenate([first, second], 1), ref)
