@@ -6,11 +6,14 @@ d_state 16, dt_rank 48, vocab 32000, random ternary weights) runs a batch
 steps (HIP-graph decode step).  value = (8*2048 + 8*256) tokens / step time.
 
 Also reported: prefill and decode tok/s separately; the roofline of the
-dominant kernel (the fused block scan), timed with HIP events on its launch
-stream inside the timed steps; and the CPU oracle (C, OpenMP on every host
-core) on a bounded sample of the same workload.
+dominant kernel (the decode step's fused norm + in_proj + conv + x_proj-partial
+kernel, 24 launches per decode step); the decode step against its algorithmic
+bytes; the prefill block scan (timed with HIP events around each launch inside
+the timed steps) against HBM and the int32 VALU rate; and the CPU oracle (C,
+OpenMP on every host core) on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--kernels]
+    python bench.py --pmc-probe     # only the dominant kernel + a copy of known size, for rocprofv3 --pmc
 """
 import argparse
 import json
@@ -22,6 +25,10 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "mamba-integer_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the decode in_proj stage kernel at batch 8, measured
+# with rocprofv3 FETCH_SIZE and WRITE_SIZE (one run each) and scaled by the
+# same counters on a 256 MiB device copy (FETCH x 2.000, WRITE x 1.000)
+IN_PROJ_STAGE_TRAFFIC_B8 = 2002168
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 39321.6 G/s
 
 
@@ -33,21 +40,46 @@ def scan_bytes(B, L, D, N):
     return T * D * 4 + T * 2 * N + D * N * 4 + B * D * N * 4
 
 
+def decode_step_bytes(dims, B):
+    """Algorithmic HBM bytes of one decode step at batch B: every packed ternary
+    matrix once (in_proj, x_proj, dt_proj, out_proj per layer, lm_head), the
+    per-layer int8 conv taps, int32 conv bias and decays, gamma, the int8
+    embedding rows, and the recurrent state read and written once (int32 scan
+    state B*D*N, int8 conv ring B*3*D)."""
+    d, D, N, R, V = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank, dims.vocab_size
+    w_layer = (2 * D * d + (R + 2 * N) * D + D * R + d * D) // 4
+    p_layer = D * 4 + D * 4 + D * N * 4 + d * 2
+    s_layer = 2 * (B * D * N * 4 + B * 3 * D)
+    return dims.n_layer * (w_layer + p_layer + s_layer) + V * d // 4 + d * 2 + B * d
+
+
+def in_proj_step_bytes(dims, B):
+    """Algorithmic bytes of one launch of the decode in_proj stage kernel
+    (mi_norm_in_proj_conv_xpart) at batch B: reads packed in_proj and x_proj
+    weights, the residual rows and their statistics, gamma, conv taps, bias and
+    ring; writes the z half, xs, the conv ring and the x_proj partials."""
+    d, D, N, R = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank
+    nx = R + 2 * N
+    reads = 2 * D * d // 4 + nx * D // 4 + B * d * 4 + B * 16 + d * 2 + D * 4 + D * 4 + B * 3 * D
+    writes = B * D + B * D + B * 3 * D + B * (D // 16) * nx * 4
+    return reads + writes
+
+
 def cpu_baseline(params, threads):
-    """Oracle (C, OpenMP) on a bounded sample: batch 8 x 32-token prefill and 4
-    decode steps of the same model, extrapolated to the 8 x 2048 + 256-step
-    workload by per-token prefill time and per-step decode time."""
+    """Oracle (C, OpenMP) on a bounded sample: the full batch 8 x 2048-token
+    prefill and 48 of the 256 decode steps of the same model (about 10-20 s on
+    16 cores), the decode time extrapolated per step."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import numpy as np
     import oracle as O
     O.set_threads(threads)
     om = O.OracleModel(params)
-    ids = np.random.default_rng(3).integers(0, params.dims.vocab_size, size=(8, 32))
+    ids = np.random.default_rng(3).integers(0, params.dims.vocab_size, size=(8, 2048))
     t0 = time.perf_counter()
     logits, st = om.prefill(ids)
     t1 = time.perf_counter()
     tok = np.argmax(logits, axis=-1)
-    steps = 4
+    steps = 48
     for _ in range(steps):
         logits, st = om.decode_step(tok, st)
         tok = np.argmax(logits, axis=-1)
@@ -57,8 +89,8 @@ def cpu_baseline(params, threads):
     t_work = 8 * 2048 * t_tok_prefill + 256 * t_decode_step
     return {
         "value": (8 * 2048 + 8 * 256) / t_work, "unit": "tok/s", "cores": threads, "kind": "port",
-        "sample": "oracle C/OpenMP: batch 8 x 32-token prefill + 4 decode steps of the d768x24 model "
-                  f"({t2 - t0:.1f} s), extrapolated to 8x2048 prefill + 256 decode steps",
+        "sample": "oracle C/OpenMP: batch 8 x 2048-token prefill + 48 decode steps of the d768x24 model "
+                  f"({t2 - t0:.1f} s), decode extrapolated to 256 steps",
         "prefill_tok_s": 1.0 / t_tok_prefill, "decode_tok_s": 8.0 / t_decode_step,
     }
 
@@ -93,6 +125,47 @@ def _time_kernel(fn, iters=20, warmup=2, reps=3):
         times.append(a.elapsed_time(b) / iters)
     times.sort()
     return times[len(times) // 2]
+
+
+def _decode_ready(run, dims, B):
+    """A live batch-B decode workspace and state (prefill of 16 tokens + one
+    decode step), the inputs of the decode stage kernels."""
+    import numpy as np
+    import torch
+    from mamba_int import ops
+    ids = torch.from_numpy(np.random.default_rng(5).integers(0, dims.vocab_size, size=(B, 16))).to("cuda:0")
+    logits, state = run.prefill(ids)
+    run.decode_step(ops.argmax(logits), state)
+    torch.cuda.synchronize()
+    return run._workspace(B), state
+
+
+def in_proj_stage_launch(run, ws, state):
+    """One launch of the decode in_proj stage kernel of layer 0 on live buffers."""
+    from mamba_int import ops
+    ly = run.layers[0]
+    return lambda: ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, state.conv[0],
+                                         ws.xs, ws.xz, row_stats=ws.stats[0], w_x=ly.w_x, xpart=ws.xpart)
+
+
+def pmc_probe():
+    """For rocprofv3 --pmc: 20 launches of the dominant kernel at the bench's
+    batch, then 3 device copies of 256 MiB (bytes known: the counter scale)."""
+    import torch
+    from mamba_int import ModelDims, init_random_params
+    from mamba_int.model import IntegerMambaRunner
+    dims = ModelDims(d_model=768, n_layer=24, vocab_size=32000, d_state=16, dt_rank=48)
+    run = IntegerMambaRunner(init_random_params(dims, 3), device="cuda:0")
+    ws, state = _decode_ready(run, dims, 8)
+    fn = in_proj_stage_launch(run, ws, state)
+    for _ in range(20):
+        fn()
+    x = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": "done", "kernel_launches": 20, "copy_bytes": 256 << 20, "copies": 3}))
 
 
 def kernel_table():
@@ -166,6 +239,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--kernels", action="store_true", help="also time each config's kernel")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the dominant kernel and a copy (for counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the integer inference path has no "
@@ -178,6 +252,9 @@ def main():
     from mamba_int.model import IntegerMambaRunner
 
     _lib.load()
+    if args.pmc_probe:
+        pmc_probe()
+        return
     dims = ModelDims(d_model=768, n_layer=24, vocab_size=32000, d_state=16, dt_rank=48)
     B, L, NDEC = 8, 2048, args.decode_steps
     params = init_random_params(dims, 3)
@@ -234,6 +311,17 @@ def main():
     achieved = sbytes / (scan_avg_ms * 1e-3) / 1e9
     updates = B * L * dims.d_inner * dims.d_state
 
+    # dominant kernel: the decode in_proj stage (24 launches per decode step);
+    # per-launch period of back-to-back launches in a HIP graph, HIP events on
+    # the launch stream (kernels inside the decode graphs cannot be bracketed
+    # one by one)
+    ws, dstate = _decode_ready(run, dims, B)
+    dom_ms = _time_kernel(in_proj_stage_launch(run, ws, dstate), iters=100, warmup=3, reps=5)
+    dom_bytes = in_proj_step_bytes(dims, B)
+    dom_gbs = dom_bytes / (dom_ms * 1e-3) / 1e9
+    step_bytes = decode_step_bytes(dims, B)
+    step_gbs = step_bytes / (ms_decode / NDEC * 1e-3) / 1e9
+
     line = {
         "metric": "prefill + decode tok/s, 1 GPU, int-Mamba d768x24; scan/GEMV % HBM roofline",
         "value": tokens / wall,
@@ -255,11 +343,22 @@ def main():
         "ms_prefill": ms_prefill,
         "ms_decode_step": ms_decode / NDEC,
         "roofline": {
-            "kernel": "fused block scan (scan_kernel<16,G,model>), one launch per layer in prefill",
-            "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-            "bytes_per_launch": sbytes, "avg_launch_ms": scan_avg_ms, "launches_timed": len(scan_ms),
-            "valu_updates_per_s": updates / (scan_avg_ms * 1e-3),
+            "kernel": "decode in_proj stage: norm + in_proj GEMV + conv + squareplus + x_proj partials "
+                      "(norm_gemv_kernel<1,true,false>, mi_norm_in_proj_conv_xpart), batch 8, 24 launches/step",
+            "bound": "hbm", "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": dom_gbs / HBM_PEAK_GBS, "traffic": IN_PROJ_STAGE_TRAFFIC_B8,
+            "bytes_per_launch": dom_bytes, "avg_launch_ms": dom_ms,
+            "method": "period of 100 back-to-back launches in one HIP graph, HIP events on the launch stream",
+        },
+        "roofline_decode_step": {
+            "bound": "hbm", "bytes_per_step": step_bytes, "achieved": step_gbs, "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS,
+        },
+        "roofline_scan": {
+            "kernel": "prefill fused block scan (model_scan_kernel<16,G>), one launch per layer",
+            "bound": "valu", "bytes_per_launch": sbytes, "avg_launch_ms": scan_avg_ms,
+            "launches_timed": len(scan_ms), "hbm_GB_s": achieved, "hbm_frac": achieved / HBM_PEAK_GBS,
+            "updates_per_s": updates / (scan_avg_ms * 1e-3),
         },
     }
     if args.kernels:
