@@ -550,10 +550,12 @@ GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ld
 template <int KIND>
 hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
     const int blocks = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);
-    if (getenv("MI_GEMM16"))
-        hipLaunchKernelGGL(gemm_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
-    else
+    // the 16x16x64 kernel is the faster one on every measured shape (config 2
+    // and the config-3 prefill projections); MI_GEMM32=1 selects the other
+    if (getenv("MI_GEMM32"))
         hipLaunchKernelGGL(gemm32_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL(gemm_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
     return hipGetLastError();
 }
 
