@@ -414,6 +414,85 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
     }
 }
 
+// --------------------------------------- batched decode GEMV, 16 < m <= 64
+// One step of up to 64 sequences: every block owns FT x 16 output features
+// and all four 16-token tiles; its WAVES waves take 16-word chunks of K (c,
+// c + WAVES, ...), two chunks in flight (one with 16 waves).  In a chunk, lane (row l16, group
+// lq) reads words [16c+4lq, 16c+4lq+4) of each of its FT weight rows with one
+// 16-byte load and the 64 activation bytes of the same k of each token tile;
+// all loads are unconditional from clamped addresses (a clamped row or token
+// only feeds results that are not stored; a chunk past the end is re-read and
+// its products skipped).  The waves' partial sums meet in LDS through integer
+// atomics (exact, order-free), then waves 0-3 finish one token tile each.
+// Requires kw % 16 == 0, 16-byte aligned w, a and lda.
+template <int KIND, int FT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
+    constexpr int U = WAVES >= 16 ? 1 : 2;  // chunks in flight (16 waves: 128 VGPRs a lane)
+    __shared__ int32_t red[FT][4][64][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lq = lane >> 4;
+    for (int i = tid; i < FT * 4 * 64 * 4; i += 64 * WAVES) (&red[0][0][0][0])[i] = 0;
+    const int n0 = blockIdx.x * 16 * FT;
+    const int nchunk = g.kw / 16;
+    const uint32_t *wrow[FT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f) wrow[f] = g.w + (int64_t)min(n0 + 16 * f + l16, g.N - 1) * g.kw;
+    const int8_t *arow[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) arow[t] = g.a + (int64_t)min(16 * t + l16, g.M - 1) * g.lda;
+    v4i acc[FT][4];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[f][t] = v4i{0, 0, 0, 0};
+    for (int c0 = wave; c0 < nchunk; c0 += U * WAVES) {
+        v4i wv[U][FT], xv[U][4][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + WAVES * u < nchunk ? c0 + WAVES * u : c0;
+            const int w = 16 * c + 4 * lq;
+#pragma unroll
+            for (int f = 0; f < FT; ++f) wv[u][f] = *reinterpret_cast<const v4i *>(wrow[f] + w);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xv[u][t][j] = *reinterpret_cast<const v4i *>(arow[t] + 16 * (w + j));
+        }
+        // keep every load of the chunks in flight ahead of the first product
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + WAVES * u < nchunk) {  // same for the whole wave
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int f = 0; f < FT; ++f) {
+                        const v4i fw = unpack16((uint32_t)wv[u][f][j]);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) acc[f][t] = mfma_i8(fw, xv[u][t][j], acc[f][t]);
+                    }
+            }
+        }
+    }
+    __syncthreads();  // red zeroed
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) atomicAdd(&red[f][t][lane][r], acc[f][t][r]);
+    __syncthreads();
+    if (wave >= 4) return;
+    // wave w finishes token tile w: lane (token 16w + l16, group lq) holds
+    // features n0 + 16f + 4lq + r
+    const int m = 16 * wave + l16;
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+        const v4i v = v4i{red[f][wave][lane][0], red[f][wave][lane][1], red[f][wave][lane][2], red[f][wave][lane][3]};
+        const RowStat st = store4<KIND>(g, m, n0 + 16 * f + 4 * lq, v);
+        if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
+    }
+}
+
 // ------------------------------------------- decode RESIDUAL GEMV, m <= 16
 // The out_proj of one decode step (a few tokens): 16 features per block, 8
 // waves taking 16-word chunks of K (c, c+8, ...).  In a chunk, lane (row
@@ -585,6 +664,20 @@ hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
     if (KIND == MI_OUT_RESIDUAL && g.M <= 16 && g.kw % 16 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
         g.lda % 16 == 0) {
         hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((g.N + 15) / 16)), dim3(512), 0, st, g);
+        return hipGetLastError();
+    }
+    if (g.M > 16 && g.M <= 64 && g.kw % 16 == 0 && aligned(g.w, 16) && aligned(g.a, 16) && g.lda % 16 == 0) {
+        // 32 features per block when that still gives >= 128 blocks; deep K
+        // (many 16-word chunks per block) spreads over 8 or 16 waves
+        const int nchunk = g.kw / 16;
+        if ((g.N + 31) / 32 >= 128 && nchunk <= 8)
+            hipLaunchKernelGGL((gemv64_kernel<KIND, 2, 4>), dim3((unsigned)((g.N + 31) / 32)), dim3(256), 0, st, g);
+        else if (nchunk <= 8)
+            hipLaunchKernelGGL((gemv64_kernel<KIND, 1, 4>), dim3((unsigned)((g.N + 15) / 16)), dim3(256), 0, st, g);
+        else if (nchunk <= 16)
+            hipLaunchKernelGGL((gemv64_kernel<KIND, 1, 8>), dim3((unsigned)((g.N + 15) / 16)), dim3(512), 0, st, g);
+        else
+            hipLaunchKernelGGL((gemv64_kernel<KIND, 1, 16>), dim3((unsigned)((g.N + 15) / 16)), dim3(1024), 0, st, g);
         return hipGetLastError();
     }
     if (g.M <= 16) return launch_gemv_mt<1, KIND>(g, st);

@@ -529,10 +529,13 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     const bool active = d < g.D;
     const int dd = active ? d : g.D - 1;
     // loads that do not depend on the staged row: ternary dt_proj words, state, decays, xs, z
+    // the dt_proj dot of a channel is split over its 4 lanes: lane q takes
+    // the packed words q, q+4, ... (clamped loads; words past kw are skipped)
     const int kw = g.R / 16;
-    uint32_t wdt[kMaxR / 16];
+    uint32_t wdt[kMaxR / 64];
 #pragma unroll
-    for (int w = 0; w < kMaxR / 16; ++w) wdt[w] = w < kw ? g.w_dt[(int64_t)dd * kw + w] : 0u;
+    for (int i = 0; i < kMaxR / 64; ++i)
+        if (4 * i < kw) wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
     int32_t *hp = g.h + ((int64_t)m * g.D + dd) * g.N;
     const int32_t *bp = g.base + (int64_t)dd * g.N;
     int32_t hv[kPerLane], bv[kPerLane];
@@ -610,13 +613,16 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
 
     int acc = 0;
 #pragma unroll
-    for (int w = 0; w < kMaxR / 16; ++w) {
+    for (int i = 0; i < kMaxR / 64; ++i) {
+        const int w = q + 4 * i;
         if (w < kw) {
-            const v4i wt = unpack16(wdt[w]);
+            const v4i wt = unpack16(wdt[i]);
             for (int j = 0; j < 4; ++j)
                 acc = __builtin_amdgcn_sdot4(wt[j], *reinterpret_cast<const int *>(&s_dt[16 * w + 4 * j]), acc, false);
         }
     }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
     const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
     const int64_t xd = rshr64((int64_t)xsv * s_dtq[dm + 20], 10);
     int64_t y = 0;

@@ -129,6 +129,12 @@ class IntegerMambaRunner:
         ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
                             state_out=conv_state, out=ws.xs, batch=B)
         ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+        if L == 1 and not fresh:
+            # one recurrent step per sequence (any batch): dt_proj + scan step + gate
+            ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
+            ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                          res_shift=ly.res_shift, row_stats=stats_out)
+            return
         ops.bitlinear(ws.xp, ly.w_dt, ops.OUT_DECAY_MOD, D, k=R, shift=ly.s_dt, out=ws.dm,
                       lda=dims.xp_width, m=T)
         if self.scan_timer is not None:

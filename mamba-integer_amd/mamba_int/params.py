@@ -80,8 +80,8 @@ def pack_ternary(w: np.ndarray) -> np.ndarray:
         raise ValueError("K must be a multiple of 16")
     if np.any((w < -1) | (w > 1)):
         raise ValueError("ternary weights must lie in {-1, 0, 1}")
-    code = (w.astype(np.int64) & 3).astype(np.uint64).reshape(n, k // 16, 16)
-    words = np.bitwise_or.reduce(code << _bitpos().astype(np.uint64), axis=-1).astype("<u4")
+    code = (w.astype(np.int8).view(np.uint8) & 3).astype(np.uint32).reshape(n, k // 16, 16)
+    words = np.bitwise_or.reduce(code << _bitpos().astype(np.uint32), axis=-1).astype("<u4")
     return words.view(np.uint8).reshape(n, k // 4)
 
 

@@ -177,3 +177,34 @@ def test_embed_and_argmax(cuda, rng):
     lg[2, 10] = lg[2, 700] = 100  # tie: first index wins
     assert np.array_equal(H(ops.argmax(T(lg))), np.argmax(lg, axis=1))
     assert torch.equal(ops.argmax(T(lg)).cpu(), torch.argmax(torch.from_numpy(lg), dim=1))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 8192, 512), (40, 4096, 256), (17, 100, 256), (64, 300, 4096), (33, 4100, 256)])
+def test_batched_decode_gemv_kinds(cuda, M, N, K):
+    """The batched decode GEMV (16 < m <= 64, K a multiple of 256; 16 or 32
+    features per block): every epilogue kind, and the residual's row
+    statistics, against the oracle."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(M + N + K)
+    a = i8(rng, M, K)
+    w = _tern(rng, N, K)
+    wp = pack_ternary(w)
+    Np = (N + 3) // 4 * 4
+    acc = H(ops.bitlinear(T(a), T(wp), ops.OUT_INT32, N, out=T(np.zeros((M, Np), np.int32)), path="gemv"))
+    assert np.array_equal(acc[:, :N], _acc_exact(a, w))
+    for kind, shift in ((O.OUT_INT8, 6), (O.OUT_DECAY_MOD, 7)):
+        got = H(ops.bitlinear(T(a), T(wp), kind, N, shift=shift, out=T(np.zeros((M, Np), np.int8)), path="gemv"))
+        assert np.array_equal(got[:, :N], O.bitlinear(a, wp, kind, shift)), kind
+    r0 = rng.integers(-(2**23) + 1, 2**23, size=(M, Np), dtype=np.int32)
+    rt = T(r0)
+    stats = torch.zeros((M, 2), dtype=torch.int64, device="cuda")
+    ops.bitlinear(T(a), T(wp), ops.OUT_RESIDUAL, N, out=rt, res_mult=4719, res_shift=16, row_stats=stats, path="gemv")
+    ref = O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=np.ascontiguousarray(r0[:, :N]), res_mult=4719, res_shift=16)
+    assert np.array_equal(H(rt)[:, :N], ref)
+    r64 = ref.astype(np.int64)
+    assert np.array_equal(H(stats), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+    xs = rng.random(M).astype(np.float32) + 0.01
+    got = H(ops.bitlinear(T(a), T(wp), ops.OUT_FLOAT, N, out=T(np.zeros((M, Np), np.float32)), x_scale=T(xs),
+                          w_scale=0.731, path="gemv"))[:, :N]
+    assert np.array_equal(got.view(np.uint32), O.bitlinear(a, wp, O.OUT_FLOAT, x_scale=xs, w_scale=0.731).view(np.uint32))

@@ -125,3 +125,18 @@ def test_chained_decode_graphs_long_generation(cuda):
     lg2 = run.decode_step(T(first[:, -1]), st)
     second = H(run.decode_loop(lg2, st, 20))
     assert np.array_equal(np.concatenate([first, second], 1), ref)
+
+
+def test_config5_width_model_batch64_decode(cuda):
+    """Config-5 architecture (d2048, d_inner 4096, N16, dt_rank 128, vocab
+    32000) with 2 layers at batch 64: prefill + recurrent decode through the
+    batched path (above the fused stages' 16-token limit), bit-exact."""
+    from mamba_int import ModelDims, init_random_params
+    from mamba_int.model import IntegerMambaRunner
+    dims = ModelDims(d_model=2048, n_layer=2, vocab_size=32000, d_state=16, dt_rank=128)
+    p = init_random_params(dims, 5)
+    ids = np.random.default_rng(6).integers(0, 32000, size=(64, 6))
+    ref = O.OracleModel(p).generate(ids, 3)
+    run = IntegerMambaRunner(p)
+    assert np.array_equal(H(run.generate(T(ids), 3, use_graph=False)), ref)
+    assert np.array_equal(H(run.generate(T(ids), 3, use_graph=True)), ref)
