@@ -196,8 +196,9 @@ mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, i
  * launch_conv1d_step (conv1d_step.cu:60-79).  Same integer rules as the
  * unfused ops, bit for bit. */
 
-/* BitShiftNorm of r (int32 [m,k], m <= 16, k % 16 == 0, k <= 3072, r 16-byte
- * and gamma 8-byte aligned; row statistics from row_stats when non-null) fused into
+/* BitShiftNorm of r (int32 [m,k], m <= 16, k % 64 == 0, k <= 3072; r and
+ * w_packed 16-byte, gamma 8-byte aligned; row statistics from row_stats when
+ * non-null) fused into
  * the BitLinear GEMV: out[m, n] = INT8 (sat8(rshr(acc, shift))) or INT32 acc,
  * out row stride ldo.  Replaces BitShiftNorm.forward + BitLinear.forward for
  * one token per sequence (the lm_head path of MambaIntegerModel.forward,

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = wave_id();
     const int wn = wave >> 1, wm = wave & 1;
     const int l16 = lane & 15, lq = lane >> 4;
 
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = wave_id();
     const int wn = wave >> 1, wm = wave & 1;
     const int l32 = lane & 31, lh = lane >> 5;
 
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
     __shared__ v4i red[3][MT][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = wave_id();
     const int l16 = lane & 15, lq = lane >> 4;
     const int n0 = blockIdx.x * 16;
     const int n = n0 + l16;
@@ -429,7 +429,7 @@ template <int KIND, int FT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
     constexpr int U = WAVES >= 16 ? 1 : 2;  // chunks in flight (16 waves: 128 VGPRs a lane)
     __shared__ int32_t red[FT][4][64][4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
     for (int i = tid; i < FT * 4 * 64 * 4; i += 64 * WAVES) (&red[0][0][0][0])[i] = 0;
     const int n0 = blockIdx.x * 16 * FT;
     const int nchunk = g.kw / 16;
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
 __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g) {
     __shared__ int32_t red[8][64][4];
     __shared__ int32_t s_new[16][17];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
     const int n0 = blockIdx.x * 16;
     const int nchunk = g.kw / 16;
     // output element of threads 0..255: token l16, feature n0 + 4lq + wave

@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
     int8_t *a = smem;                                 // [16][pitch]
     v4i *red = reinterpret_cast<v4i *>(smem + kMaxRows * pitch);  // [4][64]
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int l16 = lane & 15, lq = lane >> 4;
     // the row statistics of this thread's staging row, before any other load
     int64_t rs1 = 0, rs2 = 0;
@@ -177,13 +177,20 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
     constexpr int kPer = WIDE ? kMaxSuper : (kMaxSuper + 3) / 4;
     const int s_first = WIDE ? 0 : wave, s_step = WIDE ? 1 : 4;
 
+    // packed weights: one 16-byte load (4 words) per lane and super-step,
+    // from a clamped row (its outputs are not stored); words past K meet
+    // zero activations
     uint32_t wv[kPer][4];
+    {
+        const uint32_t *wrow = g.w + (int64_t)min(n, g.N - 1) * g.kw;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int w0 = 16 * (s_first + i * s_step) + 4 * lq;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            wv[i][j] = (n < g.N && w0 + j < g.kw) ? g.w[(int64_t)n * g.kw + w0 + j] : 0u;
+        for (int i = 0; i < kPer; ++i) {
+            if (s_first + i * s_step < nsuper) {
+                const int w0 = min(16 * (s_first + i * s_step) + 4 * lq, g.kw - 4);
+                const uint4 q4 = *reinterpret_cast<const uint4 *>(wrow + w0);
+                wv[i][0] = q4.x; wv[i][1] = q4.y; wv[i][2] = q4.z; wv[i][3] = q4.w;
+            }
+        }
     }
     // conv operands of this lane's epilogue (token l16, features nf..nf+3)
     const int m = l16;
@@ -405,7 +412,7 @@ template <int NT>
 __device__ __forceinline__ void xproj_token(const DtScanArgs &g, int m, int32_t (*s_xacc)[16 * kMaxXTiles]) {
     constexpr int CW = (64 / NT) >= 8 ? 8 : ((64 / NT) & ~1);
     static_assert(CW >= 2 && CW % 2 == 0, "chunk of word pairs");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
     const int NX = g.R + 2 * g.N;
     const int kwx = g.D / 16;               // even: d_inner % 32 == 0
     const int wpg = 2 * ((kwx + 31) / 32);  // words per lane group, even
@@ -463,7 +470,7 @@ __device__ __forceinline__ void xproj_token(const DtScanArgs &g, int m, int32_t 
 // four words feed four MFMA k-steps.  Two chunks' loads are in flight at once.
 template <int NT>
 __device__ __forceinline__ void xproj_token_c16(const DtScanArgs &g, int m, int32_t (*s_xacc)[16 * kMaxXTiles]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lq = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
     const int NX = g.R + 2 * g.N;
     const int kwx = g.D / 16;
     const int nchunk = kwx / 16;
@@ -678,12 +685,12 @@ mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma
                           int k) {
     MI_REQUIRE(m >= 0 && n >= 0 && k >= 0, MI_ERR_BAD_DIM, "%s: negative size", fn);
     MI_REQUIRE(m <= kMaxRows, MI_ERR_BAD_DIM, "%s: m=%d exceeds %d tokens", fn, m, kMaxRows);
-    MI_REQUIRE(k % 16 == 0 && k <= kMaxNormK, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 16 and <= %d", fn, k,
+    MI_REQUIRE(k % 64 == 0 && k <= kMaxNormK, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 64 and <= %d", fn, k,
                kMaxNormK);
     if ((int64_t)m * n == 0) return MI_OK;
     MI_REQUIRE(r && gamma && w, MI_ERR_NULL_POINTER, "%s: r, gamma and w_packed are required", fn);
-    MI_REQUIRE(aligned(w, 4) && aligned(gamma, 8), MI_ERR_BAD_ALIGNMENT,
-               "%s: w_packed must be 4-byte aligned, gamma 8-byte aligned", fn);
+    MI_REQUIRE(aligned(w, 16) && aligned(gamma, 8), MI_ERR_BAD_ALIGNMENT,
+               "%s: w_packed must be 16-byte aligned, gamma 8-byte aligned", fn);
     return MI_OK;
 }
 

@@ -19,6 +19,10 @@ void clear_error();
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// The wave index within the block as a scalar, so the compiler treats
+// branches on it as uniform (no per-lane masking around loads).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // ------------------------------------------------------ integer primitives
 __host__ __device__ __forceinline__ int64_t rshr64(int64_t v, int s) {
     return s <= 0 ? v : ((v + ((int64_t)1 << (s - 1))) >> s);

@@ -147,7 +147,8 @@ class IntegerMambaRunner:
                       res_shift=ly.res_shift, row_stats=stats_out)
 
     def _fused_decode_ok(self, B: int) -> bool:
-        return B <= 16 and self.dims.d_model <= 3072 and self.dims.d_state <= 64 and self.dims.dt_rank <= 256
+        return (B <= 16 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0 and self.dims.d_state <= 64
+                and self.dims.dt_rank <= 256)
 
     def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
                       h_state: torch.Tensor, li: int) -> None:
@@ -176,7 +177,7 @@ class IntegerMambaRunner:
 
     def _head(self, r_rows: torch.Tensor, stats: Optional[torch.Tensor],
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        if r_rows.shape[0] <= 16 and self.dims.d_model <= 3072:
+        if r_rows.shape[0] <= 16 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0:
             return ops.norm_bitlinear(r_rows, self.gamma_f, self.w_head, ops.OUT_INT32, self.dims.vocab_size,
                                       out=out, row_stats=stats)
         a = ops.bitshift_norm(r_rows, self.gamma_f, row_stats=stats)
