@@ -278,6 +278,55 @@ mi_status mi_argmax_keys(const int64_t *keys, int nkeys, int64_t *ids, int rows,
 mi_status mi_embed_argmax(const int64_t *keys, int nkeys, int64_t *ids, const int8_t *emb, int32_t *r,
                           int tokens, int dim, int vocab, int64_t *row_stats, int stats_layers, void *stream);
 
+/* ------------------------------------------------ whole decode step */
+/* Integer parameters of one layer (device pointers; spec mi-spec-1 layouts:
+ * packed ternary matrices [rows][cols/4] bytes, 16-byte aligned). */
+typedef struct mi_layer_params {
+    const int16_t *gamma;    /* BitShiftNorm gain [d_model] */
+    const uint8_t *w_in;     /* in_proj [2*d_inner][d_model/4] */
+    int s_in;                /* in_proj requant shift */
+    const int8_t *conv_w;    /* [d_inner][4] taps */
+    const int32_t *conv_b;   /* [d_inner] */
+    const uint8_t *w_x;      /* x_proj [dt_rank+2*d_state][d_inner/4] */
+    int s_x;
+    const uint8_t *w_dt;     /* dt_proj [d_inner][dt_rank/4] */
+    int s_dt;
+    const int32_t *base;     /* decays [d_inner][d_state] */
+    int decay_shift;
+    int s_y;
+    const uint8_t *w_out;    /* out_proj [d_model][d_inner/4] */
+    int32_t res_mult;
+    int res_shift;
+} mi_layer_params;
+
+/* The model: dims (d_inner = 2*d_model), int8 embedding [vocab][d_model],
+ * `layers` a HOST array of n_layer entries, final gain and packed lm_head
+ * [vocab][d_model/4]. */
+typedef struct mi_model_params {
+    int d_model, n_layer, vocab_size, d_state, dt_rank;
+    const int8_t *emb;
+    const mi_layer_params *layers;
+    const int16_t *gamma_f;
+    const uint8_t *w_head;
+} mi_model_params;
+
+/* Bytes of the caller-owned device workspace mi_decode_step needs at batch m
+ * (1 <= m <= 16; d_model % 64 == 0, <= 3072; dt_rank % 16 == 0 and
+ * dt_rank + 2*d_state <= 256). */
+mi_status mi_decode_workspace_size(const mi_model_params *params, int m, size_t *bytes);
+
+/* One greedy decode step of the whole model for m sequences (the reference's
+ * generation step, scripts/inference.py:147-161 over MambaIntegerModel.forward,
+ * mamba_integer_model.py:486-495, with recurrent state): ids int64 [m] in,
+ * next_ids int64 [m] out (first maximal logit), logits int32 [m][ld_logits]
+ * when non-NULL; conv_state / h_state are HOST arrays of n_layer device
+ * pointers (int8 [m][3][d_inner], int32 [m][d_inner][d_state]) updated in
+ * place; workspace 256-byte aligned, at least mi_decode_workspace_size bytes.
+ * Enqueues only kernels (no allocation, no memset): graph-capturable. */
+mi_status mi_decode_step(const mi_model_params *params, int m, const int64_t *ids, int64_t *next_ids,
+                         int32_t *logits, int ld_logits, int8_t *const *conv_state, int32_t *const *h_state,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,123 @@
+// One greedy decode step of the whole model behind the C ABI (host-side
+// orchestration of the fused decode stages; no device allocation, no memset,
+// so a caller may capture it in a HIP graph).
+//
+// Per step: embed the input ids (row statistics of layer 0, later layers'
+// statistics zeroed), then for every layer the three fused stages
+// (norm + in_proj + conv + x_proj partials; x_proj finish + dt_proj + scan
+// step + gate; out_proj + residual + row statistics), then norm + lm_head with
+// the greedy pick fused in, and the pick itself.  Mirrors the reference's
+// generation step (scripts/inference.py:147-161 over
+// MambaIntegerModel.forward, src/mamba_integer_model.py:486-495) with the
+// recurrent state of a Mamba decode instead of a full-prefix recompute.
+#include <hip/hip_runtime.h>
+
+#include "mi_common.hpp"
+
+namespace mi {
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct WsLayout {
+    size_t r, stats, xz, xs, yo, xpart, keys, total;
+};
+
+// Sub-buffer offsets of the decode workspace for batch m.
+WsLayout ws_layout(const mi_model_params &p, int m) {
+    const size_t d = p.d_model, D = 2 * d, N = p.d_state, R = p.dt_rank, V = p.vocab_size;
+    const size_t nx = R + 2 * N;
+    WsLayout w{};
+    size_t o = 0;
+    w.r = o; o += up((size_t)m * d * 4);
+    w.stats = o; o += up((size_t)(p.n_layer + 1) * m * 2 * 8);
+    w.xz = o; o += up((size_t)m * 2 * D);
+    w.xs = o; o += up((size_t)m * D);
+    w.yo = o; o += up((size_t)m * D);
+    w.xpart = o; o += up((size_t)m * (D / 16) * nx * 4);
+    w.keys = o; o += up((size_t)m * ((V + 63) / 64) * 8);
+    w.total = o;
+    return w;
+}
+
+mi_status check_model(const char *fn, const mi_model_params *p, int m) {
+    MI_REQUIRE(p, MI_ERR_NULL_POINTER, "%s: params is NULL", fn);
+    MI_REQUIRE(m >= 1 && m <= 16, MI_ERR_BAD_DIM, "%s: m=%d outside [1,16] (the fused decode stages)", fn, m);
+    MI_REQUIRE(p->n_layer >= 1 && p->vocab_size >= 1, MI_ERR_BAD_DIM, "%s: n_layer and vocab_size must be >= 1", fn);
+    MI_REQUIRE(p->d_model >= 64 && p->d_model % 64 == 0 && p->d_model <= 3072, MI_ERR_BAD_DIM,
+               "%s: d_model=%d must be a multiple of 64 in [64,3072]", fn, p->d_model);
+    MI_REQUIRE(p->dt_rank >= 16 && p->dt_rank % 16 == 0 && p->d_state >= 1 && p->d_state <= 64 &&
+                   p->dt_rank + 2 * p->d_state <= 256,
+               MI_ERR_BAD_DIM, "%s: dt_rank=%d, d_state=%d outside the fused stages' limits", fn, p->dt_rank,
+               p->d_state);
+    MI_REQUIRE(p->emb && p->layers && p->gamma_f && p->w_head, MI_ERR_NULL_POINTER,
+               "%s: emb, layers, gamma_f and w_head are required", fn);
+    return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status mi_decode_workspace_size(const mi_model_params *params, int m, size_t *bytes) {
+    clear_error();
+    mi_status st = check_model("mi_decode_workspace_size", params, m);
+    if (st != MI_OK) return st;
+    MI_REQUIRE(bytes, MI_ERR_NULL_POINTER, "mi_decode_workspace_size: bytes is NULL");
+    *bytes = ws_layout(*params, m).total;
+    return MI_OK;
+}
+
+extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const int64_t *ids, int64_t *next_ids,
+                                    int32_t *logits, int ld_logits, int8_t *const *conv_state,
+                                    int32_t *const *h_state, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+    clear_error();
+    mi_status st = check_model("mi_decode_step", params, m);
+    if (st != MI_OK) return st;
+    const mi_model_params &p = *params;
+    MI_REQUIRE(ids && next_ids && conv_state && h_state && workspace, MI_ERR_NULL_POINTER,
+               "mi_decode_step: ids, next_ids, conv_state, h_state and workspace are required");
+    MI_REQUIRE(aligned(workspace, kAlign), MI_ERR_BAD_ALIGNMENT, "mi_decode_step: workspace must be 256-byte aligned");
+    const WsLayout w = ws_layout(p, m);
+    MI_REQUIRE(workspace_bytes >= w.total, MI_ERR_BAD_ARG, "mi_decode_step: workspace of %zu bytes < %zu required",
+               workspace_bytes, w.total);
+    MI_REQUIRE(!logits || ld_logits >= p.vocab_size, MI_ERR_BAD_DIM, "mi_decode_step: ld_logits < vocab_size");
+    for (int l = 0; l < p.n_layer; ++l)
+        MI_REQUIRE(conv_state[l] && h_state[l], MI_ERR_NULL_POINTER, "mi_decode_step: state of layer %d is NULL", l);
+
+    char *base = static_cast<char *>(workspace);
+    int32_t *r = reinterpret_cast<int32_t *>(base + w.r);
+    int64_t *stats = reinterpret_cast<int64_t *>(base + w.stats);
+    int8_t *xz = reinterpret_cast<int8_t *>(base + w.xz);
+    int8_t *xs = reinterpret_cast<int8_t *>(base + w.xs);
+    int8_t *yo = reinterpret_cast<int8_t *>(base + w.yo);
+    int32_t *xpart = reinterpret_cast<int32_t *>(base + w.xpart);
+    int64_t *keys = reinterpret_cast<int64_t *>(base + w.keys);
+    const int d = p.d_model, D = 2 * d, N = p.d_state, R = p.dt_rank, nx = R + 2 * N;
+    const size_t stat_stride = (size_t)m * 2;
+
+    // every stage reports its own error; the first failure ends the step
+#define MI_STEP(call)                    \
+    do {                                 \
+        const mi_status s_ = (call);     \
+        if (s_ != MI_OK) return s_;      \
+    } while (0)
+    MI_STEP(mi_embed(ids, p.emb, r, m, d, p.vocab_size, stats, p.n_layer + 1, stream));
+    for (int l = 0; l < p.n_layer; ++l) {
+        const mi_layer_params &ly = p.layers[l];
+        MI_STEP(mi_norm_in_proj_conv_xpart(r, stats + l * stat_stride, ly.gamma, ly.w_in, ly.s_in, ly.conv_w,
+                                           ly.conv_b, conv_state[l], xs, xz, ly.w_x, nx, xpart, m, d, D, stream));
+        MI_STEP(mi_xpart_dt_scan_step(xpart, D / 16, ly.s_x, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base,
+                                      ly.decay_shift, ly.s_y, h_state[l], yo, m, D, N, stream));
+        MI_STEP(mi_bitlinear_gemv(yo, D, ly.w_out, r, d, MI_OUT_RESIDUAL, m, d, D, 0, ly.res_mult, ly.res_shift,
+                                  nullptr, 0.0f, stats + (l + 1) * stat_stride, stream));
+    }
+    MI_STEP(mi_norm_bitlinear_argmax(r, stats + p.n_layer * stat_stride, p.gamma_f, p.w_head, logits, ld_logits, keys,
+                                     m, p.vocab_size, d, stream));
+    MI_STEP(mi_argmax_keys(keys, (p.vocab_size + 63) / 64, next_ids, m, stream));
+#undef MI_STEP
+    return MI_OK;
+}

@@ -47,6 +47,8 @@ SIGNATURES = {
     "mi_norm_bitlinear_argmax": [P, P, P, P, P, I, P, I, I, I, P],
     "mi_argmax_keys": [P, I, P, I, P],
     "mi_embed_argmax": [P, I, P, P, P, I, I, I, P, I, P],
+    "mi_decode_workspace_size": [P, I, P],
+    "mi_decode_step": [P, I, P, P, P, I, P, P, P, ctypes.c_size_t, P],
 }
 
 

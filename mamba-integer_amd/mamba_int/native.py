@@ -1,0 +1,83 @@
+"""The whole decode step behind the C ABI (``mi_decode_step``): ctypes mirrors
+of ``mi_layer_params`` / ``mi_model_params`` and a small decoder object that
+owns the workspace and the state pointer arrays.
+
+This is the entry a non-Python host (a C++ engine in place of
+``src/cpp_engine/mamba_infer.cpp``) would call; from Python it runs one greedy
+step per call, enqueued on the current stream (capturable in a HIP graph).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List
+
+import torch
+
+from . import _lib
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+
+class LayerParams(ctypes.Structure):
+    """Field-for-field mirror of ``mi_layer_params`` (include/mamba_int.h)."""
+    _fields_ = [("gamma", _P), ("w_in", _P), ("s_in", _I), ("conv_w", _P), ("conv_b", _P),
+                ("w_x", _P), ("s_x", _I), ("w_dt", _P), ("s_dt", _I), ("base", _P),
+                ("decay_shift", _I), ("s_y", _I), ("w_out", _P), ("res_mult", ctypes.c_int32),
+                ("res_shift", _I)]
+
+
+class ModelParams(ctypes.Structure):
+    """Mirror of ``mi_model_params``; ``layers`` points at a host array."""
+    _fields_ = [("d_model", _I), ("n_layer", _I), ("vocab_size", _I), ("d_state", _I), ("dt_rank", _I),
+                ("emb", _P), ("layers", ctypes.POINTER(LayerParams)), ("gamma_f", _P), ("w_head", _P)]
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+class NativeDecoder:
+    """Greedy decode through ``mi_decode_step`` for the device parameters of an
+    ``IntegerMambaRunner`` at batch m (1 <= m <= 16)."""
+
+    def __init__(self, runner, m: int):
+        dims = runner.dims
+        self.runner, self.m = runner, m
+        self._layers = (LayerParams * dims.n_layer)()
+        for i, ly in enumerate(runner.layers):
+            self._layers[i] = LayerParams(_ptr(ly.gamma), _ptr(ly.w_in), ly.s_in, _ptr(ly.conv_w), _ptr(ly.conv_b),
+                                          _ptr(ly.w_x), ly.s_x, _ptr(ly.w_dt), ly.s_dt, _ptr(ly.base), ly.k, ly.s_y,
+                                          _ptr(ly.w_out), ly.res_mult, ly.res_shift)
+        self.params = ModelParams(dims.d_model, dims.n_layer, dims.vocab_size, dims.d_state, dims.dt_rank,
+                                  _ptr(runner.emb), self._layers, _ptr(runner.gamma_f), _ptr(runner.w_head))
+        self._pp = ctypes.cast(ctypes.pointer(self.params), _P)
+        nbytes = ctypes.c_size_t(0)
+        _lib.call("mi_decode_workspace_size", self._pp, m, ctypes.cast(ctypes.pointer(nbytes), _P))
+        self.ws_bytes = nbytes.value
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=runner.device)
+
+    def step(self, ids: torch.Tensor, state, next_ids: torch.Tensor, logits=None) -> torch.Tensor:
+        """One step: ids [m] int64 -> next_ids [m] int64 (and int32 logits [m, V] when given);
+        ``state`` (a DecodeState of batch m) is updated in place."""
+        n = self.params.n_layer
+        conv = (ctypes.c_void_p * n)(*[_ptr(c) for c in state.conv])
+        h = (ctypes.c_void_p * n)(*[_ptr(t) for t in state.h])
+        ld = 0 if logits is None else logits.stride(0)
+        _lib.call("mi_decode_step", self._pp, self.m, _P(_ptr(ids)), _P(_ptr(next_ids)),
+                  _P(_ptr(logits)) if logits is not None else None, ld, ctypes.cast(conv, _P), ctypes.cast(h, _P),
+                  _P(_ptr(self.workspace)), ctypes.c_size_t(self.ws_bytes),
+                  _P(torch.cuda.current_stream().cuda_stream))
+        return next_ids
+
+    def generate(self, first: torch.Tensor, state, n: int) -> torch.Tensor:
+        """n greedy steps from pick `first` [m]: returns [m, n] (column 0 = first)."""
+        out = torch.empty((self.m, n), dtype=torch.int64, device=first.device)
+        cur = first.clone()
+        nxt = torch.empty_like(cur)
+        out[:, 0] = cur
+        for i in range(1, n):
+            self.step(cur, state, nxt)
+            out[:, i] = nxt
+            cur, nxt = nxt, cur
+        return out

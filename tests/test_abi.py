@@ -95,3 +95,47 @@ def test_product_does_not_import_the_oracle():
                 src = open(os.path.join(root, f)).read()
                 assert not re.search(r"^\s*(import|from)\s+oracle", src, flags=re.M), f
                 assert "liboracle" not in src, f
+
+
+def test_decode_step_struct_layout_matches_header(tmp_path):
+    """The ctypes mirrors of mi_layer_params / mi_model_params have the C
+    compiler's sizes and field offsets (a C program built from the header)."""
+    import subprocess
+    from mamba_int.native import LayerParams, ModelParams
+    src = tmp_path / "layout.c"
+    lf = [f[0] for f in LayerParams._fields_]
+    mf = [f[0] for f in ModelParams._fields_]
+    src.write_text("#include <stdio.h>\n#include <stddef.h>\n#include \"mamba_int.h\"\nint main(void){\n"
+                   + 'printf("%zu\\n", sizeof(mi_layer_params));\n'
+                   + "".join(f'printf("%zu\\n", offsetof(mi_layer_params, {f}));\n' for f in lf)
+                   + 'printf("%zu\\n", sizeof(mi_model_params));\n'
+                   + "".join(f'printf("%zu\\n", offsetof(mi_model_params, {f}));\n' for f in mf)
+                   + "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = ([ctypes.sizeof(LayerParams)] + [getattr(LayerParams, f).offset for f in lf]
+            + [ctypes.sizeof(ModelParams)] + [getattr(ModelParams, f).offset for f in mf])
+    assert got == want
+
+
+def test_decode_step_validation():
+    """mi_decode_step / mi_decode_workspace_size reject bad models before enqueueing."""
+    from mamba_int import _lib
+    from mamba_int.native import ModelParams
+    p = ModelParams(768, 24, 32000, 16, 48, None, None, None, None)
+    pp = ctypes.cast(ctypes.pointer(p), ctypes.c_void_p)
+    n = ctypes.c_size_t(0)
+    np_ = ctypes.cast(ctypes.pointer(n), ctypes.c_void_p)
+    assert _lib.raw("mi_decode_workspace_size", None, 8, np_) == 1
+    assert _lib.raw("mi_decode_workspace_size", pp, 8, np_) == 1 and "required" in _lib.last_error()
+    p.emb = p.gamma_f = p.w_head = 0x1000
+    p.layers = ctypes.cast(ctypes.c_void_p(0x1000), type(p.layers))
+    assert _lib.raw("mi_decode_workspace_size", pp, 17, np_) == 2 and "m=17" in _lib.last_error()
+    p.d_model = 800
+    assert _lib.raw("mi_decode_workspace_size", pp, 8, np_) == 2 and "d_model" in _lib.last_error()
+    p.d_model = 768
+    assert _lib.raw("mi_decode_workspace_size", pp, 8, np_) == 0 and n.value > 0
+    ws = n.value
+    args = (pp, 8, None, None, None, 0, None, None, None, ctypes.c_size_t(ws), None)
+    assert _lib.raw("mi_decode_step", *args) == 1 and "required" in _lib.last_error()

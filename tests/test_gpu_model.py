@@ -140,3 +140,50 @@ def test_config5_width_model_batch64_decode(cuda):
     run = IntegerMambaRunner(p)
     assert np.array_equal(H(run.generate(T(ids), 3, use_graph=False)), ref)
     assert np.array_equal(H(run.generate(T(ids), 3, use_graph=True)), ref)
+
+
+def test_native_decode_step_matches_oracle(cuda):
+    """mi_decode_step (the whole step behind the C ABI): greedy continuation
+    equals the oracle's, its logits equal the runner's decode_step logits, and
+    a HIP graph of the step replays to the eager result."""
+    import torch
+    from mamba_int import ops
+    from mamba_int.model import IntegerMambaRunner
+    from mamba_int.native import NativeDecoder
+    p = _small()
+    ids = np.random.default_rng(8).integers(0, 500, size=(3, 12))
+    ref = O.OracleModel(p).generate(ids, 10)
+    run = IntegerMambaRunner(p)
+    lg, st = run.prefill(T(ids))
+    first = ops.argmax(lg)
+    dec = NativeDecoder(run, 3)
+    assert np.array_equal(H(dec.generate(first, st, 10)), ref)
+    # logits: native step vs the runner's staged decode_step on equal states
+    lg, st = run.prefill(T(ids))
+    st2 = st.clone()
+    tok = ops.argmax(lg)
+    logits = torch.zeros((3, 500), dtype=torch.int32, device="cuda")
+    nxt = torch.empty_like(tok)
+    dec.step(tok, st, nxt, logits=logits)
+    ref_logits = run.decode_step(tok, st2)
+    assert np.array_equal(H(logits), H(ref_logits))
+    assert np.array_equal(H(nxt), H(ops.argmax(ref_logits)))
+    # graph capture of the native step, replayed with eager work in between
+    lg, st = run.prefill(T(ids))
+    tok = ops.argmax(lg)
+    eager = H(dec.generate(tok, st.clone(), 6))
+    cur = tok.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            dec.step(cur, st, nxt)
+    torch.cuda.current_stream().wait_stream(side)
+    got = [H(cur)]
+    for _ in range(5):
+        g.replay()
+        cur.copy_(nxt)
+        got.append(H(cur))
+        run.forward_logits(T(ids[:, :4]))  # unrelated eager work between replays
+    assert np.array_equal(np.stack(got, 1), eager)
