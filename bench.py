@@ -171,7 +171,8 @@ def pmc_probe():
 def kernel_table():
     """Per-config kernel timings: config-1 scan, config-2 GEMM and GEMV (weights
     rotated over 512 copies so the GEMV reads HBM, not the 256 MB MALL), the
-    config-3 decode GEMVs, config-4 chunked scan."""
+    config-3 decode GEMVs, config-5 prefill and decode at batch 64, config-4
+    chunked scan."""
     import numpy as np
     import torch
     from mamba_int import ops, pack_ternary
@@ -219,6 +220,37 @@ def kernel_table():
         ms = _time_kernel(lambda: ops.bitlinear(a8, w, ops.OUT_INT32, NN, out=o, path="gemv"))
         byt = NN * KK // 4 + 8 * KK + 8 * NN * 4
         out[f"config3_decode_{name}_gemv"] = {"ms": ms, "GB_s": byt / ms / 1e6, "bytes": byt}
+    # config 5: d2048 x 48 (d_inner 4096, N 16, dt_rank 128), batch 64: 512-token
+    # prefill and greedy decode steps (device-generated random weights)
+    from mamba_int import ModelDims
+    from mamba_int.model import IntegerMambaRunner, random_device_params
+    dims5 = ModelDims(d_model=2048, n_layer=48, vocab_size=32000, d_state=16, dt_rank=128)
+    run5 = IntegerMambaRunner(random_device_params(dims5, 5, dev), device=dev)
+    ids5 = torch.randint(0, 32000, (64, 512), device=dev)
+    lg5, st5 = run5.prefill(ids5)  # warm (workspaces, kernels)
+    torch.cuda.synchronize()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record()
+    lg5, st5 = run5.prefill(ids5)
+    e1.record()
+    nd = 32
+    run5.decode_loop(lg5, st5, 4)  # capture the decode graph outside the timed steps
+    torch.cuda.synchronize()
+    e1b = torch.cuda.Event(enable_timing=True)
+    e1b.record()
+    run5.decode_loop(lg5, st5, nd + 1)
+    e2.record()
+    torch.cuda.synchronize()
+    ms_pf, ms_dec = e0.elapsed_time(e1), e1b.elapsed_time(e2) / nd
+    sb = decode_step_bytes(dims5, 64)
+    out["config5_d2048x48_b64"] = {
+        "prefill_ms_64x512": ms_pf, "prefill_tok_s": 64 * 512 / (ms_pf * 1e-3),
+        "decode_ms_per_step": ms_dec, "decode_tok_s": 64 / (ms_dec * 1e-3),
+        "decode_bytes_per_step": sb, "decode_GB_s": sb / (ms_dec * 1e-3) / 1e9,
+        "decode_hbm_frac": sb / (ms_dec * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "note": "device-generated random weights; decode steps include the host-side graph launch"}
+    del run5, st5, lg5
+    torch.cuda.empty_cache()
     # config 4: B4 L8192 H24 P64 N128, chunk 256
     B, L, H, P, NS = 4, 8192, 24, 64, 128
     x4, b4, c4 = t8(B, L, H, P), t8(B, L, H, NS), t8(B, L, H, NS)

@@ -69,6 +69,11 @@ def load() -> ctypes.CDLL:
             raise ImportError(
                 f"libmamba_int.so not found at {LIB_PATH}; build it first "
                 "(python -c 'import __graft_entry__ as g; g.build()')")
+        # torch first: it and this library then share torch's HIP runtime
+        # (both link libamdhip64.so.7; the one loaded first serves the process,
+        # and a library call made through a runtime loaded before torch's
+        # finds no device)
+        import torch  # noqa: F401
         lib = ctypes.CDLL(LIB_PATH)
         lib.mi_version.restype = ctypes.c_char_p
         lib.mi_version.argtypes = []

@@ -52,7 +52,40 @@ class DecodeState:
 
 
 def _dev(a, device) -> torch.Tensor:
+    if isinstance(a, torch.Tensor):
+        return a.to(device)
     return torch.from_numpy(a.copy()).to(device)
+
+
+def random_device_params(dims, seed: int, device: str = "cuda") -> ModelParams:
+    """A synthetic integer model generated on the device (same distributions as
+    params.init_random_params, different draws): ternary weights i.i.d. in
+    {-1,0,1} packed by mi_pack_ternary, decays uniform [16384, 32000].  For
+    benchmarks of large configurations, where drawing 10^9 weights on the host
+    would take minutes."""
+    from .params import DECAY_SHIFT, requant_shift
+    dims.validate()
+    dev = torch.device(device)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    d, D, N, R, V = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank, dims.vocab_size
+
+    def ri(lo, hi, shape, dtype):
+        return torch.randint(lo, hi + 1, shape, generator=g, device=dev, dtype=torch.int64).to(dtype)
+
+    def tern(n, k):
+        return ops.pack_ternary(ri(-1, 1, (n, k), torch.int8))
+
+    layers = []
+    for _ in range(dims.n_layer):
+        layers.append(LayerParams(
+            gamma=torch.full((d,), 256, dtype=torch.int16, device=dev), w_in=tern(2 * D, d), s_in=requant_shift(d),
+            conv_w=ri(-32, 32, (D, 4), torch.int8), conv_b=ri(-512, 512, (D,), torch.int32),
+            w_x=tern(R + 2 * N, D), s_x=requant_shift(D), w_dt=tern(D, R), s_dt=requant_shift(R) + 3,
+            base=ri(16384, 32000, (D, N), torch.int32), k=DECAY_SHIFT, s_y=14,
+            w_out=tern(d, D), res_mult=4719, res_shift=16))
+    return ModelParams(dims=dims, emb=ri(-64, 64, (V, d), torch.int8), layers=layers,
+                       gamma_f=torch.full((d,), 256, dtype=torch.int16, device=dev), w_head=tern(V, d))
 
 
 class _Workspace:
