@@ -28,7 +28,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the decode in_proj stage kernel at batch 8, measured
 # with rocprofv3 FETCH_SIZE and WRITE_SIZE (one run each) and scaled by the
 # same counters on a 256 MiB device copy (FETCH x 2.000, WRITE x 1.000)
-IN_PROJ_STAGE_TRAFFIC_B8 = 2002168
+IN_PROJ_STAGE_TRAFFIC_B8 = 2059174
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 39321.6 G/s
 
 
@@ -55,12 +55,13 @@ def decode_step_bytes(dims, B):
 
 def in_proj_step_bytes(dims, B):
     """Algorithmic bytes of one launch of the decode in_proj stage kernel
-    (mi_norm_in_proj_conv_xpart) at batch B: reads packed in_proj and x_proj
-    weights, the residual rows and their statistics, gamma, conv taps, bias and
-    ring; writes the z half, xs, the conv ring and the x_proj partials."""
+    (mi_norm_in_proj_conv_xpart) at batch B, as layers 1.. run it: reads packed
+    in_proj and x_proj weights, the residual rows and the previous out_proj's
+    row-statistics partials (d/16 per row), gamma, conv taps, bias and ring;
+    writes the z half, xs, the conv ring and the x_proj partials."""
     d, D, N, R = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank
     nx = R + 2 * N
-    reads = 2 * D * d // 4 + nx * D // 4 + B * d * 4 + B * 16 + d * 2 + D * 4 + D * 4 + B * 3 * D
+    reads = 2 * D * d // 4 + nx * D // 4 + B * d * 4 + B * (d // 16) * 16 + d * 2 + D * 4 + D * 4 + B * 3 * D
     writes = B * D + B * D + B * 3 * D + B * (D // 16) * nx * 4
     return reads + writes
 
@@ -141,11 +142,12 @@ def _decode_ready(run, dims, B):
 
 
 def in_proj_stage_launch(run, ws, state):
-    """One launch of the decode in_proj stage kernel of layer 0 on live buffers."""
+    """One launch of the decode in_proj stage kernel of layer 1 on live buffers
+    (row statistics as the out_proj partials, as in layers 1..n-1 of a step)."""
     from mamba_int import ops
-    ly = run.layers[0]
-    return lambda: ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, state.conv[0],
-                                         ws.xs, ws.xz, row_stats=ws.stats[0], w_x=ly.w_x, xpart=ws.xpart)
+    ly = run.layers[1]
+    return lambda: ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, state.conv[1],
+                                         ws.xs, ws.xz, row_stats=ws.parts, w_x=ly.w_x, xpart=ws.xpart)
 
 
 def pmc_probe():

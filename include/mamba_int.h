@@ -140,6 +140,19 @@ mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, v
                             int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
                             int res_shift, const float *x_scale, float w_scale, int64_t *row_stats,
                             void *stream);
+/* The decode out_proj with the next norm's row statistics as per-block
+ * partials instead of atomics (the residual update of BitLinear.forward +
+ * MambaIntegerBlock.forward's residual add, mamba_integer_model.py:446-447,
+ * for m <= 16 tokens): r[m, n] (int32, row stride ldr) is updated as by
+ * mi_bitlinear_gemv RESIDUAL, and stats_parts int64 [m, ceil(n/16), 2]
+ * receives, for every row i and block b of 16 features, the sum and the sum
+ * of squares of the updated r[i, 16b : 16b+16] (plain stores: no zeroing,
+ * no atomics).  The norm entries below sum them (their stats_parts =
+ * ceil(n/16)).  m <= 16; k % 64 == 0; a, w_packed, stats_parts 16-byte
+ * aligned. */
+mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const uint8_t *w_packed, int32_t *r,
+                                      int ldr, int m, int n, int k, int32_t res_mult, int res_shift,
+                                      int64_t *stats_parts, void *stream);
 
 /* ---------------------------------------------------------- block ops */
 
@@ -194,18 +207,23 @@ mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, i
  * these entries fuse the per-token stages of MambaIntegerBlock.forward
  * (mamba_integer_model.py:396-447) and the one-step conv of
  * launch_conv1d_step (conv1d_step.cu:60-79).  Same integer rules as the
- * unfused ops, bit for bit. */
+ * unfused ops, bit for bit.
+ *
+ * Row statistics of the norm entries: row_stats NULL (each block reduces
+ * the rows itself) or int64 [m, stats_parts, 2], row i's (sum r, sum r^2)
+ * being the sum over its parts: stats_parts = 1 for the full sums of
+ * mi_embed / RESIDUAL atomics (8-byte aligned), ceil(d/16) for the partials
+ * of mi_bitlinear_residual_parts (16-byte aligned); stats_parts <= 4096. */
 
 /* BitShiftNorm of r (int32 [m,k], m <= 16, k % 64 == 0, k <= 3072; r and
- * w_packed 16-byte, gamma 8-byte aligned; row statistics from row_stats when
- * non-null) fused into
+ * w_packed 16-byte, gamma 8-byte aligned) fused into
  * the BitLinear GEMV: out[m, n] = INT8 (sat8(rshr(acc, shift))) or INT32 acc,
  * out row stride ldo.  Replaces BitShiftNorm.forward + BitLinear.forward for
  * one token per sequence (the lm_head path of MambaIntegerModel.forward,
  * mamba_integer_model.py:492-494). */
-mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                            const uint8_t *w_packed, void *out, int ldo, int kind, int m, int n, int k,
-                            int shift, void *stream);
+mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                            const int16_t *gamma, const uint8_t *w_packed, void *out, int ldo, int kind,
+                            int m, int n, int k, int shift, void *stream);
 
 /* Norm + in_proj (INT8, shift s_in) + depthwise conv step + squareplus:
  * r int32 [m,d_model]; w_in packed [2*d_inner, d_model/4]; the x half goes
@@ -213,8 +231,8 @@ mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, const in
  * lands in xs int8 [m,d_inner]; the z half is written to xz int8
  * [m,2*d_inner] at columns [d_inner, 2*d_inner).  m <= 16, d_model <= 3072;
  * alignment as mi_norm_bitlinear. */
-mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                               const uint8_t *w_in, int s_in,
+mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                               const int16_t *gamma, const uint8_t *w_in, int s_in,
                                const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
                                int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream);
 
@@ -245,8 +263,9 @@ mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x, int s_x, i
  *   xpart[i, b, n] = sum over those channels c of w_x[n, c] * xs[i, c]
  * into xpart int32 [m, d_inner/16, nx], w_x packed [nx, d_inner/4]
  * (4-byte aligned), nx = dt_rank + 2*nstate <= 256. */
-mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                     const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
+mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                     const int16_t *gamma, const uint8_t *w_in, int s_in,
+                                     const int8_t *conv_w, const int32_t *conv_b,
                                      int8_t *conv_state, int8_t *xs, int8_t *xz, const uint8_t *w_x, int nx,
                                      int32_t *xpart, int m, int d_model, int d_inner, void *stream);
 
@@ -266,9 +285,9 @@ mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s_x, int dt_
  * key keys[i, b] = max over its outputs j of (logit << 32 | 0x7FFFFFFF - j),
  * so the largest key of a row names its first maximal index.  keys int64
  * [m, ceil(n/64)]; logits int32 [m, ldo] or NULL (then not stored). */
-mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                   const uint8_t *w_packed, int32_t *logits, int ldo, int64_t *keys, int m,
-                                   int n, int k, void *stream);
+mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                   const int16_t *gamma, const uint8_t *w_packed, int32_t *logits, int ldo,
+                                   int64_t *keys, int m, int n, int k, void *stream);
 
 /* ids[i] = the index the largest of keys[i, 0:nkeys] names (int64 out). */
 mi_status mi_argmax_keys(const int64_t *keys, int nkeys, int64_t *ids, int rows, void *stream);

@@ -37,6 +37,7 @@ struct GemmArgs {
     int res_shift;
     float w_scale;
     int64_t *row_stats;  // RESIDUAL: per-row (sum r, sum r^2) of the new residual, atomically added
+    int64_t *stats_parts;  // RESIDUAL, m <= 16: [M][N/16][2] per-block (sum r, sum r^2), plain stores
 };
 
 struct RowStat {
@@ -500,14 +501,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
 // 16-byte load and the 64 activation bytes of the same k of token l16, so
 // every load is issued before the first MFMA and none is conditional: a
 // token or feature index past the end is clamped, and its results are not
-// stored.  The residual each output overwrites is read at kernel start.
-// Requires kw % 16 == 0, 16-byte aligned w, a and lda.
+// stored; the words of a last, partial chunk past kw are read from a clamped
+// address and zeroed.  The residual each output overwrites is read at kernel
+// start.  Row statistics of the new residual: per-block partials with plain
+// stores (stats_parts) or 64-bit atomics (row_stats).
+// Requires kw % 4 == 0, 16-byte aligned w, a and lda.
 __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g) {
     __shared__ int32_t red[8][64][4];
     __shared__ int32_t s_new[16][17];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
     const int n0 = blockIdx.x * 16;
-    const int nchunk = g.kw / 16;
+    const int nchunk = (g.kw + 15) / 16;
     // output element of threads 0..255: token l16, feature n0 + 4lq + wave
     const int en = n0 + 4 * lq + (wave & 3);
     const bool eok = tid < 256 && l16 < g.M && en < g.N;
@@ -518,19 +522,23 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g) {
     v4i acc = v4i{0, 0, 0, 0};
     for (int c0 = wave; c0 < nchunk; c0 += 16) {
         v4i wv[2], xv[2][4];
+        bool live[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int c = c0 + 8 * u < nchunk ? c0 + 8 * u : c0;
             const int w = 16 * c + 4 * lq;
-            wv[u] = *reinterpret_cast<const v4i *>(wrow + w);
+            const int wl = min(w, g.kw - 4);  // kw % 4 == 0: all four words in or all past the row
+            live[u] = w < g.kw;
+            wv[u] = *reinterpret_cast<const v4i *>(wrow + wl);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xv[u][j] = *reinterpret_cast<const v4i *>(arow + 16 * (w + j));
+            for (int j = 0; j < 4; ++j) xv[u][j] = *reinterpret_cast<const v4i *>(arow + 16 * (wl + j));
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u)
             if (c0 + 8 * u < nchunk)  // same for the whole wave
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc = mfma_i8(unpack16((uint32_t)wv[u][j]), xv[u][j], acc);
+                for (int j = 0; j < 4; ++j)
+                    acc = mfma_i8(unpack16(live[u] ? (uint32_t)wv[u][j] : 0u), xv[u][j], acc);
     }
     *reinterpret_cast<v4i *>(&red[wave][lane][0]) = acc;
     __syncthreads();
@@ -544,19 +552,33 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g) {
         if (eok) *rp = nv;
         s_new[l16][4 * lq + r] = eok ? nv : 0;
     }
-    if (g.row_stats) {
+    if (g.row_stats || g.stats_parts) {
         __syncthreads();
-        if (tid < g.M) {
+        if (tid < 64) {
+            // lane 4i+q sums features 4q..4q+3 of token i, then the quad adds up
+            const int i = tid >> 2, q = tid & 3;
             int64_t s1 = 0, s2 = 0;
 #pragma unroll
-            for (int f = 0; f < 16; ++f) {
-                const int64_t v = s_new[tid][f];
+            for (int f = 0; f < 4; ++f) {
+                const int64_t v = s_new[i][4 * q + f];
                 s1 += v;
                 s2 += v * v;
             }
-            atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)tid), (unsigned long long)s1);
-            atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)tid + 1),
-                      (unsigned long long)s2);
+            s1 += __shfl_xor(s1, 1);
+            s2 += __shfl_xor(s2, 1);
+            s1 += __shfl_xor(s1, 2);
+            s2 += __shfl_xor(s2, 2);
+            if (q == 0 && i < g.M) {
+                if (g.stats_parts) {
+                    *reinterpret_cast<v2l *>(g.stats_parts + 2 * ((int64_t)i * gridDim.x + blockIdx.x)) =
+                        v2l{s1, s2};
+                } else {
+                    atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)i),
+                              (unsigned long long)s1);
+                    atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)i + 1),
+                              (unsigned long long)s2);
+                }
+            }
         }
     }
 }
@@ -661,7 +683,7 @@ hipError_t launch_gemv_mt(const GemmArgs &g, hipStream_t st) {
 
 template <int KIND>
 hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
-    if (KIND == MI_OUT_RESIDUAL && g.M <= 16 && g.kw % 16 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
+    if (KIND == MI_OUT_RESIDUAL && g.M <= 16 && g.kw % 4 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
         g.lda % 16 == 0) {
         hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((g.N + 15) / 16)), dim3(512), 0, st, g);
         return hipGetLastError();
@@ -739,6 +761,24 @@ extern "C" mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *
                                        const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
     return bitlinear_impl("mi_bitlinear_gemv", Path::kGemv, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
                           res_mult, res_shift, x_scale, w_scale, row_stats, stream);
+}
+
+extern "C" mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const uint8_t *w_packed, int32_t *r,
+                                                 int ldr, int m, int n, int k, int32_t res_mult, int res_shift,
+                                                 int64_t *stats_parts, void *stream) {
+    const char *fn = "mi_bitlinear_residual_parts";
+    clear_error();
+    mi_status st = validate(fn, a, lda, w_packed, r, ldr, MI_OUT_RESIDUAL, m, n, k, 0, res_shift, nullptr);
+    if (st != MI_OK || (int64_t)m * n == 0) return st;
+    MI_REQUIRE(m <= 16, MI_ERR_BAD_DIM, "%s: m=%d must be <= 16", fn, m);
+    MI_REQUIRE(k % 64 == 0, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 64", fn, k);
+    MI_REQUIRE(stats_parts, MI_ERR_NULL_POINTER, "%s: stats_parts is required", fn);
+    MI_REQUIRE(aligned(w_packed, 16) && aligned(stats_parts, 16), MI_ERR_BAD_ALIGNMENT,
+               "%s: w_packed and stats_parts must be 16-byte aligned", fn);
+    GemmArgs g = make_args(a, lda, w_packed, r, ldr, m, n, k, 0, res_mult, res_shift, nullptr, 0.0f, nullptr);
+    g.stats_parts = stats_parts;
+    hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((n + 15) / 16)), dim3(512), 0, as_stream(stream), g);
+    return check_launch(fn);
 }
 
 extern "C" mi_status mi_pack_ternary(const int8_t *w, uint8_t *packed, int n, int k, void *stream) {

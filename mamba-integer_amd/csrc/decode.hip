@@ -24,10 +24,12 @@ namespace {
 constexpr int kMaxRows = 16;    // tokens per norm_gemv launch
 constexpr int kMaxNormK = 3072; // d_model limit of the LDS-staged rows
 constexpr int kMaxXTiles = 16;  // x_proj outputs (dt_rank + 2*nstate) <= 256
+constexpr int kMaxStatParts = 4096;  // row-statistics partials per row
 
 struct NormGemvArgs {
     const int32_t *r;       // [M][K] residual, Q8
-    const int64_t *row_stats;  // [M][2] (sum r, sum r^2) or null (computed here)
+    const int64_t *row_stats;  // [M][stats_parts][2] (sum r, sum r^2) partials or null (computed here)
+    int stats_parts;           // partials per row, summed here (1: full sums)
     const int16_t *gamma;   // [K]
     const uint32_t *w;      // [N][K/16] packed words
     void *out;              // INT32: [M][ldo]; INT8: [M][ldo] (z half written)
@@ -67,9 +69,86 @@ __device__ __forceinline__ int norm_tpr(int M) {
     return 256 / Mp;
 }
 
-// (s1, s2): the row statistics of this thread's row min(threadIdx.x / TPR,
-// M - 1), loaded by the caller ahead of its other loads (used with row_stats).
-__device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, int64_t s1, int64_t s2) {
+// Row statistics from stats_parts partials [M][P][2]: the RG = min(TPR, 64)
+// lanes of a row's lane group (aligned to RG within the wave) each take the
+// partials j0, j0 + RG, ... (a group's load covers contiguous bytes).  The
+// first kStatLoads of them are loaded at kernel start, ahead of every other
+// load and without a branch (no row_stats: a clamped dummy read of r), so
+// the first wait for them does not hold back the loads issued after them;
+// any further ones and the sum follow once the first chunk of row loads is
+// in flight.  With P = 1 every lane reads its row's full sums.
+constexpr int kStatLoads = 4;
+
+struct StatParts {
+    v2l v[kStatLoads];
+};
+
+__device__ __forceinline__ int stat_group(int M) { return min(norm_tpr(M), 64); }
+
+__device__ __forceinline__ StatParts load_stat_parts(const NormGemvArgs &g, int mr) {
+    const bool have = g.row_stats != nullptr;
+    const int64_t *base = have ? g.row_stats : reinterpret_cast<const int64_t *>(g.r);
+    const int P = have ? g.stats_parts : 1, row = have ? mr : 0;
+    const int RG = stat_group(g.M), j0 = (int)threadIdx.x & (RG - 1);
+    StatParts p;
+#pragma unroll
+    for (int u = 0; u < kStatLoads; ++u) {
+        const int j = min(j0 + u * RG, P - 1);
+        p.v[u] = *reinterpret_cast<const v2l *>(base + 2 * ((int64_t)row * P + j));
+    }
+    return p;
+}
+
+// v + (v of the lane the DPP control names), 64-bit, within rows of 16 lanes
+template <int kCtrl>
+__device__ __forceinline__ int64_t dpp_add64(int64_t v) {
+    const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)v, kCtrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)((uint64_t)v >> 32), kCtrl, 0xF, 0xF, false);
+    return v + (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Sum over a lane group of 2^k lanes (aligned), every lane getting the total:
+// quad swaps (xor 1, xor 2), then the half-row and row mirrors (lane i with
+// 7 - i, then 15 - i: after the quad step each pairs with a lane of the other
+// quad / other half-row), then xor shuffles across rows.
+__device__ __forceinline__ int64_t group_sum64(int64_t v, int RG) {
+    if (RG > 1) v = dpp_add64<0xB1>(v);   // quad_perm [1,0,3,2]
+    if (RG > 2) v = dpp_add64<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (RG > 4) v = dpp_add64<0x141>(v);  // row_half_mirror
+    if (RG > 8) v = dpp_add64<0x140>(v);  // row_mirror
+    if (RG > 16) v += __shfl_xor(v, 16);
+    if (RG > 32) v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ void sum_stat_parts(const NormGemvArgs &g, int mr, const StatParts &p, int64_t &s1,
+                                               int64_t &s2) {
+    if (g.stats_parts == 1) {
+        s1 = p.v[0][0];
+        s2 = p.v[0][1];
+        return;
+    }
+    const int RG = stat_group(g.M), j0 = (int)threadIdx.x & (RG - 1);
+    s1 = 0;
+    s2 = 0;
+#pragma unroll
+    for (int u = 0; u < kStatLoads; ++u)
+        if (j0 + u * RG < g.stats_parts) {
+            s1 += p.v[u][0];
+            s2 += p.v[u][1];
+        }
+    for (int j = j0 + kStatLoads * RG; j < g.stats_parts; j += RG) {
+        const v2l v = *reinterpret_cast<const v2l *>(g.row_stats + 2 * ((int64_t)mr * g.stats_parts + j));
+        s1 += v[0];
+        s2 += v[1];
+    }
+    s1 = group_sum64(s1, RG);
+    s2 = group_sum64(s2, RG);
+}
+
+// sp: the row statistics of this thread's row min(threadIdx.x / TPR, M - 1),
+// loaded by the caller ahead of its other loads (used with row_stats).
+__device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, const StatParts &sp) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (g.row_stats) {
         // TPR threads per row, each with its row's (mu, shift) in registers
@@ -91,6 +170,8 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, int
             }
         };
         load_chunk(0);
+        int64_t s1, s2;
+        sum_stat_parts(g, mr, sp, s1, s2);
         int64_t mu64;
         const int sh = norm_shift(s1, s2, g.K, &mu64);
         const int32_t mu = (int32_t)mu64;
@@ -165,12 +246,7 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int l16 = lane & 15, lq = lane >> 4;
     // the row statistics of this thread's staging row, before any other load
-    int64_t rs1 = 0, rs2 = 0;
-    if (g.row_stats) {
-        const int mr = min(tid / norm_tpr(g.M), g.M - 1);
-        rs1 = g.row_stats[2 * mr];
-        rs2 = g.row_stats[2 * mr + 1];
-    }
+    const StatParts sp = load_stat_parts(g, min(tid / norm_tpr(g.M), g.M - 1));
     const int n0 = WIDE ? blockIdx.x * 64 + wave * 16 : blockIdx.x * 16;
     const int n = n0 + l16;
     const int nsuper = (g.kw + 15) / 16;
@@ -234,7 +310,7 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
             wx[t] = 16 * t < g.nx ? g.w_x[(int64_t)min(16 * t + l16, g.nx - 1) * xkw + n0 / 16] : 0u;
     }
 
-    stage_norm_rows(g, a, pitch, rs1, rs2);
+    stage_norm_rows(g, a, pitch, sp);
     __syncthreads();
 
     v4i acc = v4i{0, 0, 0, 0};
@@ -681,8 +757,8 @@ void launch_xproj_scan(int ntiles, dim3 grid, hipStream_t hs, const DtScanArgs &
     else hipLaunchKernelGGL((dt_scan_step_kernel<16, NPL>), grid, dim3(256), 0, hs, g);
 }
 
-mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma, const uint8_t *w, int m, int n,
-                          int k) {
+mi_status check_norm_gemv(const char *fn, const int32_t *r, const int64_t *row_stats, int stats_parts,
+                          const int16_t *gamma, const uint8_t *w, int m, int n, int k) {
     MI_REQUIRE(m >= 0 && n >= 0 && k >= 0, MI_ERR_BAD_DIM, "%s: negative size", fn);
     MI_REQUIRE(m <= kMaxRows, MI_ERR_BAD_DIM, "%s: m=%d exceeds %d tokens", fn, m, kMaxRows);
     MI_REQUIRE(k % 64 == 0 && k <= kMaxNormK, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 64 and <= %d", fn, k,
@@ -691,6 +767,12 @@ mi_status check_norm_gemv(const char *fn, const int32_t *r, const int16_t *gamma
     MI_REQUIRE(r && gamma && w, MI_ERR_NULL_POINTER, "%s: r, gamma and w_packed are required", fn);
     MI_REQUIRE(aligned(w, 16) && aligned(gamma, 8), MI_ERR_BAD_ALIGNMENT,
                "%s: w_packed must be 16-byte aligned, gamma 8-byte aligned", fn);
+    if (row_stats) {
+        MI_REQUIRE(stats_parts >= 1 && stats_parts <= kMaxStatParts, MI_ERR_BAD_ARG,
+                   "%s: stats_parts=%d outside [1,%d]", fn, stats_parts, kMaxStatParts);
+        MI_REQUIRE(aligned(row_stats, stats_parts > 1 ? 16 : 8), MI_ERR_BAD_ALIGNMENT,
+                   "%s: row_stats must be 8-byte aligned (16-byte with stats_parts > 1)", fn);
+    }
     return MI_OK;
 }
 
@@ -701,11 +783,11 @@ size_t norm_gemv_lds(int k) { return (size_t)kMaxRows * (k + 16) + 4 * 64 * size
 
 using namespace mi;
 
-extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                       const uint8_t *w_packed, void *out, int ldo, int kind, int m, int n, int k,
-                                       int shift, void *stream) {
+extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                       const int16_t *gamma, const uint8_t *w_packed, void *out, int ldo, int kind,
+                                       int m, int n, int k, int shift, void *stream) {
     clear_error();
-    mi_status st = check_norm_gemv("mi_norm_bitlinear", r, gamma, w_packed, m, n, k);
+    mi_status st = check_norm_gemv("mi_norm_bitlinear", r, row_stats, stats_parts, gamma, w_packed, m, n, k);
     if (st != MI_OK || (int64_t)m * n == 0) return st;
     MI_REQUIRE(kind == MI_OUT_INT8 || kind == MI_OUT_INT32, MI_ERR_BAD_ARG,
                "mi_norm_bitlinear: kind %d (INT8 or INT32 only)", kind);
@@ -713,8 +795,8 @@ extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stat
     MI_REQUIRE(shift >= 0 && shift <= 30, MI_ERR_BAD_ARG, "mi_norm_bitlinear: shift=%d outside [0,30]", shift);
     NormGemvArgs g{};
     MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "mi_norm_bitlinear: r must be 16-byte aligned");
-    g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_packed);
-    g.out = out; g.ldo = ldo;
+    g.r = r; g.row_stats = row_stats; g.stats_parts = stats_parts; g.gamma = gamma;
+    g.w = reinterpret_cast<const uint32_t *>(w_packed); g.out = out; g.ldo = ldo;
     g.M = m; g.N = n; g.K = k; g.kw = k / 16; g.shift = shift;
     // wide blocks (64 features) once there are enough of them to fill the GPU
     const bool wide = n >= 16384;
@@ -731,18 +813,19 @@ extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stat
     return check_launch("mi_norm_bitlinear");
 }
 
-extern "C" mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                              const uint8_t *w_packed, int32_t *logits, int ldo, int64_t *keys, int m,
-                                              int n, int k, void *stream) {
+extern "C" mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                              const int16_t *gamma, const uint8_t *w_packed, int32_t *logits, int ldo,
+                                              int64_t *keys, int m, int n, int k, void *stream) {
     clear_error();
-    mi_status st = check_norm_gemv("mi_norm_bitlinear_argmax", r, gamma, w_packed, m, n, k);
+    mi_status st =
+        check_norm_gemv("mi_norm_bitlinear_argmax", r, row_stats, stats_parts, gamma, w_packed, m, n, k);
     if (st != MI_OK || (int64_t)m * n == 0) return st;
     MI_REQUIRE(keys, MI_ERR_NULL_POINTER, "mi_norm_bitlinear_argmax: keys is required");
     MI_REQUIRE(!logits || ldo >= n, MI_ERR_BAD_DIM, "mi_norm_bitlinear_argmax: ldo=%d < n=%d", ldo, n);
     MI_REQUIRE(aligned(r, 16), MI_ERR_BAD_ALIGNMENT, "mi_norm_bitlinear_argmax: r must be 16-byte aligned");
     NormGemvArgs g{};
-    g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_packed);
-    g.out = logits; g.ldo = ldo; g.keys = keys;
+    g.r = r; g.row_stats = row_stats; g.stats_parts = stats_parts; g.gamma = gamma;
+    g.w = reinterpret_cast<const uint32_t *>(w_packed); g.out = logits; g.ldo = ldo; g.keys = keys;
     g.M = m; g.N = n; g.K = k; g.kw = k / 16; g.shift = 0;
     hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT32, false, true>), dim3((unsigned)((n + 63) / 64)), dim3(256),
                        norm_gemv_lds(k), as_stream(stream), g);
@@ -751,12 +834,12 @@ extern "C" mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *r
 
 namespace mi {
 namespace {
-mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                 const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
+mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                 const int16_t *gamma, const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
                                  int8_t *conv_state, int8_t *xs, int8_t *xz, const uint8_t *w_x, int nx,
                                  int32_t *xpart, int m, int d_model, int d_inner, void *stream) {
     clear_error();
-    mi_status st = check_norm_gemv(fn, r, gamma, w_in, m, 2 * d_inner, d_model);
+    mi_status st = check_norm_gemv(fn, r, row_stats, stats_parts, gamma, w_in, m, 2 * d_inner, d_model);
     if (st != MI_OK || (int64_t)m * d_inner == 0) return st;
     MI_REQUIRE(d_inner % 16 == 0, MI_ERR_BAD_DIM, "%s: d_inner=%d must be a multiple of 16", fn, d_inner);
     MI_REQUIRE(conv_w && conv_b && conv_state && xs && xz, MI_ERR_NULL_POINTER,
@@ -773,7 +856,8 @@ mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t
                    "%s: w_x must be 4-byte and xpart 16-byte aligned", fn);
     }
     NormGemvArgs g{};
-    g.r = r; g.row_stats = row_stats; g.gamma = gamma; g.w = reinterpret_cast<const uint32_t *>(w_in); g.out = xz;
+    g.r = r; g.row_stats = row_stats; g.stats_parts = stats_parts; g.gamma = gamma;
+    g.w = reinterpret_cast<const uint32_t *>(w_in); g.out = xz;
     g.ldo = 2 * (int64_t)d_inner;
     g.M = m; g.N = 2 * d_inner; g.K = d_model; g.kw = d_model / 16; g.shift = s_in;
     g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs; g.conv_d = d_inner;
@@ -785,25 +869,26 @@ mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t
 }  // namespace
 }  // namespace mi
 
-extern "C" mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                          const uint8_t *w_in, int s_in,
+extern "C" mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                          const int16_t *gamma, const uint8_t *w_in, int s_in,
                                           const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
                                           int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream) {
-    return norm_in_proj_conv_impl("mi_norm_in_proj_conv", r, row_stats, gamma, w_in, s_in, conv_w, conv_b,
-                                  conv_state, xs, xz, nullptr, 0, nullptr, m, d_model, d_inner, stream);
+    return norm_in_proj_conv_impl("mi_norm_in_proj_conv", r, row_stats, stats_parts, gamma, w_in, s_in, conv_w,
+                                  conv_b, conv_state, xs, xz, nullptr, 0, nullptr, m, d_model, d_inner, stream);
 }
 
-extern "C" mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, const int16_t *gamma,
-                                                const uint8_t *w_in, int s_in, const int8_t *conv_w,
-                                                const int32_t *conv_b, int8_t *conv_state, int8_t *xs, int8_t *xz,
+extern "C" mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                                const int16_t *gamma, const uint8_t *w_in, int s_in,
+                                                const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
+                                                int8_t *xs, int8_t *xz,
                                                 const uint8_t *w_x, int nx, int32_t *xpart, int m, int d_model,
                                                 int d_inner, void *stream) {
     if (!xpart) {
         mi::clear_error();
         return mi::fail(MI_ERR_NULL_POINTER, "mi_norm_in_proj_conv_xpart: xpart is required");
     }
-    return norm_in_proj_conv_impl("mi_norm_in_proj_conv_xpart", r, row_stats, gamma, w_in, s_in, conv_w, conv_b,
-                                  conv_state, xs, xz, w_x, nx, xpart, m, d_model, d_inner, stream);
+    return norm_in_proj_conv_impl("mi_norm_in_proj_conv_xpart", r, row_stats, stats_parts, gamma, w_in, s_in, conv_w,
+                                  conv_b, conv_state, xs, xz, w_x, nx, xpart, m, d_model, d_inner, stream);
 }
 
 extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const uint8_t *w_dt, int s_dt,

@@ -2,11 +2,11 @@
 // orchestration of the fused decode stages; no device allocation, no memset,
 // so a caller may capture it in a HIP graph).
 //
-// Per step: embed the input ids (row statistics of layer 0, later layers'
-// statistics zeroed), then for every layer the three fused stages
-// (norm + in_proj + conv + x_proj partials; x_proj finish + dt_proj + scan
-// step + gate; out_proj + residual + row statistics), then norm + lm_head with
-// the greedy pick fused in, and the pick itself.  Mirrors the reference's
+// Per step: embed the input ids (with their row statistics), then for every
+// layer the three fused stages (norm + in_proj + conv + x_proj partials;
+// x_proj finish + dt_proj + scan step + gate; out_proj + residual + per-block
+// row-statistics partials, which the next norm sums), then norm + lm_head
+// with the greedy pick fused in, and the pick itself.  Mirrors the reference's
 // generation step (scripts/inference.py:147-161 over
 // MambaIntegerModel.forward, src/mamba_integer_model.py:486-495) with the
 // recurrent state of a Mamba decode instead of a full-prefix recompute.
@@ -21,7 +21,7 @@ constexpr size_t kAlign = 256;
 size_t up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t r, stats, xz, xs, yo, xpart, keys, total;
+    size_t r, stats, parts, xz, xs, yo, xpart, keys, total;
 };
 
 // Sub-buffer offsets of the decode workspace for batch m.
@@ -31,7 +31,8 @@ WsLayout ws_layout(const mi_model_params &p, int m) {
     WsLayout w{};
     size_t o = 0;
     w.r = o; o += up((size_t)m * d * 4);
-    w.stats = o; o += up((size_t)(p.n_layer + 1) * m * 2 * 8);
+    w.stats = o; o += up((size_t)m * 2 * 8);
+    w.parts = o; o += up((size_t)m * (d / 16) * 2 * 8);
     w.xz = o; o += up((size_t)m * 2 * D);
     w.xs = o; o += up((size_t)m * D);
     w.yo = o; o += up((size_t)m * D);
@@ -91,13 +92,14 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
     char *base = static_cast<char *>(workspace);
     int32_t *r = reinterpret_cast<int32_t *>(base + w.r);
     int64_t *stats = reinterpret_cast<int64_t *>(base + w.stats);
+    int64_t *parts = reinterpret_cast<int64_t *>(base + w.parts);
     int8_t *xz = reinterpret_cast<int8_t *>(base + w.xz);
     int8_t *xs = reinterpret_cast<int8_t *>(base + w.xs);
     int8_t *yo = reinterpret_cast<int8_t *>(base + w.yo);
     int32_t *xpart = reinterpret_cast<int32_t *>(base + w.xpart);
     int64_t *keys = reinterpret_cast<int64_t *>(base + w.keys);
     const int d = p.d_model, D = 2 * d, N = p.d_state, R = p.dt_rank, nx = R + 2 * N;
-    const size_t stat_stride = (size_t)m * 2;
+    const int P = d / 16;  // row-statistics partials of the out_proj (one per 16 features)
 
     // every stage reports its own error; the first failure ends the step
 #define MI_STEP(call)                    \
@@ -105,18 +107,22 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
         const mi_status s_ = (call);     \
         if (s_ != MI_OK) return s_;      \
     } while (0)
-    MI_STEP(mi_embed(ids, p.emb, r, m, d, p.vocab_size, stats, p.n_layer + 1, stream));
+    MI_STEP(mi_embed(ids, p.emb, r, m, d, p.vocab_size, stats, 1, stream));
     for (int l = 0; l < p.n_layer; ++l) {
         const mi_layer_params &ly = p.layers[l];
-        MI_STEP(mi_norm_in_proj_conv_xpart(r, stats + l * stat_stride, ly.gamma, ly.w_in, ly.s_in, ly.conv_w,
-                                           ly.conv_b, conv_state[l], xs, xz, ly.w_x, nx, xpart, m, d, D, stream));
+        // layer 0 reads the embedding's full sums, later layers the partials
+        // of the previous out_proj (one buffer: each norm reads it before its
+        // layer's out_proj rewrites it, in stream order)
+        MI_STEP(mi_norm_in_proj_conv_xpart(r, l == 0 ? stats : parts, l == 0 ? 1 : P, ly.gamma, ly.w_in, ly.s_in,
+                                           ly.conv_w, ly.conv_b, conv_state[l], xs, xz, ly.w_x, nx, xpart, m, d, D,
+                                           stream));
         MI_STEP(mi_xpart_dt_scan_step(xpart, D / 16, ly.s_x, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base,
                                       ly.decay_shift, ly.s_y, h_state[l], yo, m, D, N, stream));
-        MI_STEP(mi_bitlinear_gemv(yo, D, ly.w_out, r, d, MI_OUT_RESIDUAL, m, d, D, 0, ly.res_mult, ly.res_shift,
-                                  nullptr, 0.0f, stats + (l + 1) * stat_stride, stream));
+        MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
+                                            stream));
     }
-    MI_STEP(mi_norm_bitlinear_argmax(r, stats + p.n_layer * stat_stride, p.gamma_f, p.w_head, logits, ld_logits, keys,
-                                     m, p.vocab_size, d, stream));
+    MI_STEP(mi_norm_bitlinear_argmax(r, parts, P, p.gamma_f, p.w_head, logits, ld_logits, keys, m, p.vocab_size, d,
+                                     stream));
     MI_STEP(mi_argmax_keys(keys, (p.vocab_size + 63) / 64, next_ids, m, stream));
 #undef MI_STEP
     return MI_OK;

@@ -33,18 +33,19 @@ SIGNATURES = {
     "mi_bitlinear": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
     "mi_bitlinear_gemm": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
     "mi_bitlinear_gemv": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
+    "mi_bitlinear_residual_parts": [P, I, P, P, I, I, I, I, I32, I, P, P],
     "mi_bitshift_norm": [P, P, P, I, I, P, P],
     "mi_embed": [P, P, P, I, I, I, P, I, P],
     "mi_conv_squareplus": [P, I, P, P, P, P, P, I, I, I, P],
     "mi_block_scan": [P, P, P, I, I, P, I, I, P, I, I, P, P, P, I, I, I, I, P],
     "mi_argmax_i32": [P, I, P, I, I, P],
-    "mi_norm_bitlinear": [P, P, P, P, P, I, I, I, I, I, I, P],
-    "mi_norm_in_proj_conv": [P, P, P, P, I, P, P, P, P, P, I, I, I, P],
+    "mi_norm_bitlinear": [P, P, I, P, P, P, I, I, I, I, I, I, P],
+    "mi_norm_in_proj_conv": [P, P, I, P, P, I, P, P, P, P, P, I, I, I, P],
     "mi_dt_scan_step": [P, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
     "mi_xproj_dt_scan_step": [P, P, I, I, P, I, P, I, I, P, I, I, P, P, I, I, I, P],
-    "mi_norm_in_proj_conv_xpart": [P, P, P, P, I, P, P, P, P, P, P, I, P, I, I, I, P],
+    "mi_norm_in_proj_conv_xpart": [P, P, I, P, P, I, P, P, P, P, P, P, I, P, I, I, I, P],
     "mi_xpart_dt_scan_step": [P, I, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
-    "mi_norm_bitlinear_argmax": [P, P, P, P, P, I, P, I, I, I, P],
+    "mi_norm_bitlinear_argmax": [P, P, I, P, P, P, I, P, I, I, I, P],
     "mi_argmax_keys": [P, I, P, I, P],
     "mi_embed_argmax": [P, I, P, P, P, I, I, I, P, I, P],
     "mi_decode_workspace_size": [P, I, P],

@@ -101,6 +101,11 @@ class _Workspace:
         self.yo = torch.empty((T, D), dtype=torch.int8, device=device)
         # row statistics (sum r, sum r^2) of the residual entering layer i (i = n_layer: the head)
         self.stats = torch.empty((dims.n_layer + 1, T, 2), dtype=torch.int64, device=device)
+        # decode (T <= 16): per-16-feature row-statistics partials of the out_proj,
+        # summed by the next norm (one buffer: each norm reads it before its
+        # layer's out_proj rewrites it)
+        self.parts = (torch.empty((T, d // 16, 2), dtype=torch.int64, device=device)
+                      if T <= 16 and d % 16 == 0 else None)
         # x_proj partials of the decode chain (one row per 16 channels of d_inner)
         nx = dims.dt_rank + 2 * dims.d_state
         self.xpart = (torch.empty((T, D // 16, nx), dtype=torch.int32, device=device)
@@ -131,7 +136,8 @@ class IntegerMambaRunner:
         # optional (before, after) callables around every fused scan launch
         # (the bench times that kernel with events on the launch stream)
         self.scan_timer = None
-        self._stats_valid = False
+        # row statistics of the rows the last _run left for the head (None: the head reduces them)
+        self._head_stats: Optional[torch.Tensor] = None
 
     # ------------------------------------------------------------ plumbing
     def _workspace(self, T: int) -> _Workspace:
@@ -185,28 +191,28 @@ class IntegerMambaRunner:
 
     def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
                       h_state: torch.Tensor, li: int) -> None:
-        """One token per sequence through a layer in three kernels (fused stages)."""
+        """One token per sequence through a layer in three kernels (fused stages).  The
+        norm of layer 0 reads the embedding's row statistics (ws.stats[0]), later norms
+        and the head the out_proj's per-block partials (ws.parts)."""
         dims = self.dims
-        D, R, d = dims.d_inner, dims.dt_rank, dims.d_model
+        D, R = dims.d_inner, dims.dt_rank
+        stats_in = ws.stats[0] if li == 0 else ws.parts
         if ws.xpart is not None:
             # x_proj partials from the in_proj blocks, summed by the scan step
             ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
-                                  row_stats=ws.stats[li], w_x=ly.w_x, xpart=ws.xpart)
+                                  row_stats=stats_in, w_x=ly.w_x, xpart=ws.xpart)
             ops.xpart_dt_scan_step(ws.xpart, ly.s_x, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y,
                                    h_state, ws.yo)
-            ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                          res_shift=ly.res_shift, row_stats=ws.stats[li + 1])
-            return
-        ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
-                              row_stats=ws.stats[li])
-        if dims.xp_width <= 256:
-            ops.xproj_dt_scan_step(ws.xs, ly.w_x, ly.s_x, R, ly.w_dt, ly.s_dt, ws.xz, D, ly.base, ly.k, ly.s_y,
-                                   h_state, ws.yo)
         else:
-            ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
-            ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
-        ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                      res_shift=ly.res_shift, row_stats=ws.stats[li + 1])
+            ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
+                                  row_stats=stats_in)
+            if dims.xp_width <= 256:
+                ops.xproj_dt_scan_step(ws.xs, ly.w_x, ly.s_x, R, ly.w_dt, ly.s_dt, ws.xz, D, ly.base, ly.k, ly.s_y,
+                                       h_state, ws.yo)
+            else:
+                ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+                ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
+        ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)
 
     def _head(self, r_rows: torch.Tensor, stats: Optional[torch.Tensor],
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -219,8 +225,9 @@ class IntegerMambaRunner:
     def _run(self, ids: torch.Tensor, state: DecodeState, fresh: bool) -> _Workspace:
         B, L = ids.shape
         ws = self._workspace(B * L)
-        ops.embed(ids.reshape(-1).contiguous(), self.emb, out=ws.r, row_stats=ws.stats)
+        ops.embed(ids.reshape(-1).contiguous(), self.emb, out=ws.r, row_stats=ws.stats[:1])
         decode = L == 1 and not fresh and self._fused_decode_ok(B)
+        self._head_stats = ws.parts if decode else None
         for i, ly in enumerate(self.layers):
             if decode:
                 self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
@@ -228,7 +235,6 @@ class IntegerMambaRunner:
                 # prefill: the norm of layer 0 uses the embedding's row statistics; later
                 # norms reduce their rows (atomics over 16k-row tiles cost more than they save)
                 self._layer(ly, ws, B, L, state.conv[i], state.h[i], fresh, ws.stats[0] if i == 0 else None, None)
-        self._stats_valid = decode
         return ws
 
     # ------------------------------------------------------------ public API
@@ -238,7 +244,7 @@ class IntegerMambaRunner:
         B, L = ids.shape
         state = self.new_state(B)
         ws = self._run(ids, state, fresh=True)
-        return self._head(ws.r, ws.stats[-1] if self._stats_valid else None).view(B, L, -1)
+        return self._head(ws.r, self._head_stats).view(B, L, -1)
 
     @torch.no_grad()
     def prefill(self, ids: torch.Tensor, state: Optional[DecodeState] = None
@@ -250,14 +256,14 @@ class IntegerMambaRunner:
             state = self.new_state(B)
         ws = self._run(ids, state, fresh=fresh)
         last = ws.r.view(B, L, -1)[:, -1, :].contiguous()
-        last_stats = ws.stats[-1].view(B, L, 2)[:, -1, :].contiguous() if self._stats_valid else None
-        return self._head(last, last_stats), state
+        # statistics only after a one-token step (L == 1): then the last rows are all rows
+        return self._head(last, self._head_stats if L == 1 else None), state
 
     @torch.no_grad()
     def decode_step(self, tokens: torch.Tensor, state: DecodeState) -> torch.Tensor:
         """One recurrent step for tokens [B] int64; updates `state` in place."""
         ws = self._run(tokens.view(-1, 1), state, fresh=False)
-        return self._head(ws.r, ws.stats[-1] if self._stats_valid else None)
+        return self._head(ws.r, self._head_stats)
 
     @torch.no_grad()
     def generate(self, ids: torch.Tensor, n_new: int, use_graph: bool = True) -> torch.Tensor:
@@ -310,12 +316,12 @@ class IntegerMambaRunner:
         V = self.dims.vocab_size
         for j in range(S):
             if j == 0:
-                ops.embed(hist[S - 1], self.emb, out=ws.r, row_stats=ws.stats)
+                ops.embed(hist[S - 1], self.emb, out=ws.r, row_stats=ws.stats[:1])
             else:
-                ops.embed_argmax(keys, hist[j - 1], self.emb, ws.r, ws.stats)
+                ops.embed_argmax(keys, hist[j - 1], self.emb, ws.r, ws.stats[:1])
             for i, ly in enumerate(self.layers):
                 self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
-            ops.norm_bitlinear_argmax(ws.r, self.gamma_f, self.w_head, V, keys, row_stats=ws.stats[-1])
+            ops.norm_bitlinear_argmax(ws.r, self.gamma_f, self.w_head, V, keys, row_stats=ws.parts)
         ops.argmax_keys(keys, out=hist[S - 1])
 
     def _chain_graph(self, B: int, S: int):
@@ -380,14 +386,16 @@ class IntegerMambaRunner:
                      tok_out: torch.Tensor) -> None:
         """embed -> layers -> head -> argmax for one token per sequence (graph body)."""
         B = tok.shape[0]
-        ops.embed(tok, self.emb, out=ws.r, row_stats=ws.stats)
         fused = self._fused_decode_ok(B)
+        # the fused layers hand row statistics on as out_proj partials; the others
+        # accumulate them with atomics into the per-layer rows the embed zeroes
+        ops.embed(tok, self.emb, out=ws.r, row_stats=ws.stats[:1] if fused else ws.stats)
         for i, ly in enumerate(self.layers):
             if fused:
                 self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
             else:
                 self._layer(ly, ws, B, 1, state.conv[i], state.h[i], False, ws.stats[i], ws.stats[i + 1])
-        self._head(ws.r, ws.stats[-1], out=logits)
+        self._head(ws.r, ws.parts if fused else ws.stats[-1], out=logits)
         ops.argmax(logits, out=tok_out)
 
     def _decode_graph(self, B: int, state: DecodeState):

@@ -204,6 +204,33 @@ def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
 
 
 # ------------------------------------------------------ fused decode stages
+def _stats(row_stats: Optional[torch.Tensor], m: int):
+    """(pointer, parts) of a norm's row statistics: None, int64 [m, 2] (full
+    sums) or int64 [m, parts, 2] (per-block partials, summed by the norm)."""
+    if row_stats is None:
+        return None, 1
+    _req(row_stats, torch.int64, "row_stats")
+    if row_stats.dim() == 2:
+        row_stats = row_stats.unsqueeze(1)
+    if row_stats.dim() != 3 or row_stats.shape[0] != m or row_stats.shape[2] != 2:
+        raise ValueError(f"row_stats must be [{m}, 2] or [{m}, parts, 2], got {tuple(row_stats.shape)}")
+    return _ptr(row_stats), row_stats.shape[1]
+
+
+def bitlinear_residual_parts(a: torch.Tensor, w_packed: torch.Tensor, r: torch.Tensor, res_mult: int,
+                             res_shift: int, stats_parts: torch.Tensor) -> None:
+    """Decode out_proj: r (int32 [m, n], m <= 16) += rescaled a @ W^T, and stats_parts
+    (int64 [m, ceil(n/16), 2]) <- the per-16-feature (sum, sum of squares) of the new rows."""
+    _req(a, torch.int8, "a"); _req(w_packed, torch.uint8, "w_packed"); _req(r, torch.int32, "r")
+    _req(stats_parts, torch.int64, "stats_parts")
+    m, n = r.shape
+    k = a.shape[-1]
+    if a.shape[0] != m or tuple(stats_parts.shape) != (m, (n + 15) // 16, 2):
+        raise ValueError(f"a must be [{m}, k] and stats_parts [{m}, {(n + 15) // 16}, 2]")
+    _lib.call("mi_bitlinear_residual_parts", _ptr(a), k, _ptr(w_packed), _ptr(r), n, m, n, k, int(res_mult),
+              res_shift, _ptr(stats_parts), _stream())
+
+
 def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int,
                    shift: int = 0, out=None, row_stats=None) -> torch.Tensor:
     """BitShiftNorm of r (int32 [m, k], m <= 16) fused into the BitLinear GEMV (INT8 or INT32 out)."""
@@ -211,8 +238,9 @@ def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor,
     m, k = r.shape
     o = out if out is not None else torch.empty((m, n), dtype=_OUT_DTYPE[kind], device=r.device)
     _req(o, _OUT_DTYPE[kind], "out")
-    _lib.call("mi_norm_bitlinear", _ptr(r), _ptr(_opt(row_stats, torch.int64, "row_stats")), _ptr(gamma),
-              _ptr(w_packed), _ptr(o), o.shape[-1], kind, m, n, k, shift, _stream())
+    sp, parts = _stats(row_stats, m)
+    _lib.call("mi_norm_bitlinear", _ptr(r), sp, parts, _ptr(gamma), _ptr(w_packed), _ptr(o), o.shape[-1], kind,
+              m, n, k, shift, _stream())
     return o
 
 
@@ -226,15 +254,15 @@ def norm_in_proj_conv(r, gamma, w_in, s_in: int, conv_w, conv_b, conv_state, xs,
     _req(conv_state, torch.int8, "conv_state"); _req(xs, torch.int8, "xs"); _req(xz, torch.int8, "xz")
     m, d = r.shape
     D = conv_w.shape[0]
-    stats = _ptr(_opt(row_stats, torch.int64, "row_stats"))
+    stats, parts = _stats(row_stats, m)
     if xpart is None:
-        _lib.call("mi_norm_in_proj_conv", _ptr(r), stats, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
+        _lib.call("mi_norm_in_proj_conv", _ptr(r), stats, parts, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
                   _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), m, d, D, _stream())
         return
     _req(xpart, torch.int32, "xpart"); _req(w_x, torch.uint8, "w_x")
     if tuple(xpart.shape[:2]) != (m, D // 16):
         raise ValueError(f"xpart must be [m, d_inner/16, nx], got {tuple(xpart.shape)}")
-    _lib.call("mi_norm_in_proj_conv_xpart", _ptr(r), stats, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
+    _lib.call("mi_norm_in_proj_conv_xpart", _ptr(r), stats, parts, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
               _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), _ptr(w_x), xpart.shape[-1], _ptr(xpart), m, d, D,
               _stream())
 
@@ -292,8 +320,9 @@ def norm_bitlinear_argmax(r, gamma, w_packed, n: int, keys, logits=None, row_sta
     if logits is not None:
         _req(logits, torch.int32, "logits")
         ldo = logits.stride(0)
-    _lib.call("mi_norm_bitlinear_argmax", _ptr(r), _ptr(_opt(row_stats, torch.int64, "row_stats")), _ptr(gamma),
-              _ptr(w_packed), _ptr(logits) if logits is not None else None, ldo, _ptr(keys), m, n, k, _stream())
+    sp, parts = _stats(row_stats, m)
+    _lib.call("mi_norm_bitlinear_argmax", _ptr(r), sp, parts, _ptr(gamma), _ptr(w_packed),
+              _ptr(logits) if logits is not None else None, ldo, _ptr(keys), m, n, k, _stream())
 
 
 def argmax_keys(keys, out=None) -> torch.Tensor:

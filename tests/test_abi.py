@@ -54,7 +54,12 @@ def _fake(n=64):
     (("mi_bitshift_norm", None, None, None, 4, 0, None, None), 2, "dim"),
     (("mi_conv_squareplus", None, 16, None, None, None, None, None, 1, 4, 18, None), 2, "multiple of 4"),
     (("mi_block_scan", None, None, None, 48, 16, None, 32, 16, None, 14, 13, None, None, None, 1, 4, 16, 16, None), 4, "decay_shift"),
-    (("mi_norm_bitlinear", None, None, None, None, None, 16, 1, 17, 16, 64, 0, None), 2, "m=17"),
+    (("mi_norm_bitlinear", None, None, 1, None, None, None, 16, 1, 17, 16, 64, 0, None), 2, "m=17"),
+    (("mi_norm_bitlinear", "A16", "A16", 0, "A16", "A16", "O16", 16, 1, 1, 16, 64, 0, None), 4, "stats_parts=0"),
+    (("mi_norm_bitlinear", "A16", "W4", 2, "A16", "A16", "O16", 16, 1, 1, 16, 64, 0, None), 3, "row_stats"),
+    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 17, 16, 64, 1, 0, "A16", None), 2, "m=17"),
+    (("mi_bitlinear_residual_parts", "A16", 32, "A16", "O16", 16, 1, 16, 32, 1, 0, "A16", None), 2, "multiple of 64"),
+    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 1, 16, 64, 1, 0, None, None), 1, "stats_parts"),
     (("mi_dt_scan_step", None, 80, 40, None, 2, None, None, 32, 16, None, 15, 13, None, None, 1, 16, 16, None), 2, "dt_rank"),
     (("mi_argmax_i32", None, 10, None, 1, 20, None), 2, "ld"),
 ])

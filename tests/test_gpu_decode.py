@@ -190,9 +190,9 @@ def test_xpart_decode_chain(cuda, m, d, D, N, R, stats):
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 768, 1536), (1, 768, 1536), (16, 100, 512), (3, 2048, 4096), (5, 20, 256),
-                                   (16, 64, 256 * 13)])
+                                   (16, 64, 256 * 13), (4, 96, 1600)])
 def test_decode_residual_gemv(cuda, m, n, k):
-    """The decode out_proj (RESIDUAL, m <= 16, K a multiple of 256): residual
+    """The decode out_proj (RESIDUAL, m <= 16, K a multiple of 64): residual
     update and the atomically added row statistics of the new rows."""
     import torch
     from mamba_int import ops, pack_ternary
@@ -207,6 +207,79 @@ def test_decode_residual_gemv(cuda, m, n, k):
     assert np.array_equal(H(rt), ref)
     r64 = ref.astype(np.int64)
     assert np.array_equal(H(stats), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 768, 1536), (1, 768, 1536), (16, 100, 512), (3, 2048, 4096), (5, 20, 320),
+                                   (16, 48, 64), (4, 96, 1600)])
+def test_decode_residual_parts(cuda, m, n, k):
+    """The decode out_proj with per-16-feature row-statistics partials: the
+    residual update equals the oracle's and each partial is the (sum, sum of
+    squares) of its block of the new rows (K any multiple of 64, so the last
+    256-wide chunk may be partial; n not a multiple of 16: a short last block)."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(3 * m + n + k)
+    a = i8(rng, m, k)
+    wp = pack_ternary(rng.integers(-1, 2, size=(n, k), dtype=np.int8))
+    r0 = rng.integers(-(2**23) + 1, 2**23, size=(m, n), dtype=np.int32)
+    ref = O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0, res_mult=4719, res_shift=16)
+    rt = T(r0)
+    nb = (n + 15) // 16
+    parts = torch.full((m, nb, 2), 7, dtype=torch.int64, device="cuda")
+    ops.bitlinear_residual_parts(T(a), T(wp), rt, 4719, 16, parts)
+    assert np.array_equal(H(rt), ref)
+    blk = np.zeros((m, nb * 16), np.int64)
+    blk[:, :n] = ref
+    blk = blk.reshape(m, nb, 16)
+    exp = np.stack([blk.sum(2), (blk * blk).sum(2)], -1)
+    assert np.array_equal(H(parts), exp)
+
+
+def _split_stats(rng, r, P):
+    """Row statistics of r as P random int64 partials [m, P, 2] that sum to them."""
+    r64 = r.astype(np.int64)
+    full = np.stack([r64.sum(1), (r64 * r64).sum(1)], 1)
+    parts = rng.integers(-(2**40), 2**40, size=(r.shape[0], P, 2), dtype=np.int64)
+    parts[:, -1] = full - parts[:, :-1].sum(1)
+    return parts
+
+
+@pytest.mark.parametrize("m,k,P", [(8, 768, 48), (16, 768, 48), (1, 128, 8), (3, 3072, 192), (16, 3072, 192),
+                                   (2, 256, 300), (5, 64, 2), (16, 64, 1)])
+def test_norm_stats_partials(cuda, m, k, P):
+    """The norm entries take the row statistics as stats_parts partials and sum
+    them: the narrow and wide norm GEMVs, the in_proj + conv stage and the
+    lm_head with keys equal the oracle's norm for any split of the sums (P
+    beyond 4 loads per lane group takes the kernel's extra-load loop)."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m * k + P)
+    r = _resid(rng, m, k)
+    g = rng.integers(100, 400, size=k, dtype=np.int16)
+    parts = T(_split_stats(rng, r, P))
+    a = O.bitshift_norm(r, g)
+    n = 80
+    wp = pack_ternary(rng.integers(-1, 2, size=(n, k), dtype=np.int8))
+    got = H(ops.norm_bitlinear(T(r), T(g), T(wp), ops.OUT_INT32, n, row_stats=parts))
+    assert np.array_equal(got, O.bitlinear(a, wp, O.OUT_INT32))
+    keys = torch.empty((m, (n + 63) // 64), dtype=torch.int64, device="cuda")
+    logits = torch.zeros((m, n), dtype=torch.int32, device="cuda")
+    ops.norm_bitlinear_argmax(T(r), T(g), T(wp), n, keys, logits=logits, row_stats=parts)
+    assert np.array_equal(H(logits), O.bitlinear(a, wp, O.OUT_INT32))
+    D = 64
+    wi = pack_ternary(rng.integers(-1, 2, size=(2 * D, k), dtype=np.int8))
+    cw = i8(rng, D, 4)
+    cb = rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, m, 3, D)
+    xz_ref = O.bitlinear(a, wi, O.OUT_INT8, 4)
+    xs_ref, st_ref = O.conv_squareplus(xz_ref.reshape(m, 1, 2 * D), D, cw, cb, st)
+    stg = T(st)
+    xs = torch.zeros((m, D), dtype=torch.int8, device="cuda")
+    xz = torch.zeros((m, 2 * D), dtype=torch.int8, device="cuda")
+    ops.norm_in_proj_conv(T(r), T(g), T(wi), 4, T(cw), T(cb), stg, xs, xz, row_stats=parts)
+    assert np.array_equal(H(xs), xs_ref[:, 0])
+    assert np.array_equal(H(stg), st_ref)
+    assert np.array_equal(H(xz)[:, D:], xz_ref[:, D:])
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 32000, 768), (1, 500, 128), (16, 1000, 256), (3, 64, 3072)])
