@@ -346,6 +346,47 @@ mi_status mi_decode_step(const mi_model_params *params, int m, const int64_t *id
                          int32_t *logits, int ld_logits, int8_t *const *conv_state, int32_t *const *h_state,
                          void *workspace, size_t workspace_bytes, void *stream);
 
+/* ------------------------------------------------ integer checkpoints */
+/* The integer parameters above in a versioned file (format 1, spec
+ * mi-spec-1): a 128-byte header (magic "MIQCKPT", format, spec string, dims,
+ * logit_scale, table CRC), a table of named little-endian tensors (dtype,
+ * shape, offset, bytes, CRC-32), and the tensors at 256-byte aligned offsets:
+ * 2-bit packed ternary matrices, int8 embedding and conv taps, int32 conv
+ * bias and decay numerators, int16 gains, and the per-layer shifts.
+ * Replaces the reference's inference export (scripts/export_int8.py:50-135,
+ * magic 0xDAD1C: float embedding, conv and gains, one byte per ternary
+ * weight plus a float scale) and its loader load_model
+ * (src/cpp_engine/mamba_infer.cpp:46-118), which exit()s on any error and
+ * allocates every tensor itself.  Files are written by
+ * mamba_int.checkpoint.save and converted from the reference's float state
+ * dicts by mamba_int.checkpoint.convert_state_dict. */
+typedef struct mi_checkpoint mi_checkpoint;
+
+typedef struct mi_checkpoint_info {
+    int format_version;
+    char spec[16];             /* "mi-spec-1" */
+    int d_model, n_layer, vocab_size, d_state, dt_rank;
+    float logit_scale;         /* float logits = int32 logits * logit_scale (> 0) */
+    size_t device_bytes;       /* bytes mi_checkpoint_upload fills */
+} mi_checkpoint_info;
+
+/* Reads a checkpoint into host memory and validates it: magic, format,
+ * spec, dims, table CRC, every tensor's dtype, shape (against the dims),
+ * alignment and CRC-32, the ternary codes, the shifts (decay shift 15) and
+ * decays in [0, 32000].  *out is NULL on failure; close with
+ * mi_checkpoint_close. */
+mi_status mi_checkpoint_open(const char *path, mi_checkpoint **out);
+mi_status mi_checkpoint_get_info(const mi_checkpoint *ck, mi_checkpoint_info *info);
+/* Copies every tensor into `device` (256-byte aligned, at least
+ * info.device_bytes) on `stream`, waits for the copies, and fills *params
+ * (its `layers` = the caller's HOST array `layers` of n_layers = n_layer
+ * entries) with pointers into `device`, ready for mi_decode_step.  No device
+ * allocation. */
+mi_status mi_checkpoint_upload(const mi_checkpoint *ck, void *device, size_t device_bytes,
+                               mi_model_params *params, mi_layer_params *layers, int n_layers,
+                               void *stream);
+void mi_checkpoint_close(mi_checkpoint *ck);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,9 @@ SIGNATURES = {
     "mi_embed_argmax": [P, I, P, P, P, I, I, I, P, I, P],
     "mi_decode_workspace_size": [P, I, P],
     "mi_decode_step": [P, I, P, P, P, I, P, P, P, ctypes.c_size_t, P],
+    "mi_checkpoint_open": [ctypes.c_char_p, P],
+    "mi_checkpoint_get_info": [P, P],
+    "mi_checkpoint_upload": [P, P, ctypes.c_size_t, P, P, I, P],
 }
 
 
@@ -80,6 +83,8 @@ def load() -> ctypes.CDLL:
         lib.mi_version.argtypes = []
         lib.mi_last_error_string.restype = ctypes.c_char_p
         lib.mi_last_error_string.argtypes = []
+        lib.mi_checkpoint_close.restype = None
+        lib.mi_checkpoint_close.argtypes = [P]
         for name, args in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args

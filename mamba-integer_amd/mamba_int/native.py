@@ -33,29 +33,77 @@ class ModelParams(ctypes.Structure):
                 ("emb", _P), ("layers", ctypes.POINTER(LayerParams)), ("gamma_f", _P), ("w_head", _P)]
 
 
+class CheckpointInfo(ctypes.Structure):
+    """Mirror of ``mi_checkpoint_info``."""
+    _fields_ = [("format_version", _I), ("spec", ctypes.c_char * 16), ("d_model", _I), ("n_layer", _I),
+                ("vocab_size", _I), ("d_state", _I), ("dt_rank", _I), ("logit_scale", ctypes.c_float),
+                ("device_bytes", ctypes.c_size_t)]
+
+
 def _ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
+class NativeCheckpoint:
+    """An integer checkpoint read and validated by the native loader
+    (``mi_checkpoint_open``) and, with a device, uploaded into one device
+    buffer (``mi_checkpoint_upload``) that ``params`` points into: the C++
+    engine's ``load_model`` (``src/cpp_engine/mamba_infer.cpp:46-118``) with
+    status codes instead of exit() and no allocation inside the library."""
+
+    def __init__(self, path: str, device=None):
+        ck = _P()
+        _lib.call("mi_checkpoint_open", str(path).encode(), ctypes.byref(ck))
+        try:
+            self.info = CheckpointInfo()
+            _lib.call("mi_checkpoint_get_info", ck, ctypes.byref(self.info))
+            self.params = None
+            if device is not None:
+                n = self.info.n_layer
+                self.buffer = torch.empty(self.info.device_bytes, dtype=torch.uint8, device=device)
+                self._layers = (LayerParams * n)()
+                self.params = ModelParams()
+                _lib.call("mi_checkpoint_upload", ck, _P(_ptr(self.buffer)), ctypes.c_size_t(self.info.device_bytes),
+                          ctypes.byref(self.params), self._layers, n,
+                          _P(torch.cuda.current_stream(self.buffer.device).cuda_stream))
+        finally:
+            _lib.load().mi_checkpoint_close(ck)
+
+    def decoder(self, m: int) -> "NativeDecoder":
+        if self.params is None:
+            raise ValueError("the checkpoint was opened without a device")
+        return NativeDecoder.from_params(self.params, self.buffer.device, m, owner=self)
+
+
 class NativeDecoder:
-    """Greedy decode through ``mi_decode_step`` for the device parameters of an
-    ``IntegerMambaRunner`` at batch m (1 <= m <= 16)."""
+    """Greedy decode through ``mi_decode_step`` at batch m (1 <= m <= 16), for
+    the device parameters of an ``IntegerMambaRunner`` or of a
+    ``NativeCheckpoint`` (``from_params``)."""
 
     def __init__(self, runner, m: int):
         dims = runner.dims
-        self.runner, self.m = runner, m
-        self._layers = (LayerParams * dims.n_layer)()
+        layers = (LayerParams * dims.n_layer)()
         for i, ly in enumerate(runner.layers):
-            self._layers[i] = LayerParams(_ptr(ly.gamma), _ptr(ly.w_in), ly.s_in, _ptr(ly.conv_w), _ptr(ly.conv_b),
-                                          _ptr(ly.w_x), ly.s_x, _ptr(ly.w_dt), ly.s_dt, _ptr(ly.base), ly.k, ly.s_y,
-                                          _ptr(ly.w_out), ly.res_mult, ly.res_shift)
-        self.params = ModelParams(dims.d_model, dims.n_layer, dims.vocab_size, dims.d_state, dims.dt_rank,
-                                  _ptr(runner.emb), self._layers, _ptr(runner.gamma_f), _ptr(runner.w_head))
+            layers[i] = LayerParams(_ptr(ly.gamma), _ptr(ly.w_in), ly.s_in, _ptr(ly.conv_w), _ptr(ly.conv_b),
+                                    _ptr(ly.w_x), ly.s_x, _ptr(ly.w_dt), ly.s_dt, _ptr(ly.base), ly.k, ly.s_y,
+                                    _ptr(ly.w_out), ly.res_mult, ly.res_shift)
+        params = ModelParams(dims.d_model, dims.n_layer, dims.vocab_size, dims.d_state, dims.dt_rank,
+                             _ptr(runner.emb), layers, _ptr(runner.gamma_f), _ptr(runner.w_head))
+        self._setup(params, runner.device, m, owner=(runner, layers))
+
+    @classmethod
+    def from_params(cls, params: ModelParams, device, m: int, owner=None) -> "NativeDecoder":
+        self = cls.__new__(cls)
+        self._setup(params, device, m, owner)
+        return self
+
+    def _setup(self, params: ModelParams, device, m: int, owner) -> None:
+        self.owner, self.m, self.params = owner, m, params  # owner keeps the device tensors alive
         self._pp = ctypes.cast(ctypes.pointer(self.params), _P)
         nbytes = ctypes.c_size_t(0)
         _lib.call("mi_decode_workspace_size", self._pp, m, ctypes.cast(ctypes.pointer(nbytes), _P))
         self.ws_bytes = nbytes.value
-        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=runner.device)
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
 
     def step(self, ids: torch.Tensor, state, next_ids: torch.Tensor, logits=None) -> torch.Tensor:
         """One step: ids [m] int64 -> next_ids [m] int64 (and int32 logits [m, V] when given);

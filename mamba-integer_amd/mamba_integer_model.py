@@ -24,7 +24,7 @@ import numpy as np
 import torch
 import torch.nn as nn
 
-from mamba_int import ops
+from mamba_int import checkpoint, ops
 from mamba_int.model import IntegerMambaRunner
 from mamba_int.params import (DECAY_SHIFT, LayerParams, ModelDims, ModelParams,
                               init_random_params, requant_shift)
@@ -116,6 +116,19 @@ class MambaIntegerModel(nn.Module):
         # logits_float = logit_int * 2^-4 (Q4 activations) / sqrt(2K/3) * output_scale
         self.logit_scale = self.output_scale / 16.0 / math.sqrt(2.0 * self.dims.d_model / 3.0)
         self._runner: Optional[IntegerMambaRunner] = None
+
+    @classmethod
+    def from_checkpoint(cls, path: str) -> "MambaIntegerModel":
+        """The model of a format-1 integer checkpoint (``mamba_int.checkpoint``:
+        written by ``save`` or converted from a reference float state dict by
+        ``convert_reference_checkpoint``), with its stored logit scale."""
+        params, logit_scale = checkpoint.load(path)
+        d = params.dims
+        config = {"d_model": d.d_model, "n_layer": d.n_layer, "vocab_size": d.vocab_size,
+                  "ssm_cfg": {"d_state": d.d_state, "dt_rank": d.dt_rank}}
+        model = cls(config, params=params)
+        model.logit_scale = logit_scale
+        return model
 
     def runner(self, device="cuda") -> IntegerMambaRunner:
         if self._runner is None or self._runner.device != torch.device(device):

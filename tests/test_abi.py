@@ -14,7 +14,7 @@ HEADER = os.path.join(REPO, "include", "mamba_int.h")
 
 def declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:mi_status|const char \*)\s*(mi_\w+)\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:mi_status|const char \*|void)\s*(mi_\w+)\(", text, flags=re.M)))
 
 
 def test_header_declares_entry_points():
@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared():
         assert hasattr(lib, name), name
-    bound = set(_lib.SIGNATURES) | {"mi_version", "mi_last_error_string"}
+    bound = set(_lib.SIGNATURES) | {"mi_version", "mi_last_error_string", "mi_checkpoint_close"}
     assert set(declared()) == bound
 
 
@@ -106,21 +106,25 @@ def test_decode_step_struct_layout_matches_header(tmp_path):
     """The ctypes mirrors of mi_layer_params / mi_model_params have the C
     compiler's sizes and field offsets (a C program built from the header)."""
     import subprocess
-    from mamba_int.native import LayerParams, ModelParams
+    from mamba_int.native import CheckpointInfo, LayerParams, ModelParams
     src = tmp_path / "layout.c"
     lf = [f[0] for f in LayerParams._fields_]
     mf = [f[0] for f in ModelParams._fields_]
+    cf = [f[0] for f in CheckpointInfo._fields_]
     src.write_text("#include <stdio.h>\n#include <stddef.h>\n#include \"mamba_int.h\"\nint main(void){\n"
                    + 'printf("%zu\\n", sizeof(mi_layer_params));\n'
                    + "".join(f'printf("%zu\\n", offsetof(mi_layer_params, {f}));\n' for f in lf)
                    + 'printf("%zu\\n", sizeof(mi_model_params));\n'
                    + "".join(f'printf("%zu\\n", offsetof(mi_model_params, {f}));\n' for f in mf)
+                   + 'printf("%zu\\n", sizeof(mi_checkpoint_info));\n'
+                   + "".join(f'printf("%zu\\n", offsetof(mi_checkpoint_info, {f}));\n' for f in cf)
                    + "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = ([ctypes.sizeof(LayerParams)] + [getattr(LayerParams, f).offset for f in lf]
-            + [ctypes.sizeof(ModelParams)] + [getattr(ModelParams, f).offset for f in mf])
+            + [ctypes.sizeof(ModelParams)] + [getattr(ModelParams, f).offset for f in mf]
+            + [ctypes.sizeof(CheckpointInfo)] + [getattr(CheckpointInfo, f).offset for f in cf])
     assert got == want
 
 
