@@ -197,6 +197,29 @@ mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int8_t *xp, in
                         const int32_t *h_in, int32_t *h_out, int batch, int len, int d_inner,
                         int nstate, void *stream);
 
+/* BitShiftNormV2 (ssd_multihead.py:595-632; spec rule 7.1): mi_bitshift_norm
+ * with the V2 threshold table (scales 2^-1 .. 2^-6 for var >= 4 .. 4096, 2
+ * and 4 for var < 1/4 and < 1/16), the norm of the multi-head SSD block. */
+mi_status mi_bitshift_norm_v2(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens,
+                              int dim, const int64_t *row_stats, void *stream);
+
+/* Scan of the multi-head SSD block (MambaIntegerBlockV2.forward,
+ * ssd_multihead.py:536-586, over ssd_multihead_forward :92-244; spec rules
+ * 7.3-7.8): per token and head, B and C scaled to unit vectors (Q7), the
+ * decay decay_tab[h][dt + 127] (int32 [n_heads][255] in [0, 32768], shift
+ * 15), h = floor(h * n / 2^15) + B (x) x, y = C . h clamped to +-100 (Q18),
+ * gate by z, requant by s_y.  xs int8 [batch,len,d_inner] (d_inner =
+ * n_heads * d_head, d_head % 16 == 0); xp int8 [batch,len,xp_stride] planar:
+ * B of head h at columns [h*nstate, (h+1)*nstate), C at n_heads*nstate +
+ * h*nstate, dt at 2*n_heads*nstate + h; z int8 [batch,len,z_stride] at
+ * column z_off; yo int8 [batch,len,d_inner]; h_in / h_out int32
+ * [batch,n_heads,d_head,nstate] nullable (in == out allowed).  nstate in
+ * {16, 32, 64}; rows and xs/xp/z/yo 16-byte aligned. */
+mi_status mi_ssd_block_scan(const int8_t *xs, const int8_t *xp, int xp_stride, const int8_t *z,
+                            int z_stride, int z_off, const int32_t *decay_tab, int n_heads, int s_y,
+                            int8_t *yo, const int32_t *h_in, int32_t *h_out, int batch, int len,
+                            int d_inner, int nstate, void *stream);
+
 /* Greedy pick (scripts/sft_mamba_integer.py:138-141 argmax): out[r] = first
  * index of the maximum of logits[r, 0:cols] (int32 [rows, ld]). */
 mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, int cols,

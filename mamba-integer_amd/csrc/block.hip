@@ -22,6 +22,8 @@ __device__ int64_t block_sum64(int64_t v, int64_t *red) {
     return t;
 }
 
+// V2: the threshold table of BitShiftNormV2 (spec rule 7.1) instead of 4.1.
+template <bool V2>
 __global__ __launch_bounds__(kNormThreads) void norm_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
                                                             int dim) {
     __shared__ int64_t red[kNormThreads / 64];
@@ -47,10 +49,10 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(const int32_t *r, co
     const int64_t S = block_sum64(q, red);
     // threshold table of _find_power_of_2_scale (mamba_integer_model.py:169-182)
     // on var = S / (dim * 2^16): k = #[var >= 4^j, j=1..8] - #[var < 4^-j, j=1..3]
-    int kk = 0;
-    for (int j = 1; j <= 8; ++j) kk += S >= ((int64_t)dim << (2 * (j + 8)));
-    for (int j = 1; j <= 3; ++j) kk -= S < ((int64_t)dim << (2 * (8 - j)));
-    const int sh = 12 + kk;
+    // (V2: j=1..6 and j=1..2); norm_shift_for takes the statistics, so S is
+    // passed as s2 with s1 = 0 about the already-subtracted mean
+    int64_t zero_mu;
+    const int sh = norm_shift_for<V2>(0, S, dim, &zero_mu);
     for (int j = 0; j < kNormMaxPer; ++j) {
         const int i = threadIdx.x + j * kNormThreads;
         if (i < dim) out[row * dim + i] = (int8_t)clamp64(rshr64((int64_t)(v[j] - mu) * gamma[i], sh), -127, 127);
@@ -61,6 +63,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(const int32_t *r, co
 // dim <= 4096) while its sum and sum of squares are reduced.
 constexpr int kNormWaveMax = 16;
 
+template <bool V2>
 __global__ __launch_bounds__(256) void norm_wave_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
                                                         int tokens, int dim) {
     const int lane = threadIdx.x & 63;
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const int32_t *r, const 
         s2 += __shfl_xor(s2, off);
     }
     int64_t mu;
-    const int sh = norm_shift(s1, s2, dim, &mu);
+    const int sh = norm_shift_for<V2>(s1, s2, dim, &mu);
 #pragma unroll
     for (int j = 0; j < kNormWaveMax; ++j) {
         const int i = 4 * lane + 256 * j;
@@ -202,6 +205,7 @@ __global__ __launch_bounds__(256) void embed_argmax_kernel(const int64_t *keys, 
 }
 
 // Elementwise BitShiftNorm from precomputed row statistics: thread = 4 channels.
+template <bool V2>
 __global__ __launch_bounds__(256) void norm_stats_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
                                                          const int64_t *stats, int tokens, int dim) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(256) void norm_stats_kernel(const int32_t *r, const
     const int64_t t = i / d4;
     const int c = (int)(i % d4) * 4;
     int64_t mu;
-    const int sh = norm_shift(stats[2 * t], stats[2 * t + 1], dim, &mu);
+    const int sh = norm_shift_for<V2>(stats[2 * t], stats[2 * t + 1], dim, &mu);
     const int4 v = *reinterpret_cast<const int4 *>(r + t * dim + c);
     const int vv[4] = {v.x, v.y, v.z, v.w};
     uint32_t o = 0;
@@ -336,28 +340,43 @@ __global__ __launch_bounds__(256) void argmax_kernel(const int32_t *logits, int6
 
 using namespace mi;
 
-extern "C" mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
-                                      const int64_t *row_stats, void *stream) {
+namespace mi {
+namespace {
+template <bool V2>
+mi_status bitshift_norm_impl(const char *fn, const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
+                             const int64_t *row_stats, void *stream) {
     clear_error();
-    MI_REQUIRE(tokens >= 0, MI_ERR_BAD_DIM, "mi_bitshift_norm: negative tokens");
-    MI_REQUIRE(dim >= 1 && dim <= kNormThreads * kNormMaxPer, MI_ERR_BAD_DIM, "mi_bitshift_norm: dim=%d outside [1,%d]",
-               dim, kNormThreads * kNormMaxPer);
+    MI_REQUIRE(tokens >= 0, MI_ERR_BAD_DIM, "%s: negative tokens", fn);
+    MI_REQUIRE(dim >= 1 && dim <= kNormThreads * kNormMaxPer, MI_ERR_BAD_DIM, "%s: dim=%d outside [1,%d]", fn, dim,
+               kNormThreads * kNormMaxPer);
     if (tokens == 0) return MI_OK;
-    MI_REQUIRE(r && gamma && out, MI_ERR_NULL_POINTER, "mi_bitshift_norm: r, gamma and out are required");
+    MI_REQUIRE(r && gamma && out, MI_ERR_NULL_POINTER, "%s: r, gamma and out are required", fn);
     if (row_stats) {
         MI_REQUIRE(dim % 4 == 0 && aligned(r, 16) && aligned(out, 4), MI_ERR_BAD_ALIGNMENT,
-                   "mi_bitshift_norm: with row_stats, dim %% 4 == 0 and aligned r/out are required");
+                   "%s: with row_stats, dim %% 4 == 0 and aligned r/out are required", fn);
         const int64_t threads = (int64_t)tokens * (dim / 4);
-        hipLaunchKernelGGL(norm_stats_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, as_stream(stream), r,
-                           gamma, out, row_stats, tokens, dim);
+        hipLaunchKernelGGL(norm_stats_kernel<V2>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           as_stream(stream), r, gamma, out, row_stats, tokens, dim);
     } else if (dim % 4 == 0 && dim <= 256 * kNormWaveMax && aligned(r, 16) && aligned(out, 4)) {
-        hipLaunchKernelGGL(norm_wave_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, as_stream(stream), r,
-                           gamma, out, tokens, dim);
+        hipLaunchKernelGGL(norm_wave_kernel<V2>, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, as_stream(stream),
+                           r, gamma, out, tokens, dim);
     } else {
-        hipLaunchKernelGGL(norm_kernel, dim3((unsigned)tokens), dim3(kNormThreads), 0, as_stream(stream), r, gamma, out,
-                           dim);
+        hipLaunchKernelGGL(norm_kernel<V2>, dim3((unsigned)tokens), dim3(kNormThreads), 0, as_stream(stream), r, gamma,
+                           out, dim);
     }
-    return check_launch("mi_bitshift_norm");
+    return check_launch(fn);
+}
+}  // namespace
+}  // namespace mi
+
+extern "C" mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
+                                      const int64_t *row_stats, void *stream) {
+    return bitshift_norm_impl<false>("mi_bitshift_norm", r, gamma, out, tokens, dim, row_stats, stream);
+}
+
+extern "C" mi_status mi_bitshift_norm_v2(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
+                                         const int64_t *row_stats, void *stream) {
+    return bitshift_norm_impl<true>("mi_bitshift_norm_v2", r, gamma, out, tokens, dim, row_stats, stream);
 }
 
 extern "C" mi_status mi_embed(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab,

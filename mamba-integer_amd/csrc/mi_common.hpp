@@ -57,14 +57,25 @@ __host__ __device__ __forceinline__ uint64_t isqrt64(uint64_t v) {
 // S = sum (r - mu)^2 = s2 - 2 mu s1 + dim mu^2 (exact in int64 for
 // |r| < 2^23, dim <= 8192); returns the output shift 12 + k of the threshold
 // table (mamba_integer_model.py:169-182 on var = S / (dim * 2^16)).
-__host__ __device__ __forceinline__ int norm_shift(int64_t s1, int64_t s2, int dim, int64_t *mu_out) {
+// KMAX / KMIN: the table's count of "var >= 4^j" and "var < 4^-j" steps.
+template <int KMAX, int KMIN>
+__host__ __device__ __forceinline__ int norm_shift_tab(int64_t s1, int64_t s2, int dim, int64_t *mu_out) {
     const int64_t mu = s1 >= 0 ? s1 / dim : -((-s1 + dim - 1) / dim);
     const int64_t S = s2 - 2 * mu * s1 + (int64_t)dim * mu * mu;
     int kk = 0;
-    for (int j = 1; j <= 8; ++j) kk += S >= ((int64_t)dim << (2 * (j + 8)));
-    for (int j = 1; j <= 3; ++j) kk -= S < ((int64_t)dim << (2 * (8 - j)));
+    for (int j = 1; j <= KMAX; ++j) kk += S >= ((int64_t)dim << (2 * (j + 8)));
+    for (int j = 1; j <= KMIN; ++j) kk -= S < ((int64_t)dim << (2 * (8 - j)));
     *mu_out = mu;
     return 12 + kk;
+}
+__host__ __device__ __forceinline__ int norm_shift(int64_t s1, int64_t s2, int dim, int64_t *mu_out) {
+    return norm_shift_tab<8, 3>(s1, s2, dim, mu_out);
+}
+// BitShiftNormV2's table (ssd_multihead.py:613-629; spec rule 7.1): scales
+// 2^-1 .. 2^-6 for var >= 4 .. 4096, 2 and 4 for var < 1/4 and < 1/16.
+template <bool V2>
+__host__ __device__ __forceinline__ int norm_shift_for(int64_t s1, int64_t s2, int dim, int64_t *mu_out) {
+    return V2 ? norm_shift_tab<6, 2>(s1, s2, dim, mu_out) : norm_shift_tab<8, 3>(s1, s2, dim, mu_out);
 }
 
 // dt of spec rule 4.8 (mamba_integer_model.py:427) for dm in [-20, 20].

@@ -21,6 +21,7 @@
 #include <type_traits>
 
 #include "mi_common.hpp"
+#include "mi_mfma.hpp"
 
 namespace mi {
 namespace {
@@ -262,7 +263,267 @@ hipError_t launch_model_n(int G, const MScanArgs &a, hipStream_t st) {
     return hipErrorInvalidValue;
 }
 
+// ------------------------------------------------ SSD block scan (V2)
+// The scan of MambaIntegerBlockV2 (spec rules 7.4-7.8; ssd_multihead.py:
+// 536-586): per (sequence, head) a P x N state with one decay per step and
+// head, h = floor(h * n_t / 2^15) + Bq[n] * x[p], y = sum_n Cq[n] h, clamp,
+// gate, requant.  Same lane layout as model_scan_kernel (G lanes per channel,
+// S = N/G states each, split h = hh*2^15 + hl); a block's CH channels lie in
+// one head.  Per chunk the block stages x and z (channel-major), the step
+// decays (table lookup of the head's dt column) and B, C: each 16-byte piece
+// of a token's B (or C) row sums its squares, the token's N/16 pieces (lanes
+// of one quad) add up by DPP, and every piece is scaled to the unit vector in
+// Q7 before it lands in LDS, so the steps read finished coefficients.
+struct SScanArgs {
+    const int8_t *xs, *z, *xp;     // [B*L rows][row stride]; z points at its first column
+    const int32_t *tab;            // [H][255]
+    int8_t *yo;
+    const int32_t *h_in;
+    int32_t *h_out;
+    int64_t x_row, z_row, xp_row;
+    int B, L, D, H, P, s_y;
+};
+
+// Q7 unit-vector scale of spec rule 7.4 from the row's sum of squares
+__device__ __forceinline__ int32_t unit_inv(int32_t ss) {
+    if (ss == 0) return 0;
+    const uint32_t nrm = (uint32_t)isqrt64((uint64_t)ss << 16);
+    return (int32_t)((1u << 30) / nrm);
+}
+
+template <int N, int G>
+__global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
+    constexpr int S = N / G;
+    constexpr int CH = kMThreads / G;
+    constexpr int XP = kMTC + 4;
+    constexpr int X16 = CH / 16;
+    constexpr int XPIECES = kMTC * X16;
+    constexpr int XPER = (XPIECES + kMThreads - 1) / kMThreads;
+    constexpr int BC16 = N / 16;
+    constexpr int BCPIECES = kMTC * BC16;
+    constexpr int BCPER = (BCPIECES + kMThreads - 1) / kMThreads;
+    static_assert(N % 16 == 0 && BC16 <= 4 && (S == 1 || S == 2 || S % 4 == 0), "state split");
+    static_assert(BCPIECES % 64 == 0 || BCPIECES < 64, "whole waves stage B and C");
+
+    __shared__ __align__(16) int8_t s_x[2][CH][XP];        // xs, z (channel-major)
+    __shared__ __align__(16) int32_t s_b[kMTC][N];
+    __shared__ __align__(16) int32_t s_c[kMTC][N];
+    __shared__ __align__(16) int2 s_y[kMTC][CH];
+    __shared__ __align__(16) int8_t s_o[kMTC][CH];
+    __shared__ __align__(16) int32_t s_n[kMTC];
+    __shared__ int32_t s_tab[256];
+    __shared__ int32_t s_gate[256];
+
+    const int tid = threadIdx.x;
+    const int ch = tid / G;
+    const int g = tid % G;
+    const int p0 = blockIdx.x * CH;
+    const int head = p0 / a.P;
+    const int b = blockIdx.y;
+    const int p = p0 + ch;
+
+    for (int i = tid; i < 255; i += kMThreads) s_tab[i] = a.tab[(int64_t)head * 255 + i];
+    for (int i = tid; i < 256; i += kMThreads) s_gate[i] = gate_q15(i - 128);
+
+    int32_t hh[S], hl[S];
+    {
+        const int64_t sidx = ((int64_t)b * a.D + p) * N + g * S;
+        for (int s = 0; s < S; ++s) {
+            const int32_t hv = a.h_in ? a.h_in[sidx + s] : 0;
+            hh[s] = hv >> 15;
+            hl[s] = hv & 0x7fff;
+        }
+    }
+
+    // ext_vector_type registers (a union-typed uint4 array touched through
+    // lambdas is kept in scratch)
+    v4i rx[2][XPER];
+    v4i rb[BCPER], rc[BCPER];
+    int dtv = 0;
+    const int64_t row0 = (int64_t)b * a.L;
+    const int64_t b_col = (int64_t)head * N, c_col = (int64_t)a.H * N + head * N, dt_col = 2 * (int64_t)a.H * N + head;
+    auto prefetch = [&](int t0) {
+        for (int j = 0; j < XPER; ++j) {
+            const int i = tid + j * kMThreads;
+            const int tt = i / X16, c16 = i % X16;
+            const bool ok = i < XPIECES && t0 + tt < a.L;
+            const int64_t rr = row0 + t0 + tt;
+            const v4i zero = v4i{0, 0, 0, 0};
+            rx[0][j] = ok ? *reinterpret_cast<const v4i *>(a.xs + rr * a.x_row + p0 + c16 * 16) : zero;
+            rx[1][j] = ok ? *reinterpret_cast<const v4i *>(a.z + rr * a.z_row + p0 + c16 * 16) : zero;
+        }
+        for (int j = 0; j < BCPER; ++j) {
+            const int i = tid + j * kMThreads;
+            const int tt = i / BC16, c16 = i % BC16;
+            const bool ok = i < BCPIECES && t0 + tt < a.L;
+            const int64_t off = (row0 + t0 + tt) * a.xp_row + c16 * 16;
+            rb[j] = ok ? *reinterpret_cast<const v4i *>(a.xp + off + b_col) : v4i{0, 0, 0, 0};
+            rc[j] = ok ? *reinterpret_cast<const v4i *>(a.xp + off + c_col) : v4i{0, 0, 0, 0};
+        }
+        dtv = (tid < kMTC && t0 + tid < a.L) ? a.xp[(row0 + t0 + tid) * a.xp_row + dt_col] : 0;
+    };
+    // sum of squares of a 16-byte piece of int8
+    auto sumsq = [](v4i v) {
+        const uint32_t w[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+        int ss = 0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int q = sb(w[e >> 2], e & 3);
+            ss += q * q;
+        }
+        return ss;
+    };
+    auto stash = [&]() {
+        for (int j = 0; j < XPER; ++j) {
+            const int i = tid + j * kMThreads;
+            if (i >= XPIECES) break;
+            const int tt = i / X16, c16 = i % X16;
+            const uint32_t wx[4] = {(uint32_t)rx[0][j][0], (uint32_t)rx[0][j][1], (uint32_t)rx[0][j][2],
+                                    (uint32_t)rx[0][j][3]};
+            const uint32_t wz[4] = {(uint32_t)rx[1][j][0], (uint32_t)rx[1][j][1], (uint32_t)rx[1][j][2],
+                                    (uint32_t)rx[1][j][3]};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                s_x[0][c16 * 16 + e][tt] = (int8_t)sb(wx[e >> 2], e & 3);
+                s_x[1][c16 * 16 + e][tt] = (int8_t)sb(wz[e >> 2], e & 3);
+            }
+        }
+        for (int j = 0; j < BCPER; ++j) {
+            const int i = tid + j * kMThreads;
+            if (i - (tid & 63) >= BCPIECES) break;  // whole waves: the DPP sums below need every lane
+            const int tt = i / BC16, c16 = i % BC16;
+            // the token's pieces are BC16 adjacent lanes of one quad
+            int sbq = sumsq(rb[j]), scq = sumsq(rc[j]);
+            if constexpr (BC16 >= 2) {
+                sbq += __builtin_amdgcn_update_dpp(0, sbq, 0xB1, 0xF, 0xF, true);
+                scq += __builtin_amdgcn_update_dpp(0, scq, 0xB1, 0xF, 0xF, true);
+            }
+            if constexpr (BC16 >= 4) {
+                sbq += __builtin_amdgcn_update_dpp(0, sbq, 0x4E, 0xF, 0xF, true);
+                scq += __builtin_amdgcn_update_dpp(0, scq, 0x4E, 0xF, 0xF, true);
+            }
+            const int32_t ib = unit_inv(sbq), ic = unit_inv(scq);
+            const uint32_t wb[4] = {(uint32_t)rb[j][0], (uint32_t)rb[j][1], (uint32_t)rb[j][2], (uint32_t)rb[j][3]};
+            const uint32_t wc[4] = {(uint32_t)rc[j][0], (uint32_t)rc[j][1], (uint32_t)rc[j][2], (uint32_t)rc[j][3]};
+            if (i < BCPIECES) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    s_b[tt][c16 * 16 + e] = clamp32(rshr32(sb(wb[e >> 2], e & 3) * ib, 15), -127, 127);
+                    s_c[tt][c16 * 16 + e] = clamp32(rshr32(sb(wc[e >> 2], e & 3) * ic, 15), -127, 127);
+                }
+            }
+        }
+        if (tid < kMTC) s_n[tid] = s_tab[clamp32(dtv, -127, 127) + 127];
+    };
+
+    auto step = [&](int t, int xv, int nt) {
+        int bv[S], cv[S];
+        if constexpr (S >= 4) {
+            for (int q = 0; q < S / 4; ++q) {
+                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[t][g * S + 4 * q]);
+                const int4 c4 = *reinterpret_cast<const int4 *>(&s_c[t][g * S + 4 * q]);
+                bv[4 * q] = b4.x; bv[4 * q + 1] = b4.y; bv[4 * q + 2] = b4.z; bv[4 * q + 3] = b4.w;
+                cv[4 * q] = c4.x; cv[4 * q + 1] = c4.y; cv[4 * q + 2] = c4.z; cv[4 * q + 3] = c4.w;
+            }
+        } else {
+            for (int s = 0; s < S; ++s) {
+                bv[s] = s_b[t][g * S + s];
+                cv[s] = s_c[t][g * S + s];
+            }
+        }
+        int yhi = 0, ylo = 0;
+        for (int s = 0; s < S; ++s) {
+            const int u = __mul24(bv[s], xv);
+            const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt) >> 15);
+            const int d = __mul24(hh[s], nt) + c;
+            const int hn = __builtin_elementwise_add_sat(d, u);
+            hh[s] = hn >> 15;
+            hl[s] = hn & 0x7fff;
+            yhi += __mul24(cv[s], hh[s]);
+            ylo += __mul24(cv[s], hl[s]);
+        }
+        yhi = msum<G>(yhi);
+        ylo = msum<G>(ylo);
+        s_y[t][ch] = make_int2(yhi, ylo);
+    };
+
+    const int32_t ylim = 100 << 18;
+    const int nchunks = (a.L + kMTC - 1) / kMTC;
+    prefetch(0);
+    for (int cidx = 0; cidx < nchunks; ++cidx) {
+        const int t0 = cidx * kMTC;
+        const int tn = min(kMTC, a.L - t0);
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (cidx + 1 < nchunks) prefetch(t0 + kMTC);
+        for (int t4 = 0; t4 < tn; t4 += 4) {
+            const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_x[0][ch][t4]);
+            const int4 n4 = *reinterpret_cast<const int4 *>(&s_n[t4]);
+            const int nv[4] = {n4.x, n4.y, n4.z, n4.w};
+            if (t4 + 4 <= tn) {
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) step(t4 + tt, sb(xw, tt), nv[tt]);
+            } else {
+                for (int tt = 0; tt < tn - t4; ++tt) step(t4 + tt, sb(xw, tt), s_n[t4 + tt]);
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < kMTC * CH; i += kMThreads) {
+            const int tt = i / CH, cc = i % CH;
+            if (tt < tn) {
+                const int2 yv = s_y[tt][cc];
+                const int32_t y32 = clamp32(sat32_64(((int64_t)yv.x << 15) + yv.y), -ylim, ylim);
+                const int32_t gt = s_gate[s_x[1][cc][tt] + 128];
+                const int32_t yh = y32 >> 15, yl = y32 & 0x7fff;
+                const int32_t yg = yh * gt + (int32_t)(((uint32_t)yl * (uint32_t)gt) >> 15);
+                s_o[tt][cc] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < kMTC * X16; i += kMThreads) {
+            const int tt = i / X16, c16 = i % X16;
+            if (tt < tn)
+                *reinterpret_cast<uint4 *>(a.yo + (row0 + t0 + tt) * a.x_row + p0 + c16 * 16) =
+                    *reinterpret_cast<const uint4 *>(&s_o[tt][c16 * 16]);
+        }
+    }
+    if (a.h_out) {
+        const int64_t sidx = ((int64_t)b * a.D + p) * N + g * S;
+        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = (hh[s] << 15) + hl[s];
+    }
+}
+
 }  // namespace
+
+// Used by mi_ssd_block_scan: N in {16, 32, 64}, d_head % 16 == 0, 16-byte
+// aligned rows.  Lanes per channel: the split that keeps S = 4 states per
+// lane where it can (16 at N = 64, 8 at N = 32, 4 at N = 16), narrowed so a
+// block's channels stay in one head.
+hipError_t launch_ssd_scan(const int8_t *xs, const int8_t *xp, const int8_t *z, const int32_t *tab, int8_t *yo,
+                           const int32_t *h_in, int32_t *h_out, int64_t x_row, int64_t xp_row, int64_t z_row, int B,
+                           int L, int H, int P, int N, int s_y, hipStream_t st) {
+    SScanArgs a{};
+    a.xs = xs; a.xp = xp; a.z = z; a.tab = tab; a.yo = yo; a.h_in = h_in; a.h_out = h_out;
+    a.x_row = x_row; a.xp_row = xp_row; a.z_row = z_row;
+    a.B = B; a.L = L; a.D = H * P; a.H = H; a.P = P; a.s_y = s_y;
+    int G = N / 4;
+    while (P % (kMThreads / G) != 0) G *= 2;  // P % 16 == 0, so G = 16 always fits
+    const dim3 grid((unsigned)(a.D / (kMThreads / G)), (unsigned)B);
+#define MI_SCASE(NN, GG)                                                                    \
+    if (N == NN && G == GG) {                                                               \
+        hipLaunchKernelGGL((ssd_scan_kernel<NN, GG>), grid, dim3(kMThreads), 0, st, a);     \
+        return hipGetLastError();                                                           \
+    }
+    MI_SCASE(16, 4)
+    MI_SCASE(16, 8)
+    MI_SCASE(16, 16)
+    MI_SCASE(32, 8)
+    MI_SCASE(32, 16)
+    MI_SCASE(64, 16)
+#undef MI_SCASE
+    return hipErrorInvalidValue;
+}
 
 // Used by mi_block_scan for N in {16, 32, 64}, D % 16 == 0 and 16-byte aligned rows.
 hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z, const int8_t *bsrc,

@@ -458,6 +458,9 @@ hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z
                              const int8_t *csrc, const int32_t *base, int8_t *yo, const int32_t *h_in, int32_t *h_out,
                              int64_t x_row, int64_t z_row, int64_t bc_row, int B, int L, int D, int N, int s_y,
                              hipStream_t st);
+hipError_t launch_ssd_scan(const int8_t *xs, const int8_t *xp, const int8_t *z, const int32_t *tab, int8_t *yo,
+                           const int32_t *h_in, int32_t *h_out, int64_t x_row, int64_t xp_row, int64_t z_row, int B,
+                           int L, int H, int P, int N, int s_y, hipStream_t st);
 }  // namespace mi
 
 using namespace mi;
@@ -542,6 +545,35 @@ extern "C" mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int
     else
         e = launch_scan<kModeModel>(a, nstate, fast, as_stream(stream));
     if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_block_scan: launch failed: %s", hipGetErrorString(e));
+    return MI_OK;
+}
+
+extern "C" mi_status mi_ssd_block_scan(const int8_t *xs, const int8_t *xp, int xp_stride, const int8_t *z,
+                                       int z_stride, int z_off, const int32_t *decay_tab, int n_heads, int s_y,
+                                       int8_t *yo, const int32_t *h_in, int32_t *h_out, int batch, int len,
+                                       int d_inner, int nstate, void *stream) {
+    const char *fn = "mi_ssd_block_scan";
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && d_inner >= 0 && n_heads >= 1, MI_ERR_BAD_DIM, "%s: bad size", fn);
+    MI_REQUIRE(nstate == 16 || nstate == 32 || nstate == 64, MI_ERR_BAD_DIM, "%s: nstate=%d (16, 32 or 64)", fn,
+               nstate);
+    MI_REQUIRE(d_inner % n_heads == 0 && (d_inner / n_heads) % 16 == 0, MI_ERR_BAD_DIM,
+               "%s: d_inner=%d must split into %d heads of a multiple of 16 channels", fn, d_inner, n_heads);
+    MI_REQUIRE(s_y >= 0 && s_y <= 30, MI_ERR_BAD_ARG, "%s: s_y=%d outside [0,30]", fn, s_y);
+    MI_REQUIRE(xp_stride >= 2 * n_heads * nstate + n_heads && xp_stride % 16 == 0, MI_ERR_BAD_DIM,
+               "%s: xp_stride=%d must hold B, C and dt of every head and be a multiple of 16", fn, xp_stride);
+    MI_REQUIRE(z_off >= 0 && z_off + d_inner <= z_stride && z_stride % 16 == 0 && z_off % 16 == 0, MI_ERR_BAD_DIM,
+               "%s: z columns [%d,%d) and stride %d (multiples of 16)", fn, z_off, z_off + d_inner, z_stride);
+    if ((int64_t)batch * d_inner == 0 || (len == 0 && !h_out)) return MI_OK;
+    MI_REQUIRE(decay_tab && (len == 0 || (xs && xp && z && yo)), MI_ERR_NULL_POINTER, "%s: a required pointer is NULL",
+               fn);
+    MI_REQUIRE(len == 0 || (aligned(xs, 16) && aligned(xp, 16) && aligned(z, 16) && aligned(yo, 16)),
+               MI_ERR_BAD_ALIGNMENT, "%s: xs, xp, z and yo must be 16-byte aligned", fn);
+    MI_REQUIRE(aligned(h_in, 4) && aligned(h_out, 4) && aligned(decay_tab, 4), MI_ERR_BAD_ALIGNMENT,
+               "%s: h_in, h_out and decay_tab must be 4-byte aligned", fn);
+    const hipError_t e = launch_ssd_scan(xs, xp, z + z_off, decay_tab, yo, h_in, h_out, d_inner, xp_stride, z_stride,
+                                         batch, len, n_heads, d_inner / n_heads, nstate, s_y, as_stream(stream));
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return MI_OK;
 }
 

@@ -3,6 +3,7 @@
 Host side in Python on PyTorch-ROCm; compute in libmamba_int.so (gfx950 HIP
 kernels behind the C ABI of include/mamba_int.h).
 """
-from .params import ModelDims, ModelParams, LayerParams, init_random_params, pack_ternary, unpack_ternary  # noqa: F401
+from .params import (ModelDims, ModelParams, LayerParams, SSDLayerParams, init_random_params,  # noqa: F401
+                     pack_ternary, ssd_decay_table, unpack_ternary)
 
 SPEC_VERSION = "mi-spec-1"

@@ -24,6 +24,8 @@ from .params import LayerParams, ModelParams
 
 @dataclass
 class DeviceLayer:
+    """Device parameters of one layer: the dyadic-scan block uses w_dt, s_dt
+    and base, the SSD block its per-head decay table."""
     gamma: torch.Tensor
     w_in: torch.Tensor
     s_in: int
@@ -31,14 +33,15 @@ class DeviceLayer:
     conv_b: torch.Tensor
     w_x: torch.Tensor
     s_x: int
-    w_dt: torch.Tensor
-    s_dt: int
-    base: torch.Tensor
-    k: int
     s_y: int
     w_out: torch.Tensor
     res_mult: int
     res_shift: int
+    k: int = 15
+    w_dt: Optional[torch.Tensor] = None
+    s_dt: int = 0
+    base: Optional[torch.Tensor] = None
+    decay_tab: Optional[torch.Tensor] = None
 
 
 @dataclass
@@ -123,12 +126,15 @@ class IntegerMambaRunner:
         self.emb = _dev(params.emb, dv)
         self.layers: List[DeviceLayer] = []
         for lp in params.layers:
-            self.layers.append(DeviceLayer(
-                gamma=_dev(lp.gamma, dv), w_in=_dev(lp.w_in, dv), s_in=lp.s_in,
-                conv_w=_dev(lp.conv_w, dv), conv_b=_dev(lp.conv_b, dv),
-                w_x=_dev(lp.w_x, dv), s_x=lp.s_x, w_dt=_dev(lp.w_dt, dv), s_dt=lp.s_dt,
-                base=_dev(lp.base, dv), k=lp.k, s_y=lp.s_y, w_out=_dev(lp.w_out, dv),
-                res_mult=lp.res_mult, res_shift=lp.res_shift))
+            common = dict(gamma=_dev(lp.gamma, dv), w_in=_dev(lp.w_in, dv), s_in=lp.s_in,
+                          conv_w=_dev(lp.conv_w, dv), conv_b=_dev(lp.conv_b, dv), w_x=_dev(lp.w_x, dv),
+                          s_x=lp.s_x, k=lp.k, s_y=lp.s_y, w_out=_dev(lp.w_out, dv), res_mult=lp.res_mult,
+                          res_shift=lp.res_shift)
+            if self.dims.ssd:
+                self.layers.append(DeviceLayer(**common, decay_tab=_dev(lp.decay_tab, dv)))
+            else:
+                self.layers.append(DeviceLayer(**common, w_dt=_dev(lp.w_dt, dv), s_dt=lp.s_dt,
+                                               base=_dev(lp.base, dv)))
         self.gamma_f = _dev(params.gamma_f, dv)
         self.w_head = _dev(params.w_head, dv)
         self._ws: Dict[int, _Workspace] = {}
@@ -163,6 +169,9 @@ class IntegerMambaRunner:
         dims = self.dims
         D, N, R, d = dims.d_inner, dims.d_state, dims.dt_rank, dims.d_model
         T = B * L
+        if dims.ssd:
+            self._layer_ssd(ly, ws, B, L, conv_state, h_state, fresh, stats_in, stats_out)
+            return
         ops.bitshift_norm(ws.r, ly.gamma, out=ws.a, row_stats=stats_in)
         ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
         ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
@@ -185,9 +194,30 @@ class IntegerMambaRunner:
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
                       res_shift=ly.res_shift, row_stats=stats_out)
 
+    def _layer_ssd(self, ly: DeviceLayer, ws: _Workspace, B: int, L: int, conv_state: torch.Tensor,
+                   h_state: torch.Tensor, fresh: bool, stats_in: Optional[torch.Tensor],
+                   stats_out: Optional[torch.Tensor]) -> None:
+        """A MambaIntegerBlockV2 layer (``ssd_multihead.py:523-592``; spec section 7)
+        over [B, L] tokens, prefill or one recurrent step (L = 1)."""
+        dims = self.dims
+        D, d = dims.d_inner, dims.d_model
+        ops.bitshift_norm(ws.r, ly.gamma, out=ws.a, row_stats=stats_in, v2=True)
+        ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
+        ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
+                            state_out=conv_state, out=ws.xs, batch=B)
+        ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+        if self.scan_timer is not None:
+            self.scan_timer[0]()
+        ops.ssd_block_scan(ws.xs, ws.xp, ws.xz, D, ly.decay_tab, dims.n_heads, dims.d_state, ly.s_y,
+                           h_in=None if fresh else h_state, h_out=h_state, out=ws.yo, batch=B)
+        if self.scan_timer is not None:
+            self.scan_timer[1]()
+        ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                      res_shift=ly.res_shift, row_stats=stats_out)
+
     def _fused_decode_ok(self, B: int) -> bool:
-        return (B <= 16 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0 and self.dims.d_state <= 64
-                and self.dims.dt_rank <= 256)
+        return (not self.dims.ssd and B <= 16 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0
+                and self.dims.d_state <= 64 and self.dims.dt_rank <= 256)
 
     def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
                       h_state: torch.Tensor, li: int) -> None:

@@ -143,11 +143,12 @@ def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Opt
 
 
 # ---------------------------------------------------------------- block ops
-def bitshift_norm(r: torch.Tensor, gamma: torch.Tensor, out=None, row_stats=None) -> torch.Tensor:
+def bitshift_norm(r: torch.Tensor, gamma: torch.Tensor, out=None, row_stats=None, v2: bool = False) -> torch.Tensor:
+    """Integer BitShiftNorm of r int32 [T, d]; v2 selects BitShiftNormV2's table."""
     _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma")
     T, d = r.shape
     o = out if out is not None else torch.empty((T, d), dtype=torch.int8, device=r.device)
-    _lib.call("mi_bitshift_norm", _ptr(r), _ptr(gamma), _ptr(o), T, d,
+    _lib.call("mi_bitshift_norm_v2" if v2 else "mi_bitshift_norm", _ptr(r), _ptr(gamma), _ptr(o), T, d,
               _ptr(_opt(row_stats, torch.int64, "row_stats")), _stream())
     return o
 
@@ -192,6 +193,23 @@ def block_scan(xs, dm, xp, b_off: int, z, z_off: int, base, decay_shift: int, s_
     _lib.call("mi_block_scan", _ptr(xs), _ptr(dm), _ptr(xp), xp.shape[-1], b_off, _ptr(z), z.shape[-1], z_off,
               _ptr(base), decay_shift, s_y, _ptr(yo), _ptr(_opt(h_in, torch.int32, "h_in")),
               _ptr(_opt(h_out, torch.int32, "h_out")), B, L, D, N, _stream())
+    return yo
+
+
+def ssd_block_scan(xs, xp, z, z_off: int, decay_tab, n_heads: int, d_state: int, s_y: int, h_in=None, h_out=None,
+                   out=None, batch: Optional[int] = None) -> torch.Tensor:
+    """Scan of the multi-head SSD block: xs int8 [B,L,D] (or [B*L,D] with ``batch``), xp int8
+    planar [.., W], z int8 [.., Z] at column z_off, decay_tab int32 [H, 255] -> yo int8."""
+    for t, nm in ((xs, "xs"), (xp, "xp"), (z, "z")):
+        _req(t, torch.int8, nm)
+    _req(decay_tab, torch.int32, "decay_tab")
+    D = xs.shape[-1]
+    B = xs.shape[0] if batch is None else batch
+    L = xs.numel() // (D * B)
+    yo = out if out is not None else torch.empty(xs.shape, dtype=torch.int8, device=xs.device)
+    _lib.call("mi_ssd_block_scan", _ptr(xs), _ptr(xp), xp.shape[-1], _ptr(z), z.shape[-1], z_off, _ptr(decay_tab),
+              n_heads, s_y, _ptr(yo), _ptr(_opt(h_in, torch.int32, "h_in")), _ptr(_opt(h_out, torch.int32, "h_out")),
+              B, L, D, d_state, _stream())
     return yo
 
 

@@ -59,7 +59,7 @@ class BitShiftNorm(nn.Module):
 
 
 def _layer_params(dims: ModelDims, rng: np.random.Generator) -> LayerParams:
-    one = ModelDims(dims.d_model, 1, 16, dims.d_state, dims.dt_rank)
+    one = ModelDims(dims.d_model, 1, 16, dims.d_state, dims.dt_rank, dims.block, dims.n_heads, dims.d_head)
     p = init_random_params(one, int(rng.integers(0, 2**31 - 1)))
     return p.layers[0]
 
@@ -83,7 +83,7 @@ class MambaIntegerBlock(nn.Module):
     def _get_runner(self, device) -> IntegerMambaRunner:
         if self._runner is None or self._runner.device != torch.device(device):
             d = self.dims
-            mp = ModelParams(dims=ModelDims(d.d_model, 1, 16, d.d_state, d.dt_rank),
+            mp = ModelParams(dims=ModelDims(d.d_model, 1, 16, d.d_state, d.dt_rank, d.block, d.n_heads, d.d_head),
                              emb=np.zeros((16, d.d_model), np.int8), layers=[self.params],
                              gamma_f=np.full(d.d_model, 256, np.int16),
                              w_head=np.zeros((16, d.d_model // 4), np.uint8))
@@ -103,8 +103,28 @@ class MambaIntegerBlock(nn.Module):
         return ws.r.clone().view(B, L, d)
 
 
+class BitShiftNormV2(BitShiftNorm):
+    """Integer BitShiftNormV2 (``ssd_multihead.py:595-632``; spec rule 7.1)."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        out = ops.bitshift_norm(x.reshape(-1, shape[-1]).contiguous(), self.gamma_q.to(x.device), v2=True)
+        return out.view(shape)
+
+
+class MambaIntegerBlockV2(MambaIntegerBlock):
+    """One integer multi-head SSD block (``ssd_multihead.py:471-592``, selected by
+    ``ssm_cfg.use_ssd``): int32 Q8 residual in and out, spec section 7."""
+
+    def __init__(self, config: dict, layer_idx: int, params=None, seed: int = 0):
+        cfg = dict(config, ssm_cfg=dict(config.get("ssm_cfg", {}), use_ssd=True))
+        super().__init__(cfg, layer_idx, params=params, seed=seed)
+
+
 class MambaIntegerModel(nn.Module):
-    """Integer Mamba language model (``mamba_integer_model.py:466-495``)."""
+    """Integer Mamba language model (``mamba_integer_model.py:466-495``); the
+    layers are multi-head SSD blocks when ``ssm_cfg.use_ssd`` is set
+    (``:473-476``)."""
 
     def __init__(self, config: dict, params: Optional[ModelParams] = None, seed: int = 0):
         super().__init__()
@@ -152,5 +172,6 @@ class MambaIntegerModel(nn.Module):
         return torch.cat([input_ids, new], dim=1)
 
 
-__all__ = ["MambaIntegerModel", "MambaIntegerBlock", "BitShiftNorm", "DyadicScanFunction",
+__all__ = ["MambaIntegerModel", "MambaIntegerBlock", "MambaIntegerBlockV2", "BitShiftNorm", "BitShiftNormV2",
+           "DyadicScanFunction",
            "DECAY_SHIFT", "requant_shift"]

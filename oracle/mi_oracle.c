@@ -333,7 +333,7 @@ void mo_act_quant_f32(const float *x, int8_t *xq, float *x_scale, int M, int K) 
 /* -------------------------------------------------- 4. integer block ops */
 /* BitShiftNorm (mamba_integer_model.py:144-184 table, :200-223, :449-464):
  * spec rule 4.1.  r int32 [T,d] (Q8), gamma int16 [d] (Q8), out int8 [T,d]. */
-void mo_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int T, int d) {
+static void norm_rows(const int32_t *r, const int16_t *gamma, int8_t *out, int T, int d, int kmax, int kmin) {
 #pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int t = 0; t < T; ++t) {
         const int32_t *row = r + (int64_t)t * d;
@@ -350,15 +350,25 @@ void mo_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int T
             S += xv * xv;
         }
         int kk = 0;
-        for (int j = 1; j <= 8; ++j)
+        for (int j = 1; j <= kmax; ++j)
             if (S >= (int64_t)d << (2 * (j + 8))) kk += 1;
-        for (int j = 1; j <= 3; ++j)
+        for (int j = 1; j <= kmin; ++j)
             if (S < (int64_t)d << (2 * (8 - j))) kk -= 1;
         for (int i = 0; i < d; ++i) {
             int64_t xv = row[i] - mu;
             out[(int64_t)t * d + i] = sat8(rshr(xv * gamma[i], 12 + kk));
         }
     }
+}
+
+void mo_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int T, int d) {
+    norm_rows(r, gamma, out, T, d, 8, 3);
+}
+
+/* BitShiftNormV2 (ssd_multihead.py:595-632): spec rule 7.1, the V2 table
+ * (var >= 4^j -> 2^-j for j <= 6; var < 4^-j -> 2^j for j <= 2). */
+void mo_bitshift_norm_v2(const int32_t *r, const int16_t *gamma, int8_t *out, int T, int d) {
+    norm_rows(r, gamma, out, T, d, 6, 2);
 }
 
 /* Exact squareplus of spec rule 4.4 on the conv output c (Q10) -> int8 Q4. */
@@ -444,6 +454,64 @@ void mo_block_scan(const int8_t *xs, const int8_t *dm, const int8_t *xp, int xp_
             }
             if (hstate)
                 for (int n = 0; n < N; ++n) hstate[((int64_t)b * D + d) * N + n] = h[n];
+        }
+    }
+}
+
+/* ------------------------------------------ 7. multi-head SSD block (V2) */
+/* B / (||B|| + 1e-6) of ssd_multihead.py:552-553 in Q7 (spec rule 7.4):
+ * S = sum v^2; nrm = isqrt(S * 2^16); inv = floor(2^30 / nrm);
+ * out = sat8(rshr(v * inv, 15)); S = 0 gives zeros. */
+void mo_unit_q7(const int8_t *v, int8_t *out, int n) {
+    int64_t S = 0;
+    for (int i = 0; i < n; ++i) S += (int64_t)v[i] * v[i];
+    if (S == 0) {
+        for (int i = 0; i < n; ++i) out[i] = 0;
+        return;
+    }
+    int64_t nrm = (int64_t)mo_isqrt((uint64_t)S << 16);
+    int64_t inv = ((int64_t)1 << 30) / nrm;
+    for (int i = 0; i < n; ++i) out[i] = sat8(rshr((int64_t)v[i] * inv, 15));
+}
+
+/* Multi-head SSD scan of MambaIntegerBlockV2 (spec rules 7.3-7.8): the
+ * recurrence h_t = exp(A_t) h_{t-1} + B_t (x) X_t, Y_t = C_t . h_t that
+ * ssd_multihead_forward (ssd_multihead.py:92-244) evaluates in chunked matmul
+ * form, restated sequentially per (b, head, p, n) with the floor rule of
+ * dyadic_mamba_kernel.cu:53-56.  xs int8 [B,L,D] (D = H*P); xp int8
+ * [B,L,xp_stride] planar: B of head h at [h*N, h*N+N), C at H*N + h*N, dt at
+ * 2*H*N + h; z int8 [B,L,z_stride] at column z_off; tab int32 [H][255];
+ * yo int8 [B,L,D]; hstate int32 [B,H,P,N] nullable in/out. */
+void mo_ssd_v2_scan(const int8_t *xs, const int8_t *xp, int xp_stride, const int8_t *z, int z_stride, int z_off,
+                    const int32_t *tab, int s_y, int8_t *yo, int32_t *hstate, int B, int L, int H, int P, int N) {
+    const int D = H * P;
+    const int64_t ylim = (int64_t)100 << 18;
+#pragma omp parallel for collapse(2) num_threads(g_threads) schedule(static)
+    for (int b = 0; b < B; ++b) {
+        for (int c = 0; c < D; ++c) {
+            const int hd = c / P;
+            int32_t h[1024];
+            int8_t bq[1024], cq[1024];
+            for (int n = 0; n < N; ++n) h[n] = hstate ? hstate[((int64_t)b * D + c) * N + n] : 0;
+            for (int t = 0; t < L; ++t) {
+                const int64_t bt = (int64_t)b * L + t;
+                const int8_t *row = xp + bt * xp_stride;
+                const int dt = (int)clamp64(row[2 * H * N + hd], -127, 127);
+                const int32_t nt = tab[hd * 255 + dt + 127];
+                mo_unit_q7(row + hd * N, bq, N);
+                mo_unit_q7(row + H * N + hd * N, cq, N);
+                const int64_t xv = xs[bt * D + c];
+                int64_t acc = 0;
+                for (int n = 0; n < N; ++n) {
+                    h[n] = scan_step(h[n], nt, 15, (int64_t)bq[n] * xv);
+                    acc += (int64_t)cq[n] * h[n];
+                }
+                const int64_t y = clamp64(sat32(acc), -ylim, ylim);
+                const int64_t yg = floor_shr(y * mo_gate_q15(z[bt * z_stride + z_off + c]), 15);
+                yo[bt * D + c] = sat8(rshr(yg, s_y));
+            }
+            if (hstate)
+                for (int n = 0; n < N; ++n) hstate[((int64_t)b * D + c) * N + n] = h[n];
         }
     }
 }

@@ -72,6 +72,9 @@ def lib() -> ctypes.CDLL:
         L.mo_gate_q15.restype = ctypes.c_int32
         L.mo_block_scan.argtypes = [P, P, P, I, I, P, I, I, P, I, I, P, P, I, I, I, I]
         L.mo_embed.argtypes = [P, P, P, I, I]
+        L.mo_bitshift_norm_v2.argtypes = [P, P, P, I, I]
+        L.mo_unit_q7.argtypes = [P, P, I]
+        L.mo_ssd_v2_scan.argtypes = [P, P, I, P, I, I, P, I, P, P, I, I, I, I, I]
         L.mo_set_threads(len(os.sched_getaffinity(0)))
         _lib = L
     return _lib
@@ -202,6 +205,39 @@ def bitshift_norm(r, gamma):
     return out
 
 
+def bitshift_norm_v2(r, gamma):
+    """BitShiftNormV2 (spec rule 7.1)."""
+    r, gamma = _c(r, np.int32), _c(gamma, np.int16)
+    T, d = r.shape
+    out = np.empty((T, d), np.int8)
+    lib().mo_bitshift_norm_v2(_p(r), _p(gamma), _p(out), T, d)
+    return out
+
+
+def unit_q7(v):
+    """Unit vector in Q7 of an int8 vector (spec rule 7.4)."""
+    v = _c(v, np.int8).reshape(-1)
+    out = np.empty_like(v)
+    lib().mo_unit_q7(_p(v), _p(out), v.size)
+    return out
+
+
+def ssd_v2_scan(xs, xp, z_src, z_off, tab, s_y, n_heads, d_state, h_state=None):
+    """SSD block scan (spec rules 7.3-7.8): xs [B,L,D], xp [B,L,W] planar,
+    z_src [B,L,Z]; tab int32 [H,255]; returns yo [B,L,D] and the state [B,D,N]."""
+    xs, xp, z_src, tab = _c(xs, np.int8), _c(xp, np.int8), _c(z_src, np.int8), _c(tab, np.int32)
+    B, L, D = xs.shape
+    H = n_heads
+    P = D // H
+    W = xp.shape[-1]
+    N = d_state
+    hs = np.zeros((B, D, N), np.int32) if h_state is None else _c(h_state, np.int32).copy()
+    yo = np.empty((B, L, D), np.int8)
+    lib().mo_ssd_v2_scan(_p(xs), _p(xp), W, _p(z_src), z_src.shape[-1], z_off, _p(tab), s_y, _p(yo), _p(hs),
+                         B, L, H, P, N)
+    return yo, hs
+
+
 def squareplus_q(c: int) -> int:
     return int(lib().mo_squareplus_q(int(c)))
 
@@ -255,7 +291,8 @@ class LayerState:
 
 
 class OracleModel:
-    """Integer Mamba stack on the CPU oracle (spec rules 4.1-4.12)."""
+    """Integer Mamba stack on the CPU oracle (spec rules 4.1-4.12; the SSD
+    block of section 7 when dims.block is "ssd")."""
 
     def __init__(self, params: ModelParams):
         self.p = params
@@ -265,6 +302,8 @@ class OracleModel:
         dm_ = self.dims
         D, N, R = dm_.d_inner, dm_.d_state, dm_.dt_rank
         T = B * L
+        if dm_.ssd:
+            return self._layer_ssd(lp, r, B, L, state)
         a = bitshift_norm(r, lp.gamma)
         xz = bitlinear(a, lp.w_in, OUT_INT8, lp.s_in)                       # [T, 2D]
         xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b,
@@ -274,6 +313,20 @@ class OracleModel:
         yo, h = block_scan(xs, dmod.reshape(B, L, D), xp.reshape(B, L, -1), R,
                            xz.reshape(B, L, 2 * D), D, lp.base, lp.k, lp.s_y,
                            None if state is None else state.h)
+        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=r,
+                      res_mult=lp.res_mult, res_shift=lp.res_shift)
+        return r, LayerState(conv=conv_state, h=h)
+
+    def _layer_ssd(self, lp, r, B, L, state: Optional[LayerState]):
+        """MambaIntegerBlockV2 (spec section 7)."""
+        D, T = self.dims.d_inner, B * L
+        a = bitshift_norm_v2(r, lp.gamma)
+        xz = bitlinear(a, lp.w_in, OUT_INT8, lp.s_in)
+        xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b,
+                                         None if state is None else state.conv)
+        xp = bitlinear(xs.reshape(T, D), lp.w_x, OUT_INT8, lp.s_x)
+        yo, h = ssd_v2_scan(xs, xp.reshape(B, L, -1), xz.reshape(B, L, 2 * D), D, lp.decay_tab, lp.s_y,
+                            self.dims.n_heads, self.dims.d_state, None if state is None else state.h)
         r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=r,
                       res_mult=lp.res_mult, res_shift=lp.res_shift)
         return r, LayerState(conv=conv_state, h=h)
