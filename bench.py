@@ -253,6 +253,46 @@ def kernel_table():
         "note": "device-generated random weights; decode steps include the host-side graph launch"}
     del run5, st5, lg5
     torch.cuda.empty_cache()
+    # the shipped configuration (configs/config_mamba_integer_l4.json): multi-head
+    # SSD blocks (24 heads of 64, d_state 64), d768 x 24, vocab 4096; batch 8 x
+    # 2048 prefill, greedy decode steps, and the block scan alone
+    from mamba_int import init_random_params
+    dimsv = ModelDims(d_model=768, n_layer=24, vocab_size=4096, d_state=64, dt_rank=0, block="ssd", n_heads=24,
+                      d_head=64)
+    runv = IntegerMambaRunner(init_random_params(dimsv, 7), device=dev)
+    idsv = torch.randint(0, 4096, (8, 2048), device=dev)
+    lgv, stv = runv.prefill(idsv)
+    torch.cuda.synchronize()
+    e0.record()
+    lgv, stv = runv.prefill(idsv)
+    e1.record()
+    runv.decode_loop(lgv, stv, 4)
+    torch.cuda.synchronize()
+    e1b.record()
+    runv.decode_loop(lgv, stv, nd + 1)
+    e2.record()
+    torch.cuda.synchronize()
+    ms_pf, ms_dec = e0.elapsed_time(e1), e1b.elapsed_time(e2) / nd
+    Bv, Lv, Dv, Wv = 8, 2048, dimsv.d_inner, dimsv.xp_width
+    xsv, xpv, xzv = t8(Bv, Lv, Dv), t8(Bv, Lv, Wv), t8(Bv, Lv, 2 * Dv)
+    tabv = runv.layers[0].decay_tab
+    hv = torch.zeros((Bv, Dv, 64), dtype=torch.int32, device=dev)
+    yv = torch.empty((Bv, Lv, Dv), dtype=torch.int8, device=dev)
+    ms_scan = _time_kernel(lambda: ops.ssd_block_scan(xsv, xpv, xzv, Dv, tabv, 24, 64, 14, h_out=hv, out=yv),
+                           iters=5, warmup=1)
+    # each input read once, each output written once: xs, z half, yo; B, C, dt
+    # columns of xp; the decay table; the final state
+    scan_bytes = 3 * Bv * Lv * Dv + Bv * Lv * (2 * 24 * 64 + 24) + 24 * 255 * 4 + Bv * Dv * 64 * 4
+    upd = Bv * Lv * Dv * 64
+    out["shipped_ssd_d768x24_b8"] = {
+        "prefill_ms_8x2048": ms_pf, "prefill_tok_s": 8 * 2048 / (ms_pf * 1e-3),
+        "decode_ms_per_step": ms_dec, "decode_tok_s": 8 / (ms_dec * 1e-3),
+        "ssd_scan_ms": ms_scan, "ssd_scan_bytes": scan_bytes, "ssd_scan_GB_s": scan_bytes / ms_scan / 1e6,
+        "ssd_scan_hbm_frac": scan_bytes / ms_scan / 1e6 / HBM_PEAK_GBS, "ssd_scan_G_updates_s": upd / ms_scan / 1e6,
+        "note": "random integer weights (spec section 7 initialisation); decode: one graph per step, six kernels "
+                "per layer"}
+    del runv, stv, lgv
+    torch.cuda.empty_cache()
     # config 4: B4 L8192 H24 P64 N128, chunk 256
     B, L, H, P, NS = 4, 8192, 24, 64, 128
     x4, b4, c4 = t8(B, L, H, P), t8(B, L, H, NS), t8(B, L, H, NS)

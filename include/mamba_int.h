@@ -322,7 +322,9 @@ mi_status mi_embed_argmax(const int64_t *keys, int nkeys, int64_t *ids, const in
 
 /* ------------------------------------------------ whole decode step */
 /* Integer parameters of one layer (device pointers; spec mi-spec-1 layouts:
- * packed ternary matrices [rows][cols/4] bytes, 16-byte aligned). */
+ * packed ternary matrices [rows][cols/4] bytes, 16-byte aligned).  The
+ * dyadic-scan block uses w_dt, s_dt and base; the multi-head SSD block
+ * (MI_BLOCK_SSD) w_x with the planar rows of spec rule 7.3 and decay_tab. */
 typedef struct mi_layer_params {
     const int16_t *gamma;    /* BitShiftNorm gain [d_model] */
     const uint8_t *w_in;     /* in_proj [2*d_inner][d_model/4] */
@@ -339,27 +341,34 @@ typedef struct mi_layer_params {
     const uint8_t *w_out;    /* out_proj [d_model][d_inner/4] */
     int32_t res_mult;
     int res_shift;
+    const int32_t *decay_tab; /* SSD block: [n_heads][255] decay numerators */
 } mi_layer_params;
 
-/* The model: dims (d_inner = 2*d_model), int8 embedding [vocab][d_model],
- * `layers` a HOST array of n_layer entries, final gain and packed lm_head
- * [vocab][d_model/4]. */
+enum { MI_BLOCK_DYADIC = 0, MI_BLOCK_SSD = 1 };
+
+/* The model: dims, int8 embedding [vocab][d_model], `layers` a HOST array of
+ * n_layer entries, final gain and packed lm_head [vocab][d_model/4].  block
+ * MI_BLOCK_DYADIC: d_inner = 2*d_model (MambaIntegerBlock); MI_BLOCK_SSD:
+ * d_inner = n_heads*d_head (MambaIntegerBlockV2, dt_rank unused). */
 typedef struct mi_model_params {
     int d_model, n_layer, vocab_size, d_state, dt_rank;
     const int8_t *emb;
     const mi_layer_params *layers;
     const int16_t *gamma_f;
     const uint8_t *w_head;
+    int block, n_heads, d_head;
 } mi_model_params;
 
 /* Bytes of the caller-owned device workspace mi_decode_step needs at batch m
- * (1 <= m <= 16; d_model % 64 == 0, <= 3072; dt_rank % 16 == 0 and
- * dt_rank + 2*d_state <= 256). */
+ * (1 <= m <= 16; d_model % 64 == 0, <= 3072; dyadic block: dt_rank % 16 ==
+ * 0 and dt_rank + 2*d_state <= 256; SSD block: d_head % 16 == 0, d_state in
+ * {16, 32, 64}). */
 mi_status mi_decode_workspace_size(const mi_model_params *params, int m, size_t *bytes);
 
 /* One greedy decode step of the whole model for m sequences (the reference's
  * generation step, scripts/inference.py:147-161 over MambaIntegerModel.forward,
- * mamba_integer_model.py:486-495, with recurrent state): ids int64 [m] in,
+ * mamba_integer_model.py:486-495, with recurrent state; the dyadic block runs
+ * the three fused stages per layer, the SSD block six kernels): ids int64 [m] in,
  * next_ids int64 [m] out (first maximal logit), logits int32 [m][ld_logits]
  * when non-NULL; conv_state / h_state are HOST arrays of n_layer device
  * pointers (int8 [m][3][d_inner], int32 [m][d_inner][d_state]) updated in
@@ -372,7 +381,8 @@ mi_status mi_decode_step(const mi_model_params *params, int m, const int64_t *id
 /* ------------------------------------------------ integer checkpoints */
 /* The integer parameters above in a versioned file (format 1, spec
  * mi-spec-1): a 128-byte header (magic "MIQCKPT", format, spec string, dims,
- * logit_scale, table CRC), a table of named little-endian tensors (dtype,
+ * logit_scale, table CRC, block type and heads), a table of named
+ * little-endian tensors (dtype,
  * shape, offset, bytes, CRC-32), and the tensors at 256-byte aligned offsets:
  * 2-bit packed ternary matrices, int8 embedding and conv taps, int32 conv
  * bias and decay numerators, int16 gains, and the per-layer shifts.
@@ -391,6 +401,7 @@ typedef struct mi_checkpoint_info {
     int d_model, n_layer, vocab_size, d_state, dt_rank;
     float logit_scale;         /* float logits = int32 logits * logit_scale (> 0) */
     size_t device_bytes;       /* bytes mi_checkpoint_upload fills */
+    int block, n_heads, d_head; /* MI_BLOCK_DYADIC or MI_BLOCK_SSD (then n_heads, d_head) */
 } mi_checkpoint_info;
 
 /* Reads a checkpoint into host memory and validates it: magic, format,

@@ -15,7 +15,8 @@
 //   header, 128 bytes: magic "MIQCKPT\0", u32 format (1), u32 header bytes
 //     (128), char spec[16] ("mi-spec-1"), u32 d_model, n_layer, vocab_size,
 //     d_state, dt_rank, u32 tensor count, u64 table offset, u64 file bytes,
-//     f32 logit_scale, u32 CRC-32 of the table, zeros;
+//     f32 logit_scale, u32 CRC-32 of the table, u32 block (0 dyadic scan,
+//     1 multi-head SSD), u32 n_heads, u32 d_head, zeros;
 //   table: one 96-byte entry per tensor: char name[48] (NUL-padded), u32
 //     dtype (1 i8, 2 u8, 3 i16, 4 i32, 5 f32), u32 ndim, u32 shape[4], u64
 //     offset, u64 bytes, u32 CRC-32 of the bytes, u32 zero;
@@ -89,10 +90,16 @@ struct Want {
     std::vector<uint64_t> shape;
 };
 
+uint64_t ssd_xp_width(const mi_checkpoint_info &in) {
+    return ((uint64_t)2 * in.n_heads * in.d_state + in.n_heads + 15) / 16 * 16;
+}
+
 // The tensors a format-1 file holds for the given dims, in canonical order
 // (the device layout of mi_checkpoint_upload follows this order).
 std::vector<Want> expected(const mi_checkpoint_info &in) {
-    const uint64_t d = in.d_model, D = 2 * d, N = in.d_state, R = in.dt_rank, V = in.vocab_size;
+    const bool ssd = in.block == MI_BLOCK_SSD;
+    const uint64_t d = in.d_model, D = ssd ? (uint64_t)in.n_heads * in.d_head : 2 * d, N = in.d_state,
+                   R = in.dt_rank, V = in.vocab_size;
     std::vector<Want> w;
     w.push_back({"emb", kI8, {V, d}});
     w.push_back({"gamma_f", kI16, {d}});
@@ -104,9 +111,14 @@ std::vector<Want> expected(const mi_checkpoint_info &in) {
         w.push_back({p + "w_in", kU8, {2 * D, d / 4}});
         w.push_back({p + "conv_w", kI8, {D, 4}});
         w.push_back({p + "conv_b", kI32, {D}});
-        w.push_back({p + "w_x", kU8, {R + 2 * N, D / 4}});
-        w.push_back({p + "w_dt", kU8, {D, R / 4}});
-        w.push_back({p + "base", kI32, {D, N}});
+        if (ssd) {
+            w.push_back({p + "w_x", kU8, {ssd_xp_width(in), D / 4}});
+            w.push_back({p + "decay_tab", kI32, {(uint64_t)in.n_heads, 255}});
+        } else {
+            w.push_back({p + "w_x", kU8, {R + 2 * N, D / 4}});
+            w.push_back({p + "w_dt", kU8, {D, R / 4}});
+            w.push_back({p + "base", kI32, {D, N}});
+        }
         w.push_back({p + "w_out", kU8, {d, D / 4}});
     }
     return w;
@@ -143,13 +155,21 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
     const uint64_t toff = rd<uint64_t>(&b[56]), fbytes = rd<uint64_t>(&b[64]);
     in.logit_scale = rd<float>(&b[72]);
     const uint32_t tcrc = rd<uint32_t>(&b[76]);
+    const uint32_t blk = rd<uint32_t>(&b[80]), nh = rd<uint32_t>(&b[84]), dh = rd<uint32_t>(&b[88]);
     MI_REQUIRE(fbytes == b.size(), MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: header says %llu bytes, file has %zu",
                path, (unsigned long long)fbytes, b.size());
+    MI_REQUIRE(blk == MI_BLOCK_DYADIC || blk == MI_BLOCK_SSD, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: block %u "
+               "unknown", path, blk);
+    const bool ssd = blk == MI_BLOCK_SSD;
     MI_REQUIRE(dm >= 16 && dm % 16 == 0 && dm <= 65536 && nl >= 1 && nl <= 4096 && vs >= 1 && vs <= (1u << 24) &&
-                   ds >= 1 && ds <= 64 && dr >= 16 && dr % 16 == 0 && dr <= 4096,
+                   ds >= 1 && ds <= 64 &&
+                   (ssd ? (nh >= 1 && nh <= 1024 && dh >= 16 && dh % 16 == 0 && dh <= 4096 &&
+                           (ds == 16 || ds == 32 || ds == 64))
+                        : (dr >= 16 && dr % 16 == 0 && dr <= 4096)),
                MI_ERR_BAD_DIM, "mi_checkpoint_open: %s: dims d_model=%u n_layer=%u vocab=%u d_state=%u dt_rank=%u "
-               "outside the format's limits", path, dm, nl, vs, ds, dr);
+               "n_heads=%u d_head=%u outside the format's limits", path, dm, nl, vs, ds, dr, nh, dh);
     in.d_model = (int)dm; in.n_layer = (int)nl; in.vocab_size = (int)vs; in.d_state = (int)ds; in.dt_rank = (int)dr;
+    in.block = (int)blk; in.n_heads = ssd ? (int)nh : 0; in.d_head = ssd ? (int)dh : 0;
     MI_REQUIRE(in.logit_scale > 0.0f, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: logit_scale must be positive", path);
     MI_REQUIRE(toff >= kHeaderBytes && toff + (uint64_t)nt * kEntryBytes <= b.size(), MI_ERR_BAD_ARG,
                "mi_checkpoint_open: %s: tensor table outside the file", path);
@@ -217,11 +237,14 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
                    MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: layer %u: a requant shift is outside its range", path, l);
         MI_REQUIRE(s[3] == 15, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: layer %u: decay shift %d (the scan kernels "
                    "take 15)", path, l, s[3]);
-        const mi_checkpoint::Tensor &bt = ck.tensors["layers." + std::to_string(l) + ".base"];
+        // decay numerators: clamp(base + dm) of the dyadic block needs base in
+        // [0, 32000]; the SSD block's table entries are used as they are
+        const int32_t hi = ssd ? 32768 : 32000;
+        const mi_checkpoint::Tensor &bt = ck.tensors["layers." + std::to_string(l) + (ssd ? ".decay_tab" : ".base")];
         const int32_t *base = reinterpret_cast<const int32_t *>(&b[bt.offset]);
         for (uint64_t i = 0; i < bt.nbytes / 4; ++i)
-            MI_REQUIRE(base[i] >= 0 && base[i] <= 32000, MI_ERR_BAD_ARG,
-                       "mi_checkpoint_open: %s: layer %u: decay numerator %d outside [0,32000]", path, l, base[i]);
+            MI_REQUIRE(base[i] >= 0 && base[i] <= hi, MI_ERR_BAD_ARG,
+                       "mi_checkpoint_open: %s: layer %u: decay numerator %d outside [0,%d]", path, l, base[i], hi);
     }
     return MI_OK;
 }
@@ -305,6 +328,10 @@ extern "C" mi_status mi_checkpoint_upload(const mi_checkpoint *ck, void *device,
     params->gamma_f = static_cast<const int16_t *>(where["gamma_f"]);
     params->w_head = static_cast<const uint8_t *>(where["w_head"]);
     params->layers = layers;
+    params->block = in.block;
+    params->n_heads = in.n_heads;
+    params->d_head = in.d_head;
+    const bool ssd = in.block == MI_BLOCK_SSD;
     for (int l = 0; l < in.n_layer; ++l) {
         const std::string p = "layers." + std::to_string(l) + ".";
         const int32_t *s = &ck->scalars[(size_t)l * kScalars];
@@ -316,9 +343,10 @@ extern "C" mi_status mi_checkpoint_upload(const mi_checkpoint *ck, void *device,
         ly.conv_b = static_cast<const int32_t *>(where[p + "conv_b"]);
         ly.w_x = static_cast<const uint8_t *>(where[p + "w_x"]);
         ly.s_x = s[1];
-        ly.w_dt = static_cast<const uint8_t *>(where[p + "w_dt"]);
+        ly.w_dt = ssd ? nullptr : static_cast<const uint8_t *>(where[p + "w_dt"]);
         ly.s_dt = s[2];
-        ly.base = static_cast<const int32_t *>(where[p + "base"]);
+        ly.base = ssd ? nullptr : static_cast<const int32_t *>(where[p + "base"]);
+        ly.decay_tab = ssd ? static_cast<const int32_t *>(where[p + "decay_tab"]) : nullptr;
         ly.decay_shift = s[3];
         ly.s_y = s[4];
         ly.w_out = static_cast<const uint8_t *>(where[p + "w_out"]);

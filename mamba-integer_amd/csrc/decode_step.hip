@@ -21,23 +21,34 @@ constexpr size_t kAlign = 256;
 size_t up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t r, stats, parts, xz, xs, yo, xpart, keys, total;
+    size_t r, stats, parts, a, xz, xs, xp, yo, xpart, keys, total;
 };
+
+bool ssd(const mi_model_params &p) { return p.block == MI_BLOCK_SSD; }
+size_t d_inner(const mi_model_params &p) { return ssd(p) ? (size_t)p.n_heads * p.d_head : 2 * (size_t)p.d_model; }
+// x_proj width of the SSD block: planar B, C, dt rounded up to 16 (spec rule 7.3)
+size_t ssd_xp_width(const mi_model_params &p) {
+    return ((size_t)2 * p.n_heads * p.d_state + p.n_heads + 15) / 16 * 16;
+}
 
 // Sub-buffer offsets of the decode workspace for batch m.
 WsLayout ws_layout(const mi_model_params &p, int m) {
-    const size_t d = p.d_model, D = 2 * d, N = p.d_state, R = p.dt_rank, V = p.vocab_size;
-    const size_t nx = R + 2 * N;
+    const size_t d = p.d_model, D = d_inner(p), N = p.d_state, R = p.dt_rank, V = p.vocab_size;
     WsLayout w{};
     size_t o = 0;
     w.r = o; o += up((size_t)m * d * 4);
     w.stats = o; o += up((size_t)m * 2 * 8);
-    w.parts = o; o += up((size_t)m * (d / 16) * 2 * 8);
+    w.keys = o; o += up((size_t)m * ((V + 63) / 64) * 8);
     w.xz = o; o += up((size_t)m * 2 * D);
     w.xs = o; o += up((size_t)m * D);
     w.yo = o; o += up((size_t)m * D);
-    w.xpart = o; o += up((size_t)m * (D / 16) * nx * 4);
-    w.keys = o; o += up((size_t)m * ((V + 63) / 64) * 8);
+    if (ssd(p)) {
+        w.a = o; o += up((size_t)m * d);
+        w.xp = o; o += up((size_t)m * ssd_xp_width(p));
+    } else {
+        w.parts = o; o += up((size_t)m * (d / 16) * 2 * 8);
+        w.xpart = o; o += up((size_t)m * (D / 16) * (R + 2 * N) * 4);
+    }
     w.total = o;
     return w;
 }
@@ -48,10 +59,19 @@ mi_status check_model(const char *fn, const mi_model_params *p, int m) {
     MI_REQUIRE(p->n_layer >= 1 && p->vocab_size >= 1, MI_ERR_BAD_DIM, "%s: n_layer and vocab_size must be >= 1", fn);
     MI_REQUIRE(p->d_model >= 64 && p->d_model % 64 == 0 && p->d_model <= 3072, MI_ERR_BAD_DIM,
                "%s: d_model=%d must be a multiple of 64 in [64,3072]", fn, p->d_model);
-    MI_REQUIRE(p->dt_rank >= 16 && p->dt_rank % 16 == 0 && p->d_state >= 1 && p->d_state <= 64 &&
-                   p->dt_rank + 2 * p->d_state <= 256,
-               MI_ERR_BAD_DIM, "%s: dt_rank=%d, d_state=%d outside the fused stages' limits", fn, p->dt_rank,
-               p->d_state);
+    MI_REQUIRE(p->block == MI_BLOCK_DYADIC || p->block == MI_BLOCK_SSD, MI_ERR_BAD_ARG, "%s: block=%d unknown", fn,
+               p->block);
+    if (ssd(*p)) {
+        MI_REQUIRE(p->n_heads >= 1 && p->d_head >= 16 && p->d_head % 16 == 0 &&
+                       (p->d_state == 16 || p->d_state == 32 || p->d_state == 64),
+                   MI_ERR_BAD_DIM, "%s: n_heads=%d, d_head=%d, d_state=%d outside the SSD block's limits", fn,
+                   p->n_heads, p->d_head, p->d_state);
+    } else {
+        MI_REQUIRE(p->dt_rank >= 16 && p->dt_rank % 16 == 0 && p->d_state >= 1 && p->d_state <= 64 &&
+                       p->dt_rank + 2 * p->d_state <= 256,
+                   MI_ERR_BAD_DIM, "%s: dt_rank=%d, d_state=%d outside the fused stages' limits", fn, p->dt_rank,
+                   p->d_state);
+    }
     MI_REQUIRE(p->emb && p->layers && p->gamma_f && p->w_head, MI_ERR_NULL_POINTER,
                "%s: emb, layers, gamma_f and w_head are required", fn);
     return MI_OK;
@@ -98,8 +118,11 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
     int8_t *yo = reinterpret_cast<int8_t *>(base + w.yo);
     int32_t *xpart = reinterpret_cast<int32_t *>(base + w.xpart);
     int64_t *keys = reinterpret_cast<int64_t *>(base + w.keys);
-    const int d = p.d_model, D = 2 * d, N = p.d_state, R = p.dt_rank, nx = R + 2 * N;
+    const int d = p.d_model, D = (int)d_inner(p), N = p.d_state, R = p.dt_rank, nx = R + 2 * N;
     const int P = d / 16;  // row-statistics partials of the out_proj (one per 16 features)
+    if (ssd(p))
+        for (int l = 0; l < p.n_layer; ++l)
+            MI_REQUIRE(p.layers[l].decay_tab, MI_ERR_NULL_POINTER, "mi_decode_step: decay_tab of layer %d is NULL", l);
 
     // every stage reports its own error; the first failure ends the step
 #define MI_STEP(call)                    \
@@ -108,6 +131,32 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
         if (s_ != MI_OK) return s_;      \
     } while (0)
     MI_STEP(mi_embed(ids, p.emb, r, m, d, p.vocab_size, stats, 1, stream));
+    if (ssd(p)) {
+        // MambaIntegerBlockV2 (spec section 7) with the per-op entries: norm
+        // (layer 0 from the embedding's statistics, later layers reduce their
+        // rows), in_proj, conv step, x_proj, one scan step, out_proj
+        int8_t *a = reinterpret_cast<int8_t *>(base + w.a);
+        int8_t *xp = reinterpret_cast<int8_t *>(base + w.xp);
+        const int W = (int)ssd_xp_width(p);
+        for (int l = 0; l < p.n_layer; ++l) {
+            const mi_layer_params &ly = p.layers[l];
+            MI_STEP(mi_bitshift_norm_v2(r, ly.gamma, a, m, d, l == 0 ? stats : nullptr, stream));
+            MI_STEP(mi_bitlinear_gemv(a, d, ly.w_in, xz, 2 * D, MI_OUT_INT8, m, 2 * D, d, ly.s_in, 0, 0, nullptr,
+                                      0.0f, nullptr, stream));
+            MI_STEP(mi_conv_squareplus(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], conv_state[l], xs, m, 1, D,
+                                       stream));
+            MI_STEP(mi_bitlinear_gemv(xs, D, ly.w_x, xp, W, MI_OUT_INT8, m, W, D, ly.s_x, 0, 0, nullptr, 0.0f,
+                                      nullptr, stream));
+            MI_STEP(mi_ssd_block_scan(xs, xp, W, xz, 2 * D, D, ly.decay_tab, p.n_heads, ly.s_y, yo, h_state[l],
+                                      h_state[l], m, 1, D, N, stream));
+            MI_STEP(mi_bitlinear_gemv(yo, D, ly.w_out, r, d, MI_OUT_RESIDUAL, m, d, D, 0, ly.res_mult, ly.res_shift,
+                                      nullptr, 0.0f, nullptr, stream));
+        }
+        MI_STEP(mi_norm_bitlinear_argmax(r, nullptr, 1, p.gamma_f, p.w_head, logits, ld_logits, keys, m,
+                                         p.vocab_size, d, stream));
+        MI_STEP(mi_argmax_keys(keys, (p.vocab_size + 63) / 64, next_ids, m, stream));
+        return MI_OK;
+    }
     for (int l = 0; l < p.n_layer; ++l) {
         const mi_layer_params &ly = p.layers[l];
         // layer 0 reads the embedding's full sums, later layers the partials

@@ -13,19 +13,21 @@ with the kernels' alignment.  Layout (little-endian):
 - header, 128 bytes: magic ``MIQCKPT\\0``, u32 format 1, u32 header bytes 128,
   char spec[16] ``mi-spec-1``, u32 d_model, n_layer, vocab_size, d_state,
   dt_rank, u32 tensor count, u64 table offset, u64 file bytes, f32
-  logit_scale, u32 CRC-32 of the table, zeros;
+  logit_scale, u32 CRC-32 of the table, u32 block (0 dyadic scan, 1
+  multi-head SSD), u32 n_heads, u32 d_head, zeros;
 - table, 96 bytes per tensor: char name[48], u32 dtype (1 i8, 2 u8, 3 i16,
   4 i32, 5 f32), u32 ndim, u32 shape[4], u64 offset, u64 bytes, u32 CRC-32,
   u32 zero;
 - the tensors: ``emb``, ``gamma_f``, ``w_head``, ``layer_scalars`` (int32
   [n_layer, 8]: s_in, s_x, s_dt, decay_shift, s_y, res_mult, res_shift, 0) and
   per layer ``layers.{i}.{gamma, w_in, conv_w, conv_b, w_x, w_dt, base,
-  w_out}``.
+  w_out}`` (the SSD block: ``decay_tab`` in place of ``w_dt`` and ``base``).
 
 ``convert_state_dict`` maps a ``MambaIntegerModel`` float state dict (keys of
-``mamba_integer_model.py:368-394,449-484`` and ``rational_bitnet.py:150-158``)
-onto these integers with the fixed-point formats of spec mi-spec-1 (section
-6 of the spec lists the rules).
+``mamba_integer_model.py:368-394,449-484``, ``ssd_multihead.py:481-522`` for
+the multi-head SSD block, and ``rational_bitnet.py:150-158``) onto these
+integers with the fixed-point formats of spec mi-spec-1 (sections 6 and 7 of
+the spec list the rules).
 """
 from __future__ import annotations
 
@@ -37,17 +39,20 @@ from typing import Dict, List, Mapping, Tuple
 
 import numpy as np
 
-from .params import DECAY_MAX, DECAY_SHIFT, LayerParams, ModelDims, ModelParams, pack_ternary
+from .params import (DECAY_MAX, DECAY_SHIFT, LayerParams, ModelDims, ModelParams, SSDLayerParams, pack_ternary,
+                     ssd_decay_table)
 
 MAGIC = b"MIQCKPT\0"
 FORMAT = 1
 SPEC = "mi-spec-1"
 ALIGN = 256
-_HEADER = struct.Struct("<8sII16s5IIQQfI48x")
+_HEADER = struct.Struct("<8sII16s5IIQQfIIII36x")
 _ENTRY = struct.Struct("<48sII4IQQII")
 _DTYPES = {1: np.int8, 2: np.uint8, 3: np.int16, 4: np.int32, 5: np.float32}
 _CODES = {(np.dtype(v).kind, np.dtype(v).itemsize): k for k, v in _DTYPES.items()}
 _LAYER_KEYS = ("gamma", "w_in", "conv_w", "conv_b", "w_x", "w_dt", "base", "w_out")
+_SSD_KEYS = ("gamma", "w_in", "conv_w", "conv_b", "w_x", "decay_tab", "w_out")
+BLOCK_DYADIC, BLOCK_SSD = 0, 1
 
 assert _HEADER.size == 128 and _ENTRY.size == 96
 
@@ -61,10 +66,11 @@ def _expected(dims: ModelDims) -> List[Tuple[str, np.dtype, Tuple[int, ...]]]:
     out = [("emb", np.int8, (V, d)), ("gamma_f", np.int16, (d,)), ("w_head", np.uint8, (V, d // 4)),
            ("layer_scalars", np.int32, (dims.n_layer, 8))]
     shapes = {"gamma": (np.int16, (d,)), "w_in": (np.uint8, (2 * D, d // 4)), "conv_w": (np.int8, (D, 4)),
-              "conv_b": (np.int32, (D,)), "w_x": (np.uint8, (R + 2 * N, D // 4)),
-              "w_dt": (np.uint8, (D, R // 4)), "base": (np.int32, (D, N)), "w_out": (np.uint8, (d, D // 4))}
+              "conv_b": (np.int32, (D,)), "w_x": (np.uint8, (dims.xp_width, D // 4)),
+              "w_dt": (np.uint8, (D, R // 4)), "base": (np.int32, (D, N)), "w_out": (np.uint8, (d, D // 4)),
+              "decay_tab": (np.int32, (dims.n_heads, 255))}
     for i in range(dims.n_layer):
-        for k in _LAYER_KEYS:
+        for k in (_SSD_KEYS if dims.ssd else _LAYER_KEYS):
             dt, sh = shapes[k]
             out.append((f"layers.{i}.{k}", dt, sh))
     return [(n, np.dtype(t), s) for n, t, s in out]
@@ -73,9 +79,10 @@ def _expected(dims: ModelDims) -> List[Tuple[str, np.dtype, Tuple[int, ...]]]:
 def _tensors(params: ModelParams) -> Dict[str, np.ndarray]:
     t = {"emb": params.emb, "gamma_f": params.gamma_f, "w_head": params.w_head}
     sc = np.zeros((params.dims.n_layer, 8), np.int32)
+    ssd = params.dims.ssd
     for i, ly in enumerate(params.layers):
-        sc[i, :7] = (ly.s_in, ly.s_x, ly.s_dt, ly.k, ly.s_y, ly.res_mult, ly.res_shift)
-        for k in _LAYER_KEYS:
+        sc[i, :7] = (ly.s_in, ly.s_x, 0 if ssd else ly.s_dt, ly.k, ly.s_y, ly.res_mult, ly.res_shift)
+        for k in (_SSD_KEYS if ssd else _LAYER_KEYS):
             t[f"layers.{i}.{k}"] = getattr(ly, k)
     t["layer_scalars"] = sc
     return t
@@ -110,7 +117,8 @@ def save(params: ModelParams, path: str, logit_scale: float) -> None:
     end = blobs[-1][0] + len(blobs[-1][1])
     header = _HEADER.pack(MAGIC, FORMAT, _HEADER.size, SPEC.encode().ljust(16, b"\0"), dims.d_model,
                           dims.n_layer, dims.vocab_size, dims.d_state, dims.dt_rank, len(arrays), table_off, end,
-                          float(logit_scale), zlib.crc32(table))
+                          float(logit_scale), zlib.crc32(table), BLOCK_SSD if dims.ssd else BLOCK_DYADIC,
+                          dims.n_heads if dims.ssd else 0, dims.d_head if dims.ssd else 0)
     buf = bytearray(end)
     buf[:len(header)] = header
     buf[table_off:table_off + len(table)] = table
@@ -128,7 +136,7 @@ def load(path: str) -> Tuple[ModelParams, float]:
     if len(b) < _HEADER.size:
         raise CheckpointError(f"{path}: shorter than the header")
     (magic, fmt, hbytes, spec, d_model, n_layer, vocab, d_state, dt_rank, nt, toff, fbytes, logit_scale,
-     tcrc) = _HEADER.unpack_from(b, 0)
+     tcrc, block, n_heads, d_head) = _HEADER.unpack_from(b, 0)
     if magic != MAGIC:
         raise CheckpointError(f"{path}: not an integer checkpoint (bad magic)")
     if fmt != FORMAT or hbytes != _HEADER.size:
@@ -140,7 +148,13 @@ def load(path: str) -> Tuple[ModelParams, float]:
         raise CheckpointError(f"{path}: header says {fbytes} bytes, file has {len(b)}")
     if not logit_scale > 0:
         raise CheckpointError(f"{path}: logit_scale must be positive")
-    dims = ModelDims(d_model=d_model, n_layer=n_layer, vocab_size=vocab, d_state=d_state, dt_rank=dt_rank)
+    if block not in (BLOCK_DYADIC, BLOCK_SSD):
+        raise CheckpointError(f"{path}: block {block} unknown")
+    if block == BLOCK_SSD:
+        dims = ModelDims(d_model=d_model, n_layer=n_layer, vocab_size=vocab, d_state=d_state, dt_rank=dt_rank,
+                         block="ssd", n_heads=n_heads, d_head=d_head)
+    else:
+        dims = ModelDims(d_model=d_model, n_layer=n_layer, vocab_size=vocab, d_state=d_state, dt_rank=dt_rank)
     try:
         dims.validate()
     except ValueError as e:
@@ -188,6 +202,13 @@ def load(path: str) -> Tuple[ModelParams, float]:
         if k != DECAY_SHIFT:
             raise CheckpointError(f"{path}: layer {i}: decay shift {k} (the scan kernels take {DECAY_SHIFT})")
         g = lambda key: found[f"layers.{i}.{key}"]  # noqa: E731
+        if dims.ssd:
+            if g("decay_tab").min() < 0 or g("decay_tab").max() > 32768:
+                raise CheckpointError(f"{path}: layer {i}: decay numerator outside [0,32768]")
+            layers.append(SSDLayerParams(gamma=g("gamma"), w_in=g("w_in"), s_in=s_in, conv_w=g("conv_w"),
+                                         conv_b=g("conv_b"), w_x=g("w_x"), s_x=s_x, decay_tab=g("decay_tab"),
+                                         s_y=s_y, w_out=g("w_out"), res_mult=res_mult, res_shift=res_shift, k=k))
+            continue
         if g("base").min(initial=0) < 0 or g("base").max(initial=0) > DECAY_MAX:
             raise CheckpointError(f"{path}: layer {i}: decay numerator outside [0,{DECAY_MAX}]")
         layers.append(LayerParams(gamma=g("gamma"), w_in=g("w_in"), s_in=s_in, conv_w=g("conv_w"),
@@ -259,7 +280,8 @@ def _strip(sd: Mapping[str, object]) -> Dict[str, object]:
 
 def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[ModelParams, float]:
     """Integer parameters of a reference ``MambaIntegerModel`` (the dyadic-scan
-    block, ``mamba_integer_model.py:368-394,466-484``) from its float state dict.
+    block, ``mamba_integer_model.py:368-394,466-484``, or with ``use_ssd`` the
+    multi-head SSD block, ``ssd_multihead.py:471-522``) from its float state dict.
 
     Fixed-point formats of spec mi-spec-1: residual Q8, block activations Q4,
     conv taps Q6, conv bias Q10, gains Q8, decay_mod integer.  Hence
@@ -274,9 +296,6 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     sd = _strip(state_dict)
     dims = ModelDims.from_config(config)
     dims.validate()
-    if config.get("ssm_cfg", {}).get("use_ssd", False):
-        raise CheckpointError("multi-head SSD (MambaIntegerBlockV2) checkpoints are not covered by the "
-                              "mi-spec-1 block")
     d, D, N, R, V = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank, dims.vocab_size
     used = set()
 
@@ -297,6 +316,9 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     layers = []
     for i in range(dims.n_layer):
         p = f"layers.{i}."
+        if dims.ssd:
+            layers.append(_convert_ssd_layer(p, dims, get, gain))
+            continue
         w_in, s_in_w = ternary(get(p + "in_proj.weight", (2 * D, d)))
         w_x, s_x_w = ternary(get(p + "x_proj.weight", (R + 2 * N, D)))
         w_dt, s_dt_w = ternary(get(p + "dt_proj.weight", (D, R)))
@@ -324,6 +346,31 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     if extra:
         raise CheckpointError(f"state dict keys the mi-spec-1 model does not use: {extra[:5]}")
     return params, s_head / 16.0 / math.sqrt(d)
+
+
+def _convert_ssd_layer(p: str, dims: ModelDims, get, gain) -> SSDLayerParams:
+    """One MambaIntegerBlockV2 layer (``ssd_multihead.py:481-522``, spec section
+    7): the x_proj rows, per head [dt, B (N), C (N)] (``:535-546``), are
+    quantized with one scale over the whole matrix and then reordered to the
+    planar [B | C | dt | zero padding] layout; A_log becomes the per-head decay
+    table; the norm's eps is not part of the integer rule."""
+    d, D, N, H = dims.d_model, dims.d_inner, dims.d_state, dims.n_heads
+    w_in, s_in_w = ternary(get(p + "in_proj.weight", (2 * D, d)))
+    wx, s_x_w = ternary(get(p + "x_proj.weight", (H * (1 + 2 * N), D)))
+    wx = wx.reshape(H, 1 + 2 * N, D)
+    planar = np.zeros((dims.xp_width, D), np.int8)
+    planar[:H * N] = wx[:, 1:1 + N].reshape(H * N, D)
+    planar[H * N:2 * H * N] = wx[:, 1 + N:].reshape(H * N, D)
+    planar[2 * H * N:2 * H * N + H] = wx[:, 0]
+    w_out, s_out_w = ternary(get(p + "out_proj.weight", (d, D)))
+    res_mult, res_shift = residual_factor(s_out_w, float(get(p + "res_gate", (1,))[0]))
+    return SSDLayerParams(
+        gamma=gain(p + "norm"), w_in=pack_ternary(w_in), s_in=requant_shift_for(s_in_w, 4, 4),
+        conv_w=_fixed(get(p + "conv1d.weight", (D, 1, 4)).reshape(D, 4), 64.0, -127, 127, np.int8),
+        conv_b=_fixed(get(p + "conv1d.bias", (D,)), 1024.0, -(2**31), 2**31 - 1, np.int32),
+        w_x=pack_ternary(planar), s_x=requant_shift_for(s_x_w, 4, 4),
+        decay_tab=ssd_decay_table(get(p + "A_log", (H,)).numpy().astype(np.float64)), s_y=14,
+        w_out=pack_ternary(w_out), res_mult=res_mult, res_shift=res_shift)
 
 
 def convert_reference_checkpoint(state_dict_path: str, config: dict, out_path: str) -> ModelParams:

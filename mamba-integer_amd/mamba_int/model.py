@@ -250,7 +250,13 @@ class IntegerMambaRunner:
             return ops.norm_bitlinear(r_rows, self.gamma_f, self.w_head, ops.OUT_INT32, self.dims.vocab_size,
                                       out=out, row_stats=stats)
         a = ops.bitshift_norm(r_rows, self.gamma_f, row_stats=stats)
-        return ops.bitlinear(a, self.w_head, ops.OUT_INT32, self.dims.vocab_size, out=out)
+        V = self.dims.vocab_size
+        if out is not None or V % 4 == 0:
+            return ops.bitlinear(a, self.w_head, ops.OUT_INT32, V, out=out)
+        # int32 output rows are stored 16 bytes at a time: pad the row stride
+        padded = torch.empty((a.shape[0], V + (-V) % 4), dtype=torch.int32, device=a.device)
+        ops.bitlinear(a, self.w_head, ops.OUT_INT32, V, out=padded)
+        return padded[:, :V].contiguous()
 
     def _run(self, ids: torch.Tensor, state: DecodeState, fresh: bool) -> _Workspace:
         B, L = ids.shape

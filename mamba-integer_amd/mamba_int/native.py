@@ -24,20 +24,24 @@ class LayerParams(ctypes.Structure):
     _fields_ = [("gamma", _P), ("w_in", _P), ("s_in", _I), ("conv_w", _P), ("conv_b", _P),
                 ("w_x", _P), ("s_x", _I), ("w_dt", _P), ("s_dt", _I), ("base", _P),
                 ("decay_shift", _I), ("s_y", _I), ("w_out", _P), ("res_mult", ctypes.c_int32),
-                ("res_shift", _I)]
+                ("res_shift", _I), ("decay_tab", _P)]
 
 
 class ModelParams(ctypes.Structure):
     """Mirror of ``mi_model_params``; ``layers`` points at a host array."""
     _fields_ = [("d_model", _I), ("n_layer", _I), ("vocab_size", _I), ("d_state", _I), ("dt_rank", _I),
-                ("emb", _P), ("layers", ctypes.POINTER(LayerParams)), ("gamma_f", _P), ("w_head", _P)]
+                ("emb", _P), ("layers", ctypes.POINTER(LayerParams)), ("gamma_f", _P), ("w_head", _P),
+                ("block", _I), ("n_heads", _I), ("d_head", _I)]
+
+
+MI_BLOCK_DYADIC, MI_BLOCK_SSD = 0, 1
 
 
 class CheckpointInfo(ctypes.Structure):
     """Mirror of ``mi_checkpoint_info``."""
     _fields_ = [("format_version", _I), ("spec", ctypes.c_char * 16), ("d_model", _I), ("n_layer", _I),
                 ("vocab_size", _I), ("d_state", _I), ("dt_rank", _I), ("logit_scale", ctypes.c_float),
-                ("device_bytes", ctypes.c_size_t)]
+                ("device_bytes", ctypes.c_size_t), ("block", _I), ("n_heads", _I), ("d_head", _I)]
 
 
 def _ptr(t: torch.Tensor) -> int:
@@ -83,12 +87,14 @@ class NativeDecoder:
     def __init__(self, runner, m: int):
         dims = runner.dims
         layers = (LayerParams * dims.n_layer)()
+        opt = lambda t: None if t is None else _ptr(t)  # noqa: E731
         for i, ly in enumerate(runner.layers):
             layers[i] = LayerParams(_ptr(ly.gamma), _ptr(ly.w_in), ly.s_in, _ptr(ly.conv_w), _ptr(ly.conv_b),
-                                    _ptr(ly.w_x), ly.s_x, _ptr(ly.w_dt), ly.s_dt, _ptr(ly.base), ly.k, ly.s_y,
-                                    _ptr(ly.w_out), ly.res_mult, ly.res_shift)
+                                    _ptr(ly.w_x), ly.s_x, opt(ly.w_dt), ly.s_dt, opt(ly.base), ly.k, ly.s_y,
+                                    _ptr(ly.w_out), ly.res_mult, ly.res_shift, opt(ly.decay_tab))
         params = ModelParams(dims.d_model, dims.n_layer, dims.vocab_size, dims.d_state, dims.dt_rank,
-                             _ptr(runner.emb), layers, _ptr(runner.gamma_f), _ptr(runner.w_head))
+                             _ptr(runner.emb), layers, _ptr(runner.gamma_f), _ptr(runner.w_head),
+                             MI_BLOCK_SSD if dims.ssd else MI_BLOCK_DYADIC, dims.n_heads, dims.d_head)
         self._setup(params, runner.device, m, owner=(runner, layers))
 
     @classmethod

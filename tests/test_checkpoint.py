@@ -46,7 +46,8 @@ def test_round_trip_and_layout(tmp_path):
     _equal(p, q)
     assert scale == np.float32(0.0125)
     b = path.read_bytes()
-    magic, fmt, hb, spec, d, nl, v, ns, dr, nt, toff, fb, ls, tcrc = ckpt._HEADER.unpack_from(b, 0)
+    magic, fmt, hb, spec, d, nl, v, ns, dr, nt, toff, fb, ls, tcrc, blk, nh, dh = ckpt._HEADER.unpack_from(b, 0)
+    assert (blk, nh, dh) == (0, 0, 0)
     assert (magic, fmt, hb, spec.rstrip(b"\0"), fb) == (b"MIQCKPT\0", 1, 128, b"mi-spec-1", len(b))
     assert (d, nl, v, ns, dr) == (64, 2, 100, 16, 16) and nt == 4 + 8 * 2
     assert zlib.crc32(b[toff:toff + 96 * nt]) == tcrc
@@ -223,7 +224,7 @@ def test_convert_state_dict_rules(tmp_path):
 
 @pytest.mark.parametrize("change,needle", [
     ("drop", "no 'layers.1.x_proj.weight'"), ("shape", "shape"), ("extra", "does not use"),
-    ("shifts", "uniform shift"), ("bias", "dt bias"), ("ssd", "MambaIntegerBlockV2"),
+    ("shifts", "uniform shift"), ("bias", "dt bias"), ("ssd", "no 'layers.0.x_proj.weight'|shape"),
 ])
 def test_convert_rejects(change, needle):
     import torch
@@ -266,3 +267,70 @@ def test_convert_reference_checkpoint_file(tmp_path):
     r, _ = ckpt.convert_state_dict(sd, _config())
     _equal(p, r)
     assert np.array_equal(pack_ternary(unpack_ternary(q.w_head, 64)), q.w_head)
+
+
+# ------------------------------------------------ multi-head SSD block (V2)
+SSD_DIMS = ModelDims(d_model=64, n_layer=2, vocab_size=90, d_state=16, dt_rank=0, block="ssd", n_heads=2,
+                     d_head=32)
+
+
+def _ssd_state_dict(rng, dims=SSD_DIMS):
+    import torch
+    d, D, N, H, V = dims.d_model, dims.d_inner, dims.d_state, dims.n_heads, dims.vocab_size
+    f = lambda *s, sc=1.0: torch.from_numpy((rng.standard_normal(s) * sc).astype(np.float32))  # noqa: E731
+    sd = {"embedding.weight": f(V, d), "norm_f.gamma": 1 + f(d, sc=0.1), "norm_f.step_size": torch.ones(1),
+          "lm_head.weight": f(V, d, sc=d ** -1)}
+    for i in range(dims.n_layer):
+        p = f"layers.{i}."
+        sd.update({p + "norm.gamma": 1 + f(d, sc=0.1), p + "norm.step_size": torch.tensor([1.25]),
+                   p + "in_proj.weight": f(2 * D, d, sc=d ** -0.5), p + "conv1d.weight": f(D, 1, 4, sc=0.5),
+                   p + "conv1d.bias": f(D, sc=0.1), p + "x_proj.weight": f(H * (1 + 2 * N), D, sc=D ** -0.5),
+                   p + "A_log": torch.from_numpy(rng.uniform(-2.5, 0.0, H).astype(np.float32)),
+                   p + "out_proj.weight": f(d, D, sc=D ** -0.5), p + "res_gate": torch.tensor([0.144])})
+    return sd
+
+
+def _ssd_config(dims=SSD_DIMS):
+    return {"d_model": dims.d_model, "n_layer": dims.n_layer, "vocab_size": dims.vocab_size,
+            "ssm_cfg": {"d_state": dims.d_state, "use_ssd": True, "n_heads": dims.n_heads, "d_head": dims.d_head}}
+
+
+def test_ssd_round_trip_and_native_info(tmp_path):
+    from mamba_int.native import NativeCheckpoint
+    p = init_random_params(ModelDims(**SSD_DIMS.__dict__), 9)
+    path = tmp_path / "v2.miq"
+    ckpt.save(p, str(path), 0.5)
+    q, _ = ckpt.load(str(path))
+    _equal(p, q)
+    i = NativeCheckpoint(str(path)).info
+    assert (i.block, i.n_heads, i.d_head, i.d_state) == (1, 2, 32, 16)
+    p.layers[1].decay_tab[0, 3] = 32769                      # outside [0, 2^15]
+    ckpt.save(p, str(path), 0.5)
+    with pytest.raises(ckpt.CheckpointError, match="decay numerator"):
+        ckpt.load(str(path))
+    st, msg = _native_open(path)
+    assert st != 0 and "decay numerator" in msg
+
+
+def test_convert_ssd_state_dict(tmp_path):
+    """The V2 conversion: x_proj quantized over the reference's row order and
+    reordered to planar [B | C | dt | 0]; A_log -> the decay table; V2 norm gain."""
+    from mamba_int import ssd_decay_table
+    sd = _ssd_state_dict(np.random.default_rng(4))
+    p, _ = ckpt.convert_state_dict(sd, _ssd_config())
+    assert p.dims.ssd and p.dims.xp_width == 80
+    H, N, D = 2, 16, 64
+    for i in range(2):
+        ly = p.layers[i]
+        w = sd[f"layers.{i}.x_proj.weight"].numpy()
+        s = np.float32(np.abs(w).astype(np.float64).mean())
+        wq = np.clip(np.round(w / s), -1, 1).astype(np.int8).reshape(H, 1 + 2 * N, D)
+        got = unpack_ternary(ly.w_x, D)
+        assert np.array_equal(got[:H * N], wq[:, 1:1 + N].reshape(-1, D))
+        assert np.array_equal(got[H * N:2 * H * N], wq[:, 1 + N:].reshape(-1, D))
+        assert np.array_equal(got[2 * H * N:2 * H * N + H], wq[:, 0])
+        assert not got[2 * H * N + H:].any()
+        assert np.array_equal(ly.decay_tab, ssd_decay_table(sd[f"layers.{i}.A_log"].numpy()))
+        assert np.array_equal(ly.gamma, np.round(sd[f"layers.{i}.norm.gamma"].numpy() * np.float32(1.25) * 256))
+    ckpt.save(p, str(tmp_path / "c.miq"), 1.0)
+    _equal(p, ckpt.load(str(tmp_path / "c.miq"))[0])

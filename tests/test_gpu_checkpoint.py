@@ -67,3 +67,36 @@ def test_converted_float_checkpoint_matches_oracle(cuda, tmp_path):
     flt = model(T(ids))
     assert torch.equal(flt, got.to(torch.float32) * model.logit_scale)
     assert np.array_equal(H(model.generate(T(ids), 6))[:, 16:], om.generate(ids, 6))
+
+
+def test_ssd_checkpoint_native_decode_and_conversion(cuda, tmp_path):
+    """The multi-head SSD block through the file format: a random model decodes
+    natively (mi_checkpoint_upload -> mi_decode_step, the per-op SSD path) to
+    the oracle's greedy continuation, the runner-built native decoder agrees,
+    and a converted V2 float state dict matches the oracle's logits."""
+    import torch
+    from test_checkpoint import _ssd_config, _ssd_state_dict
+    from mamba_int import ops
+    from mamba_int.model import IntegerMambaRunner
+    from mamba_int.native import NativeCheckpoint, NativeDecoder
+    from mamba_integer_model import MambaIntegerModel
+    dims = ModelDims(d_model=128, n_layer=2, vocab_size=500, d_state=32, dt_rank=0, block="ssd", n_heads=4,
+                     d_head=64)
+    p = init_random_params(dims, 17)
+    path = tmp_path / "v2.miq"
+    ckpt.save(p, str(path), 0.01)
+    ids = np.random.default_rng(6).integers(0, 500, size=(3, 10))
+    ref = O.OracleModel(p).generate(ids, 8)
+    run = IntegerMambaRunner(p)
+    lg, st = run.prefill(T(ids))
+    first = ops.argmax(lg)
+    ck = NativeCheckpoint(str(path), device="cuda")
+    assert ck.params.block == 1 and ck.params.layers[1].decay_tab
+    assert np.array_equal(H(ck.decoder(3).generate(first, st.clone(), 8)), ref)
+    assert np.array_equal(H(NativeDecoder(run, 3).generate(first, st, 8)), ref)
+    sd = _ssd_state_dict(np.random.default_rng(8))
+    torch.save(sd, tmp_path / "v2.pt")
+    ckpt.convert_reference_checkpoint(str(tmp_path / "v2.pt"), _ssd_config(), str(tmp_path / "c2.miq"))
+    model = MambaIntegerModel.from_checkpoint(str(tmp_path / "c2.miq"))
+    ids = np.random.default_rng(9).integers(0, 90, size=(2, 12))
+    assert np.array_equal(H(model.forward_int(T(ids))), O.OracleModel(model.params).forward(ids))
