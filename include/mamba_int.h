@@ -143,12 +143,12 @@ mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, v
 /* The decode out_proj with the next norm's row statistics as per-block
  * partials instead of atomics (the residual update of BitLinear.forward +
  * MambaIntegerBlock.forward's residual add, mamba_integer_model.py:446-447,
- * for m <= 16 tokens): r[m, n] (int32, row stride ldr) is updated as by
+ * for m <= 64 tokens): r[m, n] (int32, row stride ldr) is updated as by
  * mi_bitlinear_gemv RESIDUAL, and stats_parts int64 [m, ceil(n/16), 2]
  * receives, for every row i and block b of 16 features, the sum and the sum
  * of squares of the updated r[i, 16b : 16b+16] (plain stores: no zeroing,
  * no atomics).  The norm entries below sum them (their stats_parts =
- * ceil(n/16)).  m <= 16; k % 64 == 0; a, w_packed, stats_parts 16-byte
+ * ceil(n/16)).  m <= 64; k % 64 == 0; a, w_packed, stats_parts 16-byte
  * aligned. */
 mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const uint8_t *w_packed, int32_t *r,
                                       int ldr, int m, int n, int k, int32_t res_mult, int res_shift,
@@ -238,7 +238,8 @@ mi_status mi_argmax_i32(const int32_t *logits, int ld, int64_t *out, int rows, i
  * mi_embed / RESIDUAL atomics (8-byte aligned), ceil(d/16) for the partials
  * of mi_bitlinear_residual_parts (16-byte aligned); stats_parts <= 4096. */
 
-/* BitShiftNorm of r (int32 [m,k], m <= 16, k % 64 == 0, k <= 3072; r and
+/* BitShiftNorm of r (int32 [m,k], m <= 64 (16-token row groups, one block
+ * row each), k % 64 == 0, k <= 3072; r and
  * w_packed 16-byte, gamma 8-byte aligned) fused into
  * the BitLinear GEMV: out[m, n] = INT8 (sat8(rshr(acc, shift))) or INT32 acc,
  * out row stride ldo.  Replaces BitShiftNorm.forward + BitLinear.forward for
@@ -252,7 +253,7 @@ mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stats, int stat
  * r int32 [m,d_model]; w_in packed [2*d_inner, d_model/4]; the x half goes
  * through the conv with conv_state int8 [m,3,d_inner] updated in place and
  * lands in xs int8 [m,d_inner]; the z half is written to xz int8
- * [m,2*d_inner] at columns [d_inner, 2*d_inner).  m <= 16, d_model <= 3072;
+ * [m,2*d_inner] at columns [d_inner, 2*d_inner).  m <= 64, d_model <= 3072;
  * alignment as mi_norm_bitlinear. */
 mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, int stats_parts,
                                const int16_t *gamma, const uint8_t *w_in, int s_in,
@@ -360,7 +361,7 @@ typedef struct mi_model_params {
 } mi_model_params;
 
 /* Bytes of the caller-owned device workspace mi_decode_step needs at batch m
- * (1 <= m <= 16; d_model % 64 == 0, <= 3072; dyadic block: dt_rank % 16 ==
+ * (1 <= m <= 64; d_model % 64 == 0, <= 3072; dyadic block: dt_rank % 16 ==
  * 0 and dt_rank + 2*d_state <= 256; SSD block: d_head % 16 == 0, d_state in
  * {16, 32, 64}). */
 mi_status mi_decode_workspace_size(const mi_model_params *params, int m, size_t *bytes);

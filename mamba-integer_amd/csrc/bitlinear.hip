@@ -37,7 +37,7 @@ struct GemmArgs {
     int res_shift;
     float w_scale;
     int64_t *row_stats;  // RESIDUAL: per-row (sum r, sum r^2) of the new residual, atomically added
-    int64_t *stats_parts;  // RESIDUAL, m <= 16: [M][N/16][2] per-block (sum r, sum r^2), plain stores
+    int64_t *stats_parts;  // RESIDUAL: [M][N/16][2] per-block (sum r, sum r^2), plain stores
 };
 
 struct RowStat {
@@ -505,8 +505,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
 // address and zeroed.  The residual each output overwrites is read at kernel
 // start.  Row statistics of the new residual: per-block partials with plain
 // stores (stats_parts) or 64-bit atomics (row_stats).
-// Requires kw % 4 == 0, 16-byte aligned w, a and lda.
-__global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g) {
+// Requires kw % 4 == 0, 16-byte aligned w, a and lda.  Blocks along y take
+// 16-token row groups (m <= 64 in one launch; the weight tile of a block is
+// then shared by the row groups through L2).
+__global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
+    GemmArgs g = g0;
+    if (gridDim.y > 1) {
+        const int64_t m0 = 16 * (int64_t)blockIdx.y;
+        g.M = min(16, g0.M - (int)m0);
+        g.a += m0 * g.lda;
+        g.out = (int32_t *)g.out + m0 * g.ldo;
+        if (g.stats_parts) g.stats_parts += m0 * gridDim.x * 2;
+        if (g.row_stats) g.row_stats += m0 * 2;
+    }
     __shared__ int32_t red[8][64][4];
     __shared__ int32_t s_new[16][17];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
@@ -770,14 +781,15 @@ extern "C" mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const
     clear_error();
     mi_status st = validate(fn, a, lda, w_packed, r, ldr, MI_OUT_RESIDUAL, m, n, k, 0, res_shift, nullptr);
     if (st != MI_OK || (int64_t)m * n == 0) return st;
-    MI_REQUIRE(m <= 16, MI_ERR_BAD_DIM, "%s: m=%d must be <= 16", fn, m);
+    MI_REQUIRE(m <= 64, MI_ERR_BAD_DIM, "%s: m=%d must be <= 64", fn, m);
     MI_REQUIRE(k % 64 == 0, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 64", fn, k);
     MI_REQUIRE(stats_parts, MI_ERR_NULL_POINTER, "%s: stats_parts is required", fn);
     MI_REQUIRE(aligned(w_packed, 16) && aligned(stats_parts, 16), MI_ERR_BAD_ALIGNMENT,
                "%s: w_packed and stats_parts must be 16-byte aligned", fn);
     GemmArgs g = make_args(a, lda, w_packed, r, ldr, m, n, k, 0, res_mult, res_shift, nullptr, 0.0f, nullptr);
     g.stats_parts = stats_parts;
-    hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((n + 15) / 16)), dim3(512), 0, as_stream(stream), g);
+    hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16)), dim3(512), 0,
+                       as_stream(stream), g);
     return check_launch(fn);
 }
 

@@ -21,7 +21,8 @@
 namespace mi {
 namespace {
 
-constexpr int kMaxRows = 16;    // tokens per norm_gemv launch
+constexpr int kMaxRows = 16;    // tokens per norm_gemv block
+constexpr int kMaxRowGroups = 4; // blocks along y: 16-token row groups of one launch
 constexpr int kMaxNormK = 3072; // d_model limit of the LDS-staged rows
 constexpr int kMaxXTiles = 16;  // x_proj outputs (dt_rank + 2*nstate) <= 256
 constexpr int kMaxStatParts = 4096;  // row-statistics partials per row
@@ -236,8 +237,26 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, con
 // issued before the rows are staged, so its latency overlaps the staging.
 constexpr int kMaxSuper = kMaxNormK / 256;
 
+// The arguments of row group y (tokens [16y, 16y + 16)): every per-token
+// pointer moves to the group's first row.
+template <int KIND>
+__device__ __forceinline__ NormGemvArgs row_group(const NormGemvArgs &g0, int y) {
+    NormGemvArgs g = g0;
+    const int64_t m0 = (int64_t)kMaxRows * y;
+    g.M = min(kMaxRows, g0.M - (int)m0);
+    g.r += m0 * g.K;
+    if (g.row_stats) g.row_stats += m0 * g.stats_parts * 2;
+    if (g.out) g.out = (char *)g.out + m0 * g.ldo * (KIND == MI_OUT_INT32 ? 4 : 1);
+    if (g.conv_state) g.conv_state += m0 * 3 * g.conv_d;
+    if (g.xs) g.xs += m0 * g.conv_d;
+    if (g.xpart) g.xpart += m0 * (g.conv_d / 16) * g.nx;
+    if (g.keys) g.keys += m0 * gridDim.x;
+    return g;
+}
+
 template <int KIND, bool CONV, bool WIDE>
-__global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g) {
+__global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g0) {
+    const NormGemvArgs g = gridDim.y > 1 ? row_group<KIND>(g0, blockIdx.y) : g0;
     extern __shared__ __align__(16) int8_t smem[];
     const int pitch = g.K + 16;                       // conflict-free b128 row reads
     int8_t *a = smem;                                 // [16][pitch]
@@ -760,7 +779,8 @@ void launch_xproj_scan(int ntiles, dim3 grid, hipStream_t hs, const DtScanArgs &
 mi_status check_norm_gemv(const char *fn, const int32_t *r, const int64_t *row_stats, int stats_parts,
                           const int16_t *gamma, const uint8_t *w, int m, int n, int k) {
     MI_REQUIRE(m >= 0 && n >= 0 && k >= 0, MI_ERR_BAD_DIM, "%s: negative size", fn);
-    MI_REQUIRE(m <= kMaxRows, MI_ERR_BAD_DIM, "%s: m=%d exceeds %d tokens", fn, m, kMaxRows);
+    MI_REQUIRE(m <= kMaxRows * kMaxRowGroups, MI_ERR_BAD_DIM, "%s: m=%d exceeds %d tokens", fn, m,
+               kMaxRows * kMaxRowGroups);
     MI_REQUIRE(k % 64 == 0 && k <= kMaxNormK, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 64 and <= %d", fn, k,
                kMaxNormK);
     if ((int64_t)m * n == 0) return MI_OK;
@@ -800,7 +820,7 @@ extern "C" mi_status mi_norm_bitlinear(const int32_t *r, const int64_t *row_stat
     g.M = m; g.N = n; g.K = k; g.kw = k / 16; g.shift = shift;
     // wide blocks (64 features) once there are enough of them to fill the GPU
     const bool wide = n >= 16384;
-    const dim3 grid((unsigned)(wide ? (n + 63) / 64 : (n + 15) / 16));
+    const dim3 grid((unsigned)(wide ? (n + 63) / 64 : (n + 15) / 16), (unsigned)((m + kMaxRows - 1) / kMaxRows));
     const size_t lds = norm_gemv_lds(k);
     hipStream_t hs = as_stream(stream);
     if (kind == MI_OUT_INT32) {
@@ -827,7 +847,8 @@ extern "C" mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *r
     g.r = r; g.row_stats = row_stats; g.stats_parts = stats_parts; g.gamma = gamma;
     g.w = reinterpret_cast<const uint32_t *>(w_packed); g.out = logits; g.ldo = ldo; g.keys = keys;
     g.M = m; g.N = n; g.K = k; g.kw = k / 16; g.shift = 0;
-    hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT32, false, true>), dim3((unsigned)((n + 63) / 64)), dim3(256),
+    hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT32, false, true>),
+                       dim3((unsigned)((n + 63) / 64), (unsigned)((m + kMaxRows - 1) / kMaxRows)), dim3(256),
                        norm_gemv_lds(k), as_stream(stream), g);
     return check_launch("mi_norm_bitlinear_argmax");
 }
@@ -862,7 +883,8 @@ mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t
     g.M = m; g.N = 2 * d_inner; g.K = d_model; g.kw = d_model / 16; g.shift = s_in;
     g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs; g.conv_d = d_inner;
     g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.nx = nx; g.xpart = xpart;
-    hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, true, false>), dim3((unsigned)(2 * d_inner / 16)), dim3(256),
+    hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, true, false>),
+                       dim3((unsigned)(2 * d_inner / 16), (unsigned)((m + kMaxRows - 1) / kMaxRows)), dim3(256),
                        norm_gemv_lds(d_model), as_stream(stream), g);
     return check_launch(fn);
 }

@@ -55,7 +55,7 @@ WsLayout ws_layout(const mi_model_params &p, int m) {
 
 mi_status check_model(const char *fn, const mi_model_params *p, int m) {
     MI_REQUIRE(p, MI_ERR_NULL_POINTER, "%s: params is NULL", fn);
-    MI_REQUIRE(m >= 1 && m <= 16, MI_ERR_BAD_DIM, "%s: m=%d outside [1,16] (the fused decode stages)", fn, m);
+    MI_REQUIRE(m >= 1 && m <= 64, MI_ERR_BAD_DIM, "%s: m=%d outside [1,64] (the fused decode stages)", fn, m);
     MI_REQUIRE(p->n_layer >= 1 && p->vocab_size >= 1, MI_ERR_BAD_DIM, "%s: n_layer and vocab_size must be >= 1", fn);
     MI_REQUIRE(p->d_model >= 64 && p->d_model % 64 == 0 && p->d_model <= 3072, MI_ERR_BAD_DIM,
                "%s: d_model=%d must be a multiple of 64 in [64,3072]", fn, p->d_model);

@@ -108,11 +108,11 @@ class _Workspace:
         # summed by the next norm (one buffer: each norm reads it before its
         # layer's out_proj rewrites it)
         self.parts = (torch.empty((T, d // 16, 2), dtype=torch.int64, device=device)
-                      if T <= 16 and d % 16 == 0 else None)
+                      if T <= 64 and d % 16 == 0 else None)
         # x_proj partials of the decode chain (one row per 16 channels of d_inner)
         nx = dims.dt_rank + 2 * dims.d_state
         self.xpart = (torch.empty((T, D // 16, nx), dtype=torch.int32, device=device)
-                      if T <= 16 and (D // 16) * nx <= 8192 else None)
+                      if T <= 64 and (D // 16) * nx <= 8192 else None)
 
 
 class IntegerMambaRunner:
@@ -216,7 +216,13 @@ class IntegerMambaRunner:
                       res_shift=ly.res_shift, row_stats=stats_out)
 
     def _fused_decode_ok(self, B: int) -> bool:
-        return (not self.dims.ssd and B <= 16 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0
+        """The three fused decode stages pay off while the work every block
+        repeats stays small: each in_proj block normalizes all B rows of d
+        channels, so the repeated work grows as B * d^2.  Measured (ms per step):
+        d768 fused wins at every B <= 64 (0.69 vs 0.84 at B64), d1024 at B16 but
+        not B64, d1536 and d2048 at no batch."""
+        d = self.dims.d_model
+        return (not self.dims.ssd and B <= 64 and d <= 1024 and B * d * d <= 64 * 768 * 768 and d % 64 == 0
                 and self.dims.d_state <= 64 and self.dims.dt_rank <= 256)
 
     def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
@@ -246,7 +252,7 @@ class IntegerMambaRunner:
 
     def _head(self, r_rows: torch.Tensor, stats: Optional[torch.Tensor],
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        if r_rows.shape[0] <= 16 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0:
+        if r_rows.shape[0] <= 64 and self.dims.d_model <= 3072 and self.dims.d_model % 64 == 0:
             return ops.norm_bitlinear(r_rows, self.gamma_f, self.w_head, ops.OUT_INT32, self.dims.vocab_size,
                                       out=out, row_stats=stats)
         a = ops.bitshift_norm(r_rows, self.gamma_f, row_stats=stats)
@@ -342,7 +348,7 @@ class IntegerMambaRunner:
 
     def _chain_ok(self, B: int) -> bool:
         """The fused chain (three kernels per layer, argmax fused into the head) fits batch B."""
-        return self._fused_decode_ok(B) and self.dims.d_model <= 3072 and self._workspace(B).xpart is not None
+        return self._fused_decode_ok(B)
 
     def _decode_chain(self, ws: _Workspace, state: DecodeState, hist: torch.Tensor, keys: torch.Tensor) -> None:
         """len(hist) greedy steps.  Step 0 embeds hist[-1] (the previous pick); step j > 0

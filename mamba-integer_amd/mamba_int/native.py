@@ -80,7 +80,7 @@ class NativeCheckpoint:
 
 
 class NativeDecoder:
-    """Greedy decode through ``mi_decode_step`` at batch m (1 <= m <= 16), for
+    """Greedy decode through ``mi_decode_step`` at batch m (1 <= m <= 64), for
     the device parameters of an ``IntegerMambaRunner`` or of a
     ``NativeCheckpoint`` (``from_params``)."""
 

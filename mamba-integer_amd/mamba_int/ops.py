@@ -237,7 +237,7 @@ def _stats(row_stats: Optional[torch.Tensor], m: int):
 
 def bitlinear_residual_parts(a: torch.Tensor, w_packed: torch.Tensor, r: torch.Tensor, res_mult: int,
                              res_shift: int, stats_parts: torch.Tensor) -> None:
-    """Decode out_proj: r (int32 [m, n], m <= 16) += rescaled a @ W^T, and stats_parts
+    """Decode out_proj: r (int32 [m, n], m <= 64) += rescaled a @ W^T, and stats_parts
     (int64 [m, ceil(n/16), 2]) <- the per-16-feature (sum, sum of squares) of the new rows."""
     _req(a, torch.int8, "a"); _req(w_packed, torch.uint8, "w_packed"); _req(r, torch.int32, "r")
     _req(stats_parts, torch.int64, "stats_parts")
@@ -251,7 +251,7 @@ def bitlinear_residual_parts(a: torch.Tensor, w_packed: torch.Tensor, r: torch.T
 
 def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int,
                    shift: int = 0, out=None, row_stats=None) -> torch.Tensor:
-    """BitShiftNorm of r (int32 [m, k], m <= 16) fused into the BitLinear GEMV (INT8 or INT32 out)."""
+    """BitShiftNorm of r (int32 [m, k], m <= 64) fused into the BitLinear GEMV (INT8 or INT32 out)."""
     _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma"); _req(w_packed, torch.uint8, "w_packed")
     m, k = r.shape
     o = out if out is not None else torch.empty((m, n), dtype=_OUT_DTYPE[kind], device=r.device)

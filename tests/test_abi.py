@@ -54,10 +54,10 @@ def _fake(n=64):
     (("mi_bitshift_norm", None, None, None, 4, 0, None, None), 2, "dim"),
     (("mi_conv_squareplus", None, 16, None, None, None, None, None, 1, 4, 18, None), 2, "multiple of 4"),
     (("mi_block_scan", None, None, None, 48, 16, None, 32, 16, None, 14, 13, None, None, None, 1, 4, 16, 16, None), 4, "decay_shift"),
-    (("mi_norm_bitlinear", None, None, 1, None, None, None, 16, 1, 17, 16, 64, 0, None), 2, "m=17"),
+    (("mi_norm_bitlinear", None, None, 1, None, None, None, 16, 1, 65, 16, 64, 0, None), 2, "m=65"),
     (("mi_norm_bitlinear", "A16", "A16", 0, "A16", "A16", "O16", 16, 1, 1, 16, 64, 0, None), 4, "stats_parts=0"),
     (("mi_norm_bitlinear", "A16", "W4", 2, "A16", "A16", "O16", 16, 1, 1, 16, 64, 0, None), 3, "row_stats"),
-    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 17, 16, 64, 1, 0, "A16", None), 2, "m=17"),
+    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 65, 16, 64, 1, 0, "A16", None), 2, "m=65"),
     (("mi_bitlinear_residual_parts", "A16", 32, "A16", "O16", 16, 1, 16, 32, 1, 0, "A16", None), 2, "multiple of 64"),
     (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 1, 16, 64, 1, 0, None, None), 1, "stats_parts"),
     (("mi_dt_scan_step", None, 80, 40, None, 2, None, None, 32, 16, None, 15, 13, None, None, 1, 16, 16, None), 2, "dt_rank"),
@@ -140,7 +140,7 @@ def test_decode_step_validation():
     assert _lib.raw("mi_decode_workspace_size", pp, 8, np_) == 1 and "required" in _lib.last_error()
     p.emb = p.gamma_f = p.w_head = 0x1000
     p.layers = ctypes.cast(ctypes.c_void_p(0x1000), type(p.layers))
-    assert _lib.raw("mi_decode_workspace_size", pp, 17, np_) == 2 and "m=17" in _lib.last_error()
+    assert _lib.raw("mi_decode_workspace_size", pp, 65, np_) == 2 and "m=65" in _lib.last_error()
     p.d_model = 800
     assert _lib.raw("mi_decode_workspace_size", pp, 8, np_) == 2 and "d_model" in _lib.last_error()
     p.d_model = 768

@@ -23,7 +23,8 @@ def _resid(rng, m, d):
     return r
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 80, 64), (8, 3072, 768), (16, 300, 256), (5, 32000, 768), (8, 64, 3072)])
+@pytest.mark.parametrize("m,n,k", [(1, 80, 64), (8, 3072, 768), (16, 300, 256), (5, 32000, 768), (8, 64, 3072),
+                                   (64, 300, 256), (40, 80, 768), (33, 32000, 128)])
 def test_norm_bitlinear(cuda, m, n, k):
     from mamba_int import ops, pack_ternary
     rng = np.random.default_rng(m + n + k)
@@ -37,7 +38,7 @@ def test_norm_bitlinear(cuda, m, n, k):
     assert np.array_equal(got8, O.bitlinear(a, wp, O.OUT_INT8, 4))
 
 
-@pytest.mark.parametrize("m,d,D", [(8, 768, 1536), (1, 128, 256), (16, 256, 512)])
+@pytest.mark.parametrize("m,d,D", [(8, 768, 1536), (1, 128, 256), (16, 256, 512), (64, 256, 512), (23, 128, 256)])
 def test_norm_in_proj_conv(cuda, m, d, D):
     import torch
     from mamba_int import ops, pack_ternary
@@ -138,7 +139,8 @@ def test_xproj_dt_scan_step(cuda, m, D, N, R):
 
 @pytest.mark.parametrize("m,d,D,N,R,stats", [(8, 768, 1536, 16, 48, True), (1, 128, 256, 16, 16, False),
                                              (16, 256, 512, 32, 32, True), (3, 64, 96, 8, 16, True),
-                                             (5, 512, 1024, 64, 128, False)])
+                                             (5, 512, 1024, 64, 128, False), (64, 768, 1536, 16, 48, True),
+                                             (40, 256, 512, 32, 32, False)])
 def test_xpart_decode_chain(cuda, m, d, D, N, R, stats):
     """norm + in_proj + conv with x_proj partials, then the scan step from those
     partials, equals the unfused oracle chain (norm, in_proj, conv, x_proj,
@@ -210,7 +212,7 @@ def test_decode_residual_gemv(cuda, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 768, 1536), (1, 768, 1536), (16, 100, 512), (3, 2048, 4096), (5, 20, 320),
-                                   (16, 48, 64), (4, 96, 1600)])
+                                   (16, 48, 64), (4, 96, 1600), (64, 2048, 4096), (37, 768, 1536)])
 def test_decode_residual_parts(cuda, m, n, k):
     """The decode out_proj with per-16-feature row-statistics partials: the
     residual update equals the oracle's and each partial is the (sum, sum of
@@ -245,7 +247,7 @@ def _split_stats(rng, r, P):
 
 
 @pytest.mark.parametrize("m,k,P", [(8, 768, 48), (16, 768, 48), (1, 128, 8), (3, 3072, 192), (16, 3072, 192),
-                                   (2, 256, 300), (5, 64, 2), (16, 64, 1)])
+                                   (2, 256, 300), (5, 64, 2), (16, 64, 1), (64, 768, 48), (29, 2048, 128)])
 def test_norm_stats_partials(cuda, m, k, P):
     """The norm entries take the row statistics as stats_parts partials and sum
     them: the narrow and wide norm GEMVs, the in_proj + conv stage and the
@@ -282,7 +284,8 @@ def test_norm_stats_partials(cuda, m, k, P):
     assert np.array_equal(H(xz)[:, D:], xz_ref[:, D:])
 
 
-@pytest.mark.parametrize("m,n,k", [(8, 32000, 768), (1, 500, 128), (16, 1000, 256), (3, 64, 3072)])
+@pytest.mark.parametrize("m,n,k", [(8, 32000, 768), (1, 500, 128), (16, 1000, 256), (3, 64, 3072), (64, 500, 128),
+                                   (50, 32000, 2048)])
 def test_lm_head_argmax_keys(cuda, m, n, k):
     """lm_head with the fused greedy pick: logits, the picked ids (first maximal
     index: every weight row is duplicated, so every logit value occurs at least

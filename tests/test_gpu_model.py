@@ -142,6 +142,26 @@ def test_config5_width_model_batch64_decode(cuda):
     assert np.array_equal(H(run.generate(T(ids), 3, use_graph=True)), ref)
 
 
+@pytest.mark.parametrize("B", [40, 64])
+def test_fused_decode_row_groups(cuda, B):
+    """Above 16 sequences the fused decode stages run 16-token row groups in
+    one launch (blockIdx.y): greedy continuation (eager and chained graphs) and
+    the native step equal the oracle."""
+    from mamba_int import ModelDims, init_random_params, ops
+    from mamba_int.model import IntegerMambaRunner
+    from mamba_int.native import NativeDecoder
+    dims = ModelDims(d_model=256, n_layer=2, vocab_size=700, d_state=16, dt_rank=16)
+    p = init_random_params(dims, 23)
+    ids = np.random.default_rng(B).integers(0, 700, size=(B, 5))
+    ref = O.OracleModel(p).generate(ids, 6)
+    run = IntegerMambaRunner(p)
+    assert run._fused_decode_ok(B)
+    assert np.array_equal(H(run.generate(T(ids), 6, use_graph=False)), ref)
+    assert np.array_equal(H(run.generate(T(ids), 6, use_graph=True)), ref)
+    lg, st = run.prefill(T(ids))
+    assert np.array_equal(H(NativeDecoder(run, B).generate(ops.argmax(lg), st, 6)), ref)
+
+
 def test_native_decode_step_matches_oracle(cuda):
     """mi_decode_step (the whole step behind the C ABI): greedy continuation
     equals the oracle's, its logits equal the runner's decode_step logits, and
