@@ -260,6 +260,14 @@ mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_stats, int s
                                const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
                                int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream);
 
+/* mi_norm_in_proj_conv with BitShiftNormV2's threshold table (spec rule
+ * 7.1): the first decode stage of the multi-head SSD block
+ * (MambaIntegerBlockV2.forward, ssd_multihead.py:523-536). */
+mi_status mi_norm_v2_in_proj_conv(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                  const int16_t *gamma, const uint8_t *w_in, int s_in,
+                                  const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
+                                  int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream);
+
 /* dt_proj (DECAY_MOD, shift s_dt) + decay + dt + one scan step + y + gate +
  * requant (spec rules 4.6-4.11 at L = 1): xp int8 [m,xp_stride] (dt_raw at
  * [0,dt_rank), B, C after it); w_dt packed [d_inner, dt_rank/4]; xs int8
@@ -369,7 +377,7 @@ mi_status mi_decode_workspace_size(const mi_model_params *params, int m, size_t 
 /* One greedy decode step of the whole model for m sequences (the reference's
  * generation step, scripts/inference.py:147-161 over MambaIntegerModel.forward,
  * mamba_integer_model.py:486-495, with recurrent state; the dyadic block runs
- * the three fused stages per layer, the SSD block six kernels): ids int64 [m] in,
+ * the three fused stages per layer, the SSD block four): ids int64 [m] in,
  * next_ids int64 [m] out (first maximal logit), logits int32 [m][ld_logits]
  * when non-NULL; conv_state / h_state are HOST arrays of n_layer device
  * pointers (int8 [m][3][d_inner], int32 [m][d_inner][d_state]) updated in

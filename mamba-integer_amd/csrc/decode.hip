@@ -51,7 +51,14 @@ struct NormGemvArgs {
     // greedy-pick partials of the wide INT32 kernel (optional): keys[m][block]
     // = largest (logit << 32 | 0x7FFFFFFF - index) over the block's outputs
     int64_t *keys;
+    // BitShiftNormV2's threshold table (the multi-head SSD block) instead of
+    // MambaIntegerBlock's
+    bool norm_v2;
 };
+
+__device__ __forceinline__ int norm_shift_args(const NormGemvArgs &g, int64_t s1, int64_t s2, int64_t *mu) {
+    return g.norm_v2 ? norm_shift_tab<6, 2>(s1, s2, g.K, mu) : norm_shift_tab<8, 3>(s1, s2, g.K, mu);
+}
 
 __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -174,7 +181,7 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, con
         int64_t s1, s2;
         sum_stat_parts(g, mr, sp, s1, s2);
         int64_t mu64;
-        const int sh = norm_shift(s1, s2, g.K, &mu64);
+        const int sh = norm_shift_args(g, s1, s2, &mu64);
         const int32_t mu = (int32_t)mu64;
         const int64_t rnd = (int64_t)1 << (sh - 1);
         const int ngrp = (K4 + TPR - 1) / TPR;
@@ -215,7 +222,7 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, con
         t1 = wave_sum64(t1);
         t2 = wave_sum64(t2);
         int64_t mu;
-        const int sh = norm_shift(t1, t2, g.K, &mu);
+        const int sh = norm_shift_args(g, t1, t2, &mu);
         for (int i = 4 * lane; i < g.K; i += 256) {
             const int4 v = *reinterpret_cast<const int4 *>(row + i);
             const int vv[4] = {v.x, v.y, v.z, v.w};
@@ -855,8 +862,8 @@ extern "C" mi_status mi_norm_bitlinear_argmax(const int32_t *r, const int64_t *r
 
 namespace mi {
 namespace {
-mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t *row_stats, int stats_parts,
-                                 const int16_t *gamma, const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
+mi_status norm_in_proj_conv_impl(const char *fn, bool norm_v2, const int32_t *r, const int64_t *row_stats,
+                                 int stats_parts, const int16_t *gamma, const uint8_t *w_in, int s_in, const int8_t *conv_w, const int32_t *conv_b,
                                  int8_t *conv_state, int8_t *xs, int8_t *xz, const uint8_t *w_x, int nx,
                                  int32_t *xpart, int m, int d_model, int d_inner, void *stream) {
     clear_error();
@@ -882,7 +889,7 @@ mi_status norm_in_proj_conv_impl(const char *fn, const int32_t *r, const int64_t
     g.ldo = 2 * (int64_t)d_inner;
     g.M = m; g.N = 2 * d_inner; g.K = d_model; g.kw = d_model / 16; g.shift = s_in;
     g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs; g.conv_d = d_inner;
-    g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.nx = nx; g.xpart = xpart;
+    g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.nx = nx; g.xpart = xpart; g.norm_v2 = norm_v2;
     hipLaunchKernelGGL((norm_gemv_kernel<MI_OUT_INT8, true, false>),
                        dim3((unsigned)(2 * d_inner / 16), (unsigned)((m + kMaxRows - 1) / kMaxRows)), dim3(256),
                        norm_gemv_lds(d_model), as_stream(stream), g);
@@ -895,8 +902,16 @@ extern "C" mi_status mi_norm_in_proj_conv(const int32_t *r, const int64_t *row_s
                                           const int16_t *gamma, const uint8_t *w_in, int s_in,
                                           const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
                                           int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream) {
-    return norm_in_proj_conv_impl("mi_norm_in_proj_conv", r, row_stats, stats_parts, gamma, w_in, s_in, conv_w,
-                                  conv_b, conv_state, xs, xz, nullptr, 0, nullptr, m, d_model, d_inner, stream);
+    return norm_in_proj_conv_impl("mi_norm_in_proj_conv", false, r, row_stats, stats_parts, gamma, w_in, s_in,
+                                  conv_w, conv_b, conv_state, xs, xz, nullptr, 0, nullptr, m, d_model, d_inner, stream);
+}
+
+extern "C" mi_status mi_norm_v2_in_proj_conv(const int32_t *r, const int64_t *row_stats, int stats_parts,
+                                             const int16_t *gamma, const uint8_t *w_in, int s_in,
+                                             const int8_t *conv_w, const int32_t *conv_b, int8_t *conv_state,
+                                             int8_t *xs, int8_t *xz, int m, int d_model, int d_inner, void *stream) {
+    return norm_in_proj_conv_impl("mi_norm_v2_in_proj_conv", true, r, row_stats, stats_parts, gamma, w_in, s_in,
+                                  conv_w, conv_b, conv_state, xs, xz, nullptr, 0, nullptr, m, d_model, d_inner, stream);
 }
 
 extern "C" mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats, int stats_parts,
@@ -909,8 +924,8 @@ extern "C" mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t 
         mi::clear_error();
         return mi::fail(MI_ERR_NULL_POINTER, "mi_norm_in_proj_conv_xpart: xpart is required");
     }
-    return norm_in_proj_conv_impl("mi_norm_in_proj_conv_xpart", r, row_stats, stats_parts, gamma, w_in, s_in, conv_w,
-                                  conv_b, conv_state, xs, xz, w_x, nx, xpart, m, d_model, d_inner, stream);
+    return norm_in_proj_conv_impl("mi_norm_in_proj_conv_xpart", false, r, row_stats, stats_parts, gamma, w_in,
+                                  s_in, conv_w, conv_b, conv_state, xs, xz, w_x, nx, xpart, m, d_model, d_inner, stream);
 }
 
 extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const uint8_t *w_dt, int s_dt,

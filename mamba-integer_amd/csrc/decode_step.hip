@@ -21,7 +21,7 @@ constexpr size_t kAlign = 256;
 size_t up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t r, stats, parts, a, xz, xs, xp, yo, xpart, keys, total;
+    size_t r, stats, parts, xz, xs, xp, yo, xpart, keys, total;
 };
 
 bool ssd(const mi_model_params &p) { return p.block == MI_BLOCK_SSD; }
@@ -42,11 +42,10 @@ WsLayout ws_layout(const mi_model_params &p, int m) {
     w.xz = o; o += up((size_t)m * 2 * D);
     w.xs = o; o += up((size_t)m * D);
     w.yo = o; o += up((size_t)m * D);
+    w.parts = o; o += up((size_t)m * (d / 16) * 2 * 8);
     if (ssd(p)) {
-        w.a = o; o += up((size_t)m * d);
         w.xp = o; o += up((size_t)m * ssd_xp_width(p));
     } else {
-        w.parts = o; o += up((size_t)m * (d / 16) * 2 * 8);
         w.xpart = o; o += up((size_t)m * (D / 16) * (R + 2 * N) * 4);
     }
     w.total = o;
@@ -132,28 +131,24 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
     } while (0)
     MI_STEP(mi_embed(ids, p.emb, r, m, d, p.vocab_size, stats, 1, stream));
     if (ssd(p)) {
-        // MambaIntegerBlockV2 (spec section 7) with the per-op entries: norm
-        // (layer 0 from the embedding's statistics, later layers reduce their
-        // rows), in_proj, conv step, x_proj, one scan step, out_proj
-        int8_t *a = reinterpret_cast<int8_t *>(base + w.a);
+        // MambaIntegerBlockV2 (spec section 7) in four kernels per layer: V2
+        // norm + in_proj + conv step (row statistics as for the dyadic block),
+        // x_proj, one block-scan step, out_proj with statistics partials
         int8_t *xp = reinterpret_cast<int8_t *>(base + w.xp);
         const int W = (int)ssd_xp_width(p);
         for (int l = 0; l < p.n_layer; ++l) {
             const mi_layer_params &ly = p.layers[l];
-            MI_STEP(mi_bitshift_norm_v2(r, ly.gamma, a, m, d, l == 0 ? stats : nullptr, stream));
-            MI_STEP(mi_bitlinear_gemv(a, d, ly.w_in, xz, 2 * D, MI_OUT_INT8, m, 2 * D, d, ly.s_in, 0, 0, nullptr,
-                                      0.0f, nullptr, stream));
-            MI_STEP(mi_conv_squareplus(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], conv_state[l], xs, m, 1, D,
-                                       stream));
+            MI_STEP(mi_norm_v2_in_proj_conv(r, l == 0 ? stats : parts, l == 0 ? 1 : P, ly.gamma, ly.w_in, ly.s_in,
+                                            ly.conv_w, ly.conv_b, conv_state[l], xs, xz, m, d, D, stream));
             MI_STEP(mi_bitlinear_gemv(xs, D, ly.w_x, xp, W, MI_OUT_INT8, m, W, D, ly.s_x, 0, 0, nullptr, 0.0f,
                                       nullptr, stream));
             MI_STEP(mi_ssd_block_scan(xs, xp, W, xz, 2 * D, D, ly.decay_tab, p.n_heads, ly.s_y, yo, h_state[l],
                                       h_state[l], m, 1, D, N, stream));
-            MI_STEP(mi_bitlinear_gemv(yo, D, ly.w_out, r, d, MI_OUT_RESIDUAL, m, d, D, 0, ly.res_mult, ly.res_shift,
-                                      nullptr, 0.0f, nullptr, stream));
+            MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
+                                                stream));
         }
-        MI_STEP(mi_norm_bitlinear_argmax(r, nullptr, 1, p.gamma_f, p.w_head, logits, ld_logits, keys, m,
-                                         p.vocab_size, d, stream));
+        MI_STEP(mi_norm_bitlinear_argmax(r, parts, P, p.gamma_f, p.w_head, logits, ld_logits, keys, m, p.vocab_size,
+                                         d, stream));
         MI_STEP(mi_argmax_keys(keys, (p.vocab_size + 63) / 64, next_ids, m, stream));
         return MI_OK;
     }

@@ -43,6 +43,7 @@ SIGNATURES = {
     "mi_argmax_i32": [P, I, P, I, I, P],
     "mi_norm_bitlinear": [P, P, I, P, P, P, I, I, I, I, I, I, P],
     "mi_norm_in_proj_conv": [P, P, I, P, P, I, P, P, P, P, P, I, I, I, P],
+    "mi_norm_v2_in_proj_conv": [P, P, I, P, P, I, P, P, P, P, P, I, I, I, P],
     "mi_dt_scan_step": [P, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
     "mi_xproj_dt_scan_step": [P, P, I, I, P, I, P, I, I, P, I, I, P, P, I, I, I, P],
     "mi_norm_in_proj_conv_xpart": [P, P, I, P, P, I, P, P, P, P, P, P, I, P, I, I, I, P],

@@ -222,8 +222,8 @@ class IntegerMambaRunner:
         d768 fused wins at every B <= 64 (0.69 vs 0.84 at B64), d1024 at B16 but
         not B64, d1536 and d2048 at no batch."""
         d = self.dims.d_model
-        return (not self.dims.ssd and B <= 64 and d <= 1024 and B * d * d <= 64 * 768 * 768 and d % 64 == 0
-                and self.dims.d_state <= 64 and self.dims.dt_rank <= 256)
+        return (B <= 64 and d <= 1024 and B * d * d <= 64 * 768 * 768 and d % 64 == 0 and self.dims.d_state <= 64
+                and self.dims.dt_rank <= 256)
 
     def _layer_decode(self, ly: DeviceLayer, ws: _Workspace, conv_state: torch.Tensor,
                       h_state: torch.Tensor, li: int) -> None:
@@ -233,6 +233,16 @@ class IntegerMambaRunner:
         dims = self.dims
         D, R = dims.d_inner, dims.dt_rank
         stats_in = ws.stats[0] if li == 0 else ws.parts
+        if dims.ssd:
+            # MambaIntegerBlockV2 in four kernels: V2 norm + in_proj + conv step,
+            # x_proj, one block-scan step (unit B/C, head decay, gate), out_proj
+            ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,
+                                  row_stats=stats_in, v2=True)
+            ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
+            ops.ssd_block_scan(ws.xs, ws.xp, ws.xz, D, ly.decay_tab, dims.n_heads, dims.d_state, ly.s_y,
+                               h_in=h_state, h_out=h_state, out=ws.yo, batch=ws.T)
+            ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)
+            return
         if ws.xpart is not None:
             # x_proj partials from the in_proj blocks, summed by the scan step
             ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, conv_state, ws.xs, ws.xz,

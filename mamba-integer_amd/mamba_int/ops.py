@@ -263,18 +263,21 @@ def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor,
 
 
 def norm_in_proj_conv(r, gamma, w_in, s_in: int, conv_w, conv_b, conv_state, xs, xz, row_stats=None,
-                      w_x=None, xpart=None) -> None:
+                      w_x=None, xpart=None, v2: bool = False) -> None:
     """Decode stage: norm + in_proj GEMV + conv step + squareplus (x half -> xs, conv_state
     updated in place), z half -> xz[:, d_inner:].  With w_x and xpart [m, d_inner/16, nx]
-    int32, also the per-16-channel x_proj partials."""
+    int32, also the per-16-channel x_proj partials; v2: BitShiftNormV2's table."""
     _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma"); _req(w_in, torch.uint8, "w_in")
     _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
     _req(conv_state, torch.int8, "conv_state"); _req(xs, torch.int8, "xs"); _req(xz, torch.int8, "xz")
     m, d = r.shape
     D = conv_w.shape[0]
     stats, parts = _stats(row_stats, m)
+    if v2 and xpart is not None:
+        raise ValueError("the V2 norm stage has no x_proj partials")
     if xpart is None:
-        _lib.call("mi_norm_in_proj_conv", _ptr(r), stats, parts, _ptr(gamma), _ptr(w_in), s_in, _ptr(conv_w),
+        _lib.call("mi_norm_v2_in_proj_conv" if v2 else "mi_norm_in_proj_conv", _ptr(r), stats, parts, _ptr(gamma),
+                  _ptr(w_in), s_in, _ptr(conv_w),
                   _ptr(conv_b), _ptr(conv_state), _ptr(xs), _ptr(xz), m, d, D, _stream())
         return
     _req(xpart, torch.int32, "xpart"); _req(w_x, torch.uint8, "w_x")
