@@ -694,9 +694,11 @@ hipError_t launch_gemv_mt(const GemmArgs &g, hipStream_t st) {
 
 template <int KIND>
 hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
-    if (KIND == MI_OUT_RESIDUAL && g.M <= 16 && g.kw % 4 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
+    if (KIND == MI_OUT_RESIDUAL && g.M <= 64 && g.kw % 4 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
         g.lda % 16 == 0) {
-        hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((g.N + 15) / 16)), dim3(512), 0, st, g);
+        // 16-token row groups along y (weight tiles shared through L2)
+        hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((g.N + 15) / 16), (unsigned)((g.M + 15) / 16)),
+                           dim3(512), 0, st, g);
         return hipGetLastError();
     }
     if (g.M > 16 && g.M <= 64 && g.kw % 16 == 0 && aligned(g.w, 16) && aligned(g.a, 16) && g.lda % 16 == 0) {

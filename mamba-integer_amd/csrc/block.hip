@@ -276,8 +276,11 @@ __global__ __launch_bounds__(256) void conv_sqp_kernel(const int8_t *xz, int64_t
     if (tg == 0 && st_out) {
         for (int j = 0; j < 3; ++j) {
             const int t = L - 3 + j;
-            const uint32_t val = t >= 0 ? *reinterpret_cast<const uint32_t *>(xz + ((int64_t)b * L + t) * xz_stride + d)
-                                        : keep_state[3 + t];
+            // keep_state is selected, not indexed: a register array indexed at
+            // run time would be kept in scratch
+            const uint32_t kept = t == -3 ? keep_state[0] : (t == -2 ? keep_state[1] : keep_state[2]);
+            const uint32_t val =
+                t >= 0 ? *reinterpret_cast<const uint32_t *>(xz + ((int64_t)b * L + t) * xz_stride + d) : kept;
             *reinterpret_cast<uint32_t *>(st_out + ((int64_t)b * 3 + j) * D + d) = val;
         }
     }

@@ -102,8 +102,10 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
     // a wave-uniform choice: every lane of the wave can drop the decay clamp
     const bool wave_safe = __all(safe);
 
-    uint4 rx[3][XPER];
-    uint4 rb[BCPER], rc[BCPER];
+    // ext_vector_type registers (a union-typed uint4 array touched through
+    // lambdas is kept in scratch)
+    v4i rx[3][XPER];
+    v4i rb[BCPER], rc[BCPER];
     const int64_t row0 = (int64_t)b * a.L;
     auto prefetch = [&](int t0) {
         for (int j = 0; j < XPER; ++j) {
@@ -111,18 +113,18 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             const int tt = i / X16, c16 = i % X16;
             const bool ok = i < XPIECES && t0 + tt < a.L && p0 + c16 * 16 < a.D;
             const int64_t rr = row0 + t0 + tt;
-            const uint4 zero = make_uint4(0, 0, 0, 0);
-            rx[0][j] = ok ? *reinterpret_cast<const uint4 *>(a.xs + rr * a.x_row + p0 + c16 * 16) : zero;
-            rx[1][j] = ok ? *reinterpret_cast<const uint4 *>(a.dm + rr * a.x_row + p0 + c16 * 16) : zero;
-            rx[2][j] = ok ? *reinterpret_cast<const uint4 *>(a.z + rr * a.z_row + p0 + c16 * 16) : zero;
+            const v4i zero = v4i{0, 0, 0, 0};
+            rx[0][j] = ok ? *reinterpret_cast<const v4i *>(a.xs + rr * a.x_row + p0 + c16 * 16) : zero;
+            rx[1][j] = ok ? *reinterpret_cast<const v4i *>(a.dm + rr * a.x_row + p0 + c16 * 16) : zero;
+            rx[2][j] = ok ? *reinterpret_cast<const v4i *>(a.z + rr * a.z_row + p0 + c16 * 16) : zero;
         }
         for (int j = 0; j < BCPER; ++j) {
             const int i = tid + j * kMThreads;
             const int tt = i / BC16, c16 = i % BC16;
             const bool ok = i < BCPIECES && t0 + tt < a.L;
             const int64_t off = (row0 + t0 + tt) * a.bc_row + c16 * 16;
-            rb[j] = ok ? *reinterpret_cast<const uint4 *>(a.bsrc + off) : make_uint4(0, 0, 0, 0);
-            rc[j] = ok ? *reinterpret_cast<const uint4 *>(a.csrc + off) : make_uint4(0, 0, 0, 0);
+            rb[j] = ok ? *reinterpret_cast<const v4i *>(a.bsrc + off) : v4i{0, 0, 0, 0};
+            rc[j] = ok ? *reinterpret_cast<const v4i *>(a.csrc + off) : v4i{0, 0, 0, 0};
         }
     };
     auto stash = [&]() {
@@ -130,9 +132,12 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             const int i = tid + j * kMThreads;
             if (i >= XPIECES) break;
             const int tt = i / X16, c16 = i % X16;
-            const uint32_t wx[4] = {rx[0][j].x, rx[0][j].y, rx[0][j].z, rx[0][j].w};
-            const uint32_t wd[4] = {rx[1][j].x, rx[1][j].y, rx[1][j].z, rx[1][j].w};
-            const uint32_t wz[4] = {rx[2][j].x, rx[2][j].y, rx[2][j].z, rx[2][j].w};
+            const uint32_t wx[4] = {(uint32_t)rx[0][j][0], (uint32_t)rx[0][j][1], (uint32_t)rx[0][j][2],
+                                    (uint32_t)rx[0][j][3]};
+            const uint32_t wd[4] = {(uint32_t)rx[1][j][0], (uint32_t)rx[1][j][1], (uint32_t)rx[1][j][2],
+                                    (uint32_t)rx[1][j][3]};
+            const uint32_t wz[4] = {(uint32_t)rx[2][j][0], (uint32_t)rx[2][j][1], (uint32_t)rx[2][j][2],
+                                    (uint32_t)rx[2][j][3]};
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int dmv = clamp32(sb(wd[e >> 2], e & 3), -20, 20);
@@ -145,8 +150,8 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             const int i = tid + j * kMThreads;
             if (i >= BCPIECES) break;
             const int tt = i / BC16, c16 = i % BC16;
-            const uint32_t wb[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};
-            const uint32_t wc[4] = {rc[j].x, rc[j].y, rc[j].z, rc[j].w};
+            const uint32_t wb[4] = {(uint32_t)rb[j][0], (uint32_t)rb[j][1], (uint32_t)rb[j][2], (uint32_t)rb[j][3]};
+            const uint32_t wc[4] = {(uint32_t)rc[j][0], (uint32_t)rc[j][1], (uint32_t)rc[j][2], (uint32_t)rc[j][3]};
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 s_b[tt][c16 * 16 + e] = sb(wb[e >> 2], e & 3);

@@ -439,15 +439,16 @@ class IntegerMambaRunner:
         """embed -> layers -> head -> argmax for one token per sequence (graph body)."""
         B = tok.shape[0]
         fused = self._fused_decode_ok(B)
-        # the fused layers hand row statistics on as out_proj partials; the others
-        # accumulate them with atomics into the per-layer rows the embed zeroes
-        ops.embed(tok, self.emb, out=ws.r, row_stats=ws.stats[:1] if fused else ws.stats)
+        # the fused layers hand row statistics on as out_proj partials
+        ops.embed(tok, self.emb, out=ws.r, row_stats=ws.stats[:1])
         for i, ly in enumerate(self.layers):
             if fused:
                 self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
             else:
-                self._layer(ly, ws, B, 1, state.conv[i], state.h[i], False, ws.stats[i], ws.stats[i + 1])
-        self._head(ws.r, ws.parts if fused else ws.stats[-1], out=logits)
+                # the batched layers' norms reduce their rows (row statistics by
+                # atomics from the out_proj of 64 rows cost more than they save)
+                self._layer(ly, ws, B, 1, state.conv[i], state.h[i], False, ws.stats[0] if i == 0 else None, None)
+        self._head(ws.r, ws.parts if fused else None, out=logits)
         ops.argmax(logits, out=tok_out)
 
     def _decode_graph(self, B: int, state: DecodeState):
