@@ -106,12 +106,165 @@ __device__ __forceinline__ void flush_row_stat(const GemmArgs &g, RowStat st, in
 constexpr int kBM = 128, kBN = 128, kBK = 128;
 constexpr int kApitch = kBK + 16;       // bytes per staged activation row (bank-conflict free b128 reads)
 constexpr int kWpitch = kBK / 16 + 4;   // words per staged weight row (conflict free b32 reads)
+constexpr int kA2pitch = kBK + 32;      // activation row pitch of gemm_kernel (160 B)
+constexpr int kOpitch = 144;            // int8 output tile pitch in LDS (conflict-free dword writes)
 
-// Three blocks (12 waves) per CU: 768 blocks of the 4096 x 3072 x 768 problem
-// then run in one round and each block's global-load latency hides behind the
-// other two blocks' MFMA work.
+// gemm_kernel: 128(n) x 128(m) block tile, 4 waves stacked along n (each 32
+// weight rows x all 128 tokens, so every unpacked weight fragment feeds 8
+// MFMAs), K staged 128 at a time, double buffered, one barrier per stage.
+// Loads are branch-free: token and weight rows are clamped to the last valid
+// row (their products only reach outputs that are never stored) and the
+// weight words of a K tail beyond k are zeroed when staged.  Each thread
+// fetches 4 x 16 activation bytes and one 16-byte run of 4 weight words per
+// stage.  158 VGPRs: three blocks per CU (the waves-per-EU hint of 2 leaves the
+// scheduler room and measured faster than 3 at the same occupancy).
+//
+// LDSOUT (int8 and decay-mod outputs with 16-byte aligned rows): the
+// requantised tile goes through LDS and leaves as whole 128-byte row segments
+// in 16-byte stores, instead of one dword per lane.
+struct GemmStage {
+    v4i a0, a1, a2, a3;
+    v4i w;
+    int wmask;   // 0 for the weight words of a K tail beyond k
+};
+
+template <int KIND, bool LDSOUT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs g) {
+    __shared__ __align__(16) int8_t sA[2][kBM * kA2pitch];
+    __shared__ __align__(16) uint32_t sW[2][kBN * kWpitch];
+    static_assert(kBM * kOpitch <= kBM * kA2pitch, "output tile must fit one activation buffer");
+    static_assert(kBK == 128, "the stage loop below is written for two 64-deep halves");
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wn = wave_id();
+    const int l16 = lane & 15, lq = lane >> 4;
+
+    // blockIdx.x walks m-tiles fastest so the blocks that share a weight tile run together
+    const int mtiles = (g.M + kBM - 1) / kBM;
+    const int m0 = (blockIdx.x % mtiles) * kBM;
+    const int n0 = (blockIdx.x / mtiles) * kBN;
+    const int nk = (g.K + kBK - 1) / kBK;
+
+    const int arow = tid >> 3, ac16 = tid & 7;   // activation rows arow + 32j, 16 bytes at k = 16 * ac16
+    const int wrow = tid >> 1, wh = tid & 1;     // weight row wrow, words 4 * wh .. 4 * wh + 3
+    const int8_t *pa[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = min(m0 + arow + 32 * j, g.M - 1);
+        pa[j] = g.a + (int64_t)m * g.lda + ac16 * 16;
+    }
+    const uint32_t *pw = g.w + (int64_t)min(n0 + wrow, g.N - 1) * g.kw + wh * 4;
+
+    GemmStage S;
+    auto load = [&](int kt) {
+        const int off = kt * kBK + ac16 * 16 < g.K ? kt * kBK : 0;
+        S.a0 = *reinterpret_cast<const v4i *>(pa[0] + off);
+        S.a1 = *reinterpret_cast<const v4i *>(pa[1] + off);
+        S.a2 = *reinterpret_cast<const v4i *>(pa[2] + off);
+        S.a3 = *reinterpret_cast<const v4i *>(pa[3] + off);
+        const bool wok = kt * (kBK / 16) + wh * 4 < g.kw;
+        S.w = *reinterpret_cast<const v4i *>(pw + (wok ? kt * (kBK / 16) : 0));
+        S.wmask = wok ? -1 : 0;
+    };
+    auto store_stage = [&](int buf) {
+        *reinterpret_cast<v4i *>(&sA[buf][(arow + 0) * kA2pitch + ac16 * 16]) = S.a0;
+        *reinterpret_cast<v4i *>(&sA[buf][(arow + 32) * kA2pitch + ac16 * 16]) = S.a1;
+        *reinterpret_cast<v4i *>(&sA[buf][(arow + 64) * kA2pitch + ac16 * 16]) = S.a2;
+        *reinterpret_cast<v4i *>(&sA[buf][(arow + 96) * kA2pitch + ac16 * 16]) = S.a3;
+        *reinterpret_cast<v4i *>(&sW[buf][wrow * kWpitch + wh * 4]) = S.w & S.wmask;
+    };
+
+    v4i acc[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    load(0);
+    store_stage(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load(kt + 1);
+        {
+            // the two 64-deep halves of the stage: all four weight words and the
+            // first half's activation fragments up front; each fragment of the
+            // second half is read into the register its first-half twin frees
+            const uint32_t *wr = &sW[buf][(wn * 32 + l16) * kWpitch + lq];
+            const uint32_t w00 = wr[0], w01 = wr[16 * kWpitch], w10 = wr[4], w11 = wr[16 * kWpitch + 4];
+            const int8_t *ar = &sA[buf][l16 * kA2pitch + lq * 16];
+            v4i fa[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) fa[j] = *reinterpret_cast<const v4i *>(ar + j * 16 * kA2pitch);
+            const v4i f0 = unpack16(w00), f1 = unpack16(w01);
+            const v4i h0 = unpack16(w10), h1 = unpack16(w11);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc[0][j] = mfma_i8(f0, fa[j], acc[0][j]);
+                acc[1][j] = mfma_i8(f1, fa[j], acc[1][j]);
+                fa[j] = *reinterpret_cast<const v4i *>(ar + j * 16 * kA2pitch + 64);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc[0][j] = mfma_i8(h0, fa[j], acc[0][j]);
+                acc[1][j] = mfma_i8(h1, fa[j], acc[1][j]);
+            }
+        }
+        if (kt + 1 < nk) store_stage(buf ^ 1);
+        __syncthreads();   // after the last stage: every wave is done reading sA / sW
+    }
+
+    if constexpr (LDSOUT) {
+        int8_t *sO = &sA[0][0];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int q = rshr32(acc[i][j][r], g.shift);
+                    const int v = KIND == MI_OUT_INT8 ? clamp32(q, -127, 127) : clamp32(q, -20, 20);
+                    pk |= (uint32_t)(v & 255) << (8 * r);
+                }
+                *reinterpret_cast<uint32_t *>(&sO[(j * 16 + l16) * kOpitch + wn * 32 + i * 16 + 4 * lq]) = pk;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int row = arow + 32 * p;
+            const int gm = m0 + row, gn = n0 + ac16 * 16;
+            const v4i v = *reinterpret_cast<const v4i *>(&sO[row * kOpitch + ac16 * 16]);
+            if (gm < g.M && gn < g.N) {
+                int8_t *o = (int8_t *)g.out + (int64_t)gm * g.ldo + gn;
+                if (gn + 16 <= g.N) {
+                    *reinterpret_cast<v4i *>(o) = v;
+                } else {
+                    for (int e = 0; e < 16 && gn + e < g.N; ++e) o[e] = (int8_t)(v[e >> 2] >> (8 * (e & 3)));
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int m = m0 + j * 16 + l16;
+            RowStat st{0, 0};
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const RowStat e = store4<KIND>(g, m, n0 + wn * 32 + i * 16 + 4 * lq, acc[i][j]);
+                st.s1 += e.s1;
+                st.s2 += e.s2;
+            }
+            if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
+        }
+    }
+}
+
+// gemm_any_kernel: any k % 16 == 0 and 4-byte aligned weights (e.g. dt_proj
+// with k = dt_rank): 4 waves of 64x64, weights fetched one word per thread.
 template <int KIND>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemm_any_kernel(GemmArgs g) {
     __shared__ __align__(16) int8_t sA[2][kBM * kApitch];
     __shared__ __align__(16) uint32_t sW[2][kBN * kWpitch];
 
@@ -121,7 +274,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
     const int wn = wave >> 1, wm = wave & 1;
     const int l16 = lane & 15, lq = lane >> 4;
 
-    // blockIdx.x walks m-tiles fastest so the blocks that share a weight tile run together
     const int mtiles = (g.M + kBM - 1) / kBM;
     const int m0 = (blockIdx.x % mtiles) * kBM;
     const int n0 = (blockIdx.x / mtiles) * kBN;
@@ -197,131 +349,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
             st.s2 += e.s2;
         }
         if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
-    }
-}
-
-// ------------------------------------------------ prefill GEMM, 32x32 MFMA
-// v_mfma_i32_32x32x32_i8 sustains more of the int8 rate than the 16x16x64
-// form.  Operands: lane l holds 16 consecutive k (group l/32) of row l%32 in
-// both A (weights) and B (tokens); result register r of lane l is
-// (n = 8*(r/4) + 4*(l/32) + r%4, m = l%32), so registers 4q..4q+3 are four
-// consecutive features of one token.  Block tile 128(n) x 128(m), 4 waves of
-// 64x64 (2x2 MFMAs per 32-wide k step), K staged 128 at a time, packed
-// weights kept packed in LDS (pitch 10 words: conflict-free b32 reads by 32
-// rows x 2 k-groups).
-typedef int v16i __attribute__((ext_vector_type(16)));
-constexpr int kW32pitch = kBK / 16 + 2;
-
-__device__ __forceinline__ void flush_row_stat32(const GemmArgs &g, RowStat st, int m, int lh) {
-    st.s1 += __shfl_xor(st.s1, 32);
-    st.s2 += __shfl_xor(st.s2, 32);
-    if (lh == 0 && m < g.M) {
-        atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m), (unsigned long long)st.s1);
-        atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m + 1), (unsigned long long)st.s2);
-    }
-}
-
-template <int KIND>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemm32_kernel(GemmArgs g) {
-    __shared__ __align__(16) int8_t sA[2][kBM * kApitch];
-    __shared__ __align__(16) uint32_t sW[2][kBN * kW32pitch];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = wave_id();
-    const int wn = wave >> 1, wm = wave & 1;
-    const int l32 = lane & 31, lh = lane >> 5;
-
-    const int mtiles = (g.M + kBM - 1) / kBM;
-    const int m0 = (blockIdx.x % mtiles) * kBM;
-    const int n0 = (blockIdx.x / mtiles) * kBN;
-
-    uint4 ra[4];
-    uint32_t rw[4];
-    auto load_stage = [&](int k0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            const int row = i >> 3, c16 = i & 7;
-            const int m = m0 + row, k = k0 + c16 * 16;
-            ra[j] = (m < g.M && k < g.K) ? *reinterpret_cast<const uint4 *>(g.a + (int64_t)m * g.lda + k)
-                                         : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            const int row = i >> 3, c = i & 7;
-            const int n = n0 + row, kw = (k0 >> 4) + c;
-            rw[j] = (n < g.N && kw < g.kw) ? g.w[(int64_t)n * g.kw + kw] : 0u;
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            const int row = i >> 3, c16 = i & 7;
-            *reinterpret_cast<uint4 *>(&sA[buf][row * kApitch + c16 * 16]) = ra[j];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = tid + 256 * j;
-            const int row = i >> 3, c = i & 7;
-            sW[buf][row * kW32pitch + c] = rw[j];
-        }
-    };
-
-    v16i acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-    const int nk = (g.K + kBK - 1) / kBK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
-#pragma unroll
-        for (int ks = 0; ks < kBK / 32; ++ks) {
-            v4i fw[2], fa[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wn * 64 + i * 32 + l32;
-                fw[i] = unpack16(sW[buf][row * kW32pitch + ks * 2 + lh]);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = wm * 64 + j * 32 + l32;
-                fa[j] = *reinterpret_cast<const v4i *>(&sA[buf][row * kApitch + ks * 32 + lh * 16]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[i], fa[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) store_stage(buf ^ 1);
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int m = m0 + wm * 64 + j * 32 + l32;
-        RowStat st{0, 0};
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const v4i v = v4i{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                const RowStat e = store4<KIND>(g, m, n0 + wn * 64 + i * 32 + 8 * q + 4 * lh, v);
-                st.s1 += e.s1;
-                st.s2 += e.s2;
-            }
-        if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat32(g, st, m, lh);
     }
 }
 
@@ -661,13 +688,17 @@ GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ld
 
 template <int KIND>
 hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
-    const int blocks = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);
-    // the 16x16x64 kernel is the faster one on every measured shape (config 2
-    // and the config-3 prefill projections); MI_GEMM32=1 selects the other
-    if (getenv("MI_GEMM32"))
-        hipLaunchKernelGGL(gemm32_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
+    const dim3 grid((unsigned)(((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN)));
+    // gemm_kernel reads each weight row as 16-byte runs of 4 words
+    if (g.kw % 4 != 0 || !aligned(g.w, 16)) {
+        hipLaunchKernelGGL(gemm_any_kernel<KIND>, grid, dim3(256), 0, st, g);
+        return hipGetLastError();
+    }
+    constexpr bool kInt8Out = KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD;
+    if (kInt8Out && g.ldo % 16 == 0 && aligned(g.out, 16))
+        hipLaunchKernelGGL((gemm_kernel<KIND, kInt8Out>), grid, dim3(256), 0, st, g);
     else
-        hipLaunchKernelGGL(gemm_kernel<KIND>, dim3(blocks), dim3(256), 0, st, g);
+        hipLaunchKernelGGL((gemm_kernel<KIND, false>), grid, dim3(256), 0, st, g);
     return hipGetLastError();
 }
 

@@ -90,6 +90,38 @@ def test_bitlinear_kinds(cuda, M, N, K):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K", [(200, 200, 192), (130, 36, 64), (257, 129, 320)])
+@pytest.mark.parametrize("pad", [0, 4, 16])
+def test_gemm_tile_edges(cuda, M, N, K, pad):
+    """Prefill GEMM edge tiles: a K tail of 64 past the last 128-deep stage, ragged
+    M and N (the int8 tile store's 16-byte runs cut short), output row pitches that
+    select the staged 16-byte store (pitch % 16 == 0) or the per-lane dword
+    store, and the RESIDUAL row statistics."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(M * 3 + N + K + pad)
+    a = i8(rng, M, K)
+    wp = pack_ternary(_tern(rng, N, K))
+    ldo = (N + 15) // 16 * 16 + pad
+    for kind, shift in ((O.OUT_INT8, 3), (O.OUT_DECAY_MOD, 6)):
+        out = T(np.full((M, ldo), 99, np.int8))
+        got = H(ops.bitlinear(T(a), T(wp), kind, N, shift=shift, out=out, path="gemm"))
+        assert np.array_equal(got[:, :N], O.bitlinear(a, wp, kind, shift)), kind
+        assert (got[:, N:] == 99).all(), "stored past n"
+    r0 = rng.integers(-(2**22), 2**22, size=(M, N), dtype=np.int32)
+    rp = np.zeros((M, ldo), np.int32)
+    rp[:, :N] = r0
+    rt = T(rp)
+    st = torch.zeros((M, 2), dtype=torch.int64, device="cuda")
+    ops.bitlinear(T(a), T(wp), ops.OUT_RESIDUAL, N, out=rt, res_mult=-3001, res_shift=11, path="gemm", row_stats=st)
+    ref = O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0, res_mult=-3001, res_shift=11)
+    assert np.array_equal(H(rt)[:, :N], ref)
+    r64 = ref.astype(np.int64)
+    assert np.array_equal(H(st), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+    acc = H(ops.bitlinear(T(a), T(wp), ops.OUT_INT32, N, out=T(np.zeros((M, ldo), np.int32)), path="gemm"))
+    assert np.array_equal(acc[:, :N], O.bitlinear(a, wp, O.OUT_INT32))
+
+
 def test_act_quant_and_bitlinear_float_face(cuda):
     """Drop-in BitLinear: GPU output bit-identical to the reference's CPU formula
     (rational_bitnet.py:63-111,167-213 evaluated with torch on the CPU)."""
