@@ -301,6 +301,19 @@ mi_status mi_norm_in_proj_conv_xpart(const int32_t *r, const int64_t *row_stats,
                                      int8_t *conv_state, int8_t *xs, int8_t *xz, const uint8_t *w_x, int nx,
                                      int32_t *xpart, int m, int d_model, int d_inner, void *stream);
 
+/* The decode conv step followed by x_proj, for widths where the in_proj
+ * stage does not carry the conv (conv1d_step.cu:12-58, then self.x_proj,
+ * mamba_integer_model.py:378-379,404-414): one token per sequence, the x half
+ * of xz int8 [m, xz_stride] (columns 0..d_inner-1) through the depthwise conv
+ * step + squareplus with conv_state int8 [m,3,d_inner] shifted in place ->
+ * xs int8 [m,d_inner], then xp int8 [m, xp_stride] = sat8(rshr(xs @ w_x^T,
+ * s_x)) for w_x packed [nx, d_inner/4], nx <= 256.  w_x, conv_w int8
+ * [d_inner,4] and conv_b int32 [d_inner] 16-byte aligned.  One block per
+ * token; d_inner a multiple of 256, <= 8192.  The row feeds mi_dt_scan_step. */
+mi_status mi_conv_step_xproj(const int8_t *xz, int xz_stride, const int8_t *conv_w, const int32_t *conv_b,
+                             int8_t *conv_state, int8_t *xs, const uint8_t *w_x, int s_x, int nx, int8_t *xp,
+                             int xp_stride, int m, int d_inner, void *stream);
+
 /* mi_dt_scan_step with x_proj finished from those partials:
  * xp[i, n] = sat8(rshr(sum over b < nblk of xpart[i, b, n], s_x)), then
  * dt_rank, B and C as in mi_dt_scan_step.  nblk = d_inner/16 for the

@@ -1030,3 +1030,149 @@ extern "C" mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x,
     else launch_xproj_scan<0>(ntiles, grid, hs, g);
     return check_launch("mi_xproj_dt_scan_step");
 }
+
+// ------------------------------------------------ conv step + x_proj
+// Decode (one token per sequence) for widths where the in_proj stage does not
+// carry the conv: one block of 8 waves per token.  Each thread runs the
+// depthwise conv step + squareplus of 4 channels per pass (conv1d_step.cu:
+// 30-57; the state rows shift in place) and parks xs in LDS.  x_proj then runs
+// on MFMA with the token as column 0 of the B operand: wave w takes the
+// 256-channel slices w, w+8, ... of K for all NT 16-row tiles of the nx
+// outputs, lane group q reading weight words 4q..4q+3 of a slice with one
+// 16-byte load per tile, every tile's load issued before the first MFMA (rows
+// past nx are clamped; their sums are never stored).  The k order inside a
+// slice is permuted alike in both operands.  The waves' sums meet in LDS and
+// the block writes the requantised int8 x_proj row, so the consumer
+// (mi_dt_scan_step) reads nx bytes per token.
+namespace mi {
+namespace {
+
+constexpr int kConvXMaxD = 8192;
+constexpr int kConvXWaves = 8;
+
+struct ConvXArgs {
+    const int8_t *xz;
+    int64_t xz_stride;
+    const int8_t *conv_w;
+    const int32_t *conv_b;
+    int8_t *conv_state;   // [M][3][D]
+    int8_t *xs;           // [M][D]
+    const uint32_t *w_x;  // [nx][D/16] words
+    int8_t *xp;           // [M][xp_stride]
+    int64_t xp_stride;
+    int M, D, nx, s_x;
+};
+
+template <int NT>
+__global__ __launch_bounds__(64 * kConvXWaves) void conv_step_xproj_kernel(ConvXArgs g) {
+    __shared__ __align__(16) int8_t s_xs[kConvXMaxD];
+    __shared__ int32_t s_red[kConvXWaves][16 * NT];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = wave_id();
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int m = blockIdx.x;
+
+    const int8_t *xr = g.xz + (int64_t)m * g.xz_stride;
+    int8_t *st = g.conv_state + (int64_t)m * 3 * g.D;
+    for (int ch = 4 * tid; ch < g.D; ch += 4 * 64 * kConvXWaves) {
+        const uint32_t x = *reinterpret_cast<const uint32_t *>(xr + ch);
+        const uint32_t s0 = *reinterpret_cast<const uint32_t *>(st + ch);
+        const uint32_t s1 = *reinterpret_cast<const uint32_t *>(st + g.D + ch);
+        const uint32_t s2 = *reinterpret_cast<const uint32_t *>(st + 2 * g.D + ch);
+        const v4i cw = *reinterpret_cast<const v4i *>(g.conv_w + (int64_t)ch * 4);
+        const v4i cb = *reinterpret_cast<const v4i *>(g.conv_b + ch);
+        uint32_t o = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t w = (uint32_t)cw[e];
+            const int32_t acc = cb[e] + (int)(int8_t)w * (int)(int8_t)(s0 >> (8 * e)) +
+                                (int)(int8_t)(w >> 8) * (int)(int8_t)(s1 >> (8 * e)) +
+                                (int)(int8_t)(w >> 16) * (int)(int8_t)(s2 >> (8 * e)) +
+                                (int)(int8_t)(w >> 24) * (int)(int8_t)(x >> (8 * e));
+            o |= (uint32_t)(sqp_q(acc) & 255) << (8 * e);
+        }
+        *reinterpret_cast<uint32_t *>(g.xs + (int64_t)m * g.D + ch) = o;
+        *reinterpret_cast<uint32_t *>(st + ch) = s1;
+        *reinterpret_cast<uint32_t *>(st + g.D + ch) = s2;
+        *reinterpret_cast<uint32_t *>(st + 2 * g.D + ch) = x;
+        *reinterpret_cast<uint32_t *>(&s_xs[ch]) = o;
+    }
+    __syncthreads();
+
+    const int xkw = g.D / 16;
+    const int nslice = g.D / 256;
+    const uint32_t *wrow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wrow[t] = g.w_x + (int64_t)min(16 * t + l16, g.nx - 1) * xkw + 4 * lq;
+    v4i acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
+    for (int sl = wave; sl < nslice; sl += kConvXWaves) {
+        v4i wv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wv[t] = *reinterpret_cast<const v4i *>(wrow[t] + 16 * sl);
+        const int w0 = 16 * sl + 4 * lq;   // this lane group's 4 words of the slice
+        v4i fb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            fb[j] = l16 == 0 ? *reinterpret_cast<const v4i *>(&s_xs[16 * (w0 + j)]) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t] = mfma_i8(unpack16((uint32_t)wv[t][j]), fb[j], acc[t]);
+    }
+    // lanes of token column 0 (l16 == 0) hold outputs 16t + 4lq + r
+    if (l16 == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) *reinterpret_cast<v4i *>(&s_red[wave][16 * t + 4 * lq]) = acc[t];
+    }
+    __syncthreads();
+    const int used = min(kConvXWaves, nslice);
+    for (int n = tid; n < g.nx; n += 64 * kConvXWaves) {
+        int v = 0;
+        for (int w = 0; w < used; ++w) v += s_red[w][n];
+        g.xp[(int64_t)m * g.xp_stride + n] = (int8_t)clamp32(rshr32(v, g.s_x), -127, 127);
+    }
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" mi_status mi_conv_step_xproj(const int8_t *xz, int xz_stride, const int8_t *conv_w,
+                                        const int32_t *conv_b, int8_t *conv_state, int8_t *xs,
+                                        const uint8_t *w_x, int s_x, int nx, int8_t *xp, int xp_stride, int m,
+                                        int d_inner, void *stream) {
+    using namespace mi;
+    clear_error();
+    MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_conv_step_xproj: negative size");
+    MI_REQUIRE(d_inner % 256 == 0 && d_inner <= kConvXMaxD, MI_ERR_BAD_DIM,
+               "mi_conv_step_xproj: d_inner=%d must be a multiple of 256 and <= %d", d_inner, kConvXMaxD);
+    MI_REQUIRE(nx >= 1 && nx <= 16 * kMaxXTiles, MI_ERR_BAD_DIM, "mi_conv_step_xproj: nx=%d outside [1,%d]", nx,
+               16 * kMaxXTiles);
+    MI_REQUIRE(xz_stride >= d_inner && xz_stride % 4 == 0 && xp_stride >= nx, MI_ERR_BAD_DIM,
+               "mi_conv_step_xproj: xz_stride=%d (>= d_inner, multiple of 4) or xp_stride=%d (>= nx) too small",
+               xz_stride, xp_stride);
+    MI_REQUIRE(s_x >= 0 && s_x <= 30, MI_ERR_BAD_ARG, "mi_conv_step_xproj: s_x=%d outside [0,30]", s_x);
+    if ((int64_t)m * d_inner == 0) return MI_OK;
+    MI_REQUIRE(xz && conv_w && conv_b && conv_state && xs && w_x && xp, MI_ERR_NULL_POINTER,
+               "mi_conv_step_xproj: a required pointer is NULL");
+    MI_REQUIRE(aligned(xz, 4) && aligned(conv_w, 16) && aligned(conv_b, 16) && aligned(conv_state, 4) &&
+                   aligned(xs, 4) && aligned(w_x, 16),
+               MI_ERR_BAD_ALIGNMENT,
+               "mi_conv_step_xproj: xz, conv_state, xs 4-byte, conv_w, conv_b, w_x 16-byte aligned");
+    ConvXArgs g{};
+    g.xz = xz; g.xz_stride = xz_stride; g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs;
+    g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.xp = xp; g.xp_stride = xp_stride;
+    g.M = m; g.D = d_inner; g.nx = nx; g.s_x = s_x;
+    const dim3 grid((unsigned)m), block(64 * kConvXWaves);
+    const int nt = (nx + 15) / 16;
+    if (nt <= 2) hipLaunchKernelGGL(conv_step_xproj_kernel<2>, grid, block, 0, as_stream(stream), g);
+    else if (nt <= 4) hipLaunchKernelGGL(conv_step_xproj_kernel<4>, grid, block, 0, as_stream(stream), g);
+    else if (nt <= 6) hipLaunchKernelGGL(conv_step_xproj_kernel<6>, grid, block, 0, as_stream(stream), g);
+    else if (nt <= 8) hipLaunchKernelGGL(conv_step_xproj_kernel<8>, grid, block, 0, as_stream(stream), g);
+    else if (nt <= 10) hipLaunchKernelGGL(conv_step_xproj_kernel<10>, grid, block, 0, as_stream(stream), g);
+    else if (nt <= 12) hipLaunchKernelGGL(conv_step_xproj_kernel<12>, grid, block, 0, as_stream(stream), g);
+    else hipLaunchKernelGGL(conv_step_xproj_kernel<16>, grid, block, 0, as_stream(stream), g);
+    return check_launch("mi_conv_step_xproj");
+}

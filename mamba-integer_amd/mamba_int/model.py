@@ -174,10 +174,20 @@ class IntegerMambaRunner:
             return
         ops.bitshift_norm(ws.r, ly.gamma, out=ws.a, row_stats=stats_in)
         ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
+        step = L == 1 and not fresh
+        if step and self._conv_xproj_ok():
+            # one recurrent step per sequence: conv step + x_proj (one block per token),
+            # then dt_proj + scan step + gate
+            ops.conv_step_xproj(ws.xz, D, ly.conv_w, ly.conv_b, conv_state, ly.w_x, ly.s_x, dims.xp_width,
+                                xs=ws.xs, xp=ws.xp)
+            ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
+            ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                          res_shift=ly.res_shift, row_stats=stats_out)
+            return
         ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
                             state_out=conv_state, out=ws.xs, batch=B)
         ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
-        if L == 1 and not fresh:
+        if step:
             # one recurrent step per sequence (any batch): dt_proj + scan step + gate
             ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
             ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
@@ -214,6 +224,12 @@ class IntegerMambaRunner:
             self.scan_timer[1]()
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
                       res_shift=ly.res_shift, row_stats=stats_out)
+
+    def _conv_xproj_ok(self) -> bool:
+        """mi_conv_step_xproj's limits (d_inner a multiple of 256 up to 8192,
+        x_proj rows <= 256): the batched decode's conv step carries x_proj."""
+        D = self.dims.d_inner
+        return D % 256 == 0 and D <= 8192 and self.dims.xp_width <= 256
 
     def _fused_decode_ok(self, B: int) -> bool:
         """The three fused decode stages pay off while the work every block

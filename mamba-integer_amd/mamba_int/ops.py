@@ -288,6 +288,24 @@ def norm_in_proj_conv(r, gamma, w_in, s_in: int, conv_w, conv_b, conv_state, xs,
               _stream())
 
 
+def conv_step_xproj(xz, d_inner: int, conv_w, conv_b, conv_state, w_x, s_x: int, nx: int, xs=None, xp=None):
+    """Decode stage: conv step + squareplus of the x half of xz (int8 [m, >= d_inner]) with
+    the conv state updated in place -> xs, then x_proj (INT8, shift s_x) -> xp int8 [m, >= nx]."""
+    _req(xz, torch.int8, "xz"); _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
+    _req(conv_state, torch.int8, "conv_state"); _req(w_x, torch.uint8, "w_x")
+    m = xz.shape[0]
+    if xs is None:
+        xs = torch.empty((m, d_inner), dtype=torch.int8, device=xz.device)
+    if xp is None:
+        xp = torch.empty((m, nx), dtype=torch.int8, device=xz.device)
+    _req(xs, torch.int8, "xs"); _req(xp, torch.int8, "xp")
+    if tuple(xs.shape) != (m, d_inner) or xp.shape[0] != m or xp.shape[-1] < nx:
+        raise ValueError(f"xs must be [{m}, {d_inner}] and xp [{m}, >= {nx}]")
+    _lib.call("mi_conv_step_xproj", _ptr(xz), xz.shape[-1], _ptr(conv_w), _ptr(conv_b), _ptr(conv_state), _ptr(xs),
+              _ptr(w_x), s_x, nx, _ptr(xp), xp.shape[-1], m, d_inner, _stream())
+    return xs, xp
+
+
 def xpart_dt_scan_step(xpart, s_x: int, dt_rank: int, w_dt, s_dt: int, xs, z, z_off: int, base,
                        decay_shift: int, s_y: int, h_state, yo) -> None:
     """Decode stage: x_proj from per-block partials + dt_proj + decay + dt + scan step + gate -> yo."""

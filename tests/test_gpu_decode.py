@@ -191,6 +191,49 @@ def test_xpart_decode_chain(cuda, m, d, D, N, R, stats):
     assert np.array_equal(H(hg), h_ref)
 
 
+@pytest.mark.parametrize("m,D,N,R", [(64, 4096, 16, 128), (37, 1024, 16, 48), (5, 256, 8, 16), (20, 768, 10, 16),
+                                     (1, 8192, 64, 128), (3, 4352, 16, 32)])
+def test_conv_step_xproj_chain(cuda, m, D, N, R):
+    """The batched decode's conv step + x_proj (mi_conv_step_xproj, one block per
+    token), then the scan step, equals the unfused oracle chain (conv + squareplus,
+    x_proj, dt_proj, block scan); the conv state shifts in place.  Covers more
+    256-channel slices than waves (D 8192, 4352), x_proj rows not a multiple of 16
+    and a padded xp row."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m + D + N + R)
+    NX = R + 2 * N
+    xz = i8(rng, m, 2 * D, lo=-128)
+    cw = i8(rng, D, 4)
+    cb = rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, m, 3, D)
+    wx = pack_ternary(rng.integers(-1, 2, size=(NX, D), dtype=np.int8))
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    h0 = rng.integers(-(2**22), 2**22, size=(m, D, N), dtype=np.int32)
+    xs_ref, st_ref = O.conv_squareplus(xz.reshape(m, 1, 2 * D), D, cw, cb, st)
+    xs_ref = xs_ref[:, 0]
+    xp_ref = O.bitlinear(xs_ref, wx, O.OUT_INT8, 5)
+    dm = O.bitlinear(np.ascontiguousarray(xp_ref[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs_ref.reshape(m, 1, D), dm.reshape(m, 1, D), xp_ref.reshape(m, 1, NX), R,
+                                 xz.reshape(m, 1, 2 * D), D, base, 15, 13, h_state=h0)
+    stg = T(st)
+    xzg = T(xz)
+    xs = torch.full((m, D), 5, dtype=torch.int8, device="cuda")
+    W = (NX + 15) // 16 * 16
+    xp = torch.full((m, W), 9, dtype=torch.int8, device="cuda")
+    ops.conv_step_xproj(xzg, D, T(cw), T(cb), stg, T(wx), 5, NX, xs=xs, xp=xp)
+    assert np.array_equal(H(xs), xs_ref)
+    assert np.array_equal(H(stg), st_ref)
+    assert np.array_equal(H(xp)[:, :NX], xp_ref)
+    assert (H(xp)[:, NX:] == 9).all()
+    hg = T(h0)
+    yo = T(np.zeros((m, D), np.int8))
+    ops.dt_scan_step(xp, R, T(wdt), 2, xs, xzg, D, T(base), 15, 13, hg, yo)
+    assert np.array_equal(H(yo), yo_ref[:, 0])
+    assert np.array_equal(H(hg), h_ref)
+
+
 @pytest.mark.parametrize("m,n,k", [(8, 768, 1536), (1, 768, 1536), (16, 100, 512), (3, 2048, 4096), (5, 20, 256),
                                    (16, 64, 256 * 13), (4, 96, 1600)])
 def test_decode_residual_gemv(cuda, m, n, k):
