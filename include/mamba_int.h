@@ -164,6 +164,14 @@ mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const uint8_t *w
 mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens,
                            int dim, const int64_t *row_stats, void *stream);
 
+/* mi_bitshift_norm (v2 != 0: mi_bitshift_norm_v2) with the row statistics
+ * given as per-block partials: stats_parts int64 [tokens, nparts, 2] (16-byte
+ * aligned), the (sum, sum of squares) pairs that mi_bitlinear_residual_parts
+ * stores per 16 output features, summed per row here.  dim % 4 == 0, r
+ * 16-byte aligned.  For batches whose norm would otherwise reduce its rows. */
+mi_status mi_bitshift_norm_parts(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
+                                 const int64_t *stats_parts, int nparts, int v2, void *stream);
+
 /* Embedding (mamba_integer_model.py:470,487): r[t,:] = emb[ids[t],:] << 4.
  * ids int64 [tokens] (an id outside [0,vocab) gives a zero row), emb int8
  * [vocab,dim], r int32.  row_stats (nullable, int64

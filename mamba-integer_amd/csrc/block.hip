@@ -223,6 +223,47 @@ __global__ __launch_bounds__(256) void norm_stats_kernel(const int32_t *r, const
     *reinterpret_cast<uint32_t *>(out + t * dim + c) = o;
 }
 
+// BitShiftNorm from per-block row-statistics partials (int64 [tokens][nparts][2],
+// the stores of mi_bitlinear_residual_parts): block (c, t) loads its 1024
+// channels of row t, sums the row's nparts pairs across the block, then
+// normalizes 4 channels per thread.
+template <bool V2>
+__global__ __launch_bounds__(256) void norm_parts_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
+                                                         const int64_t *parts, int nparts, int dim) {
+    __shared__ int64_t red[2][4];
+    const int64_t t = blockIdx.y;
+    const int c = (blockIdx.x * 256 + (int)threadIdx.x) * 4;
+    const bool ok = c < dim;
+    const int4 v = *reinterpret_cast<const int4 *>(r + t * dim + (ok ? c : 0));
+    const v2l *pp = reinterpret_cast<const v2l *>(parts + t * nparts * 2);
+    int64_t s1 = 0, s2 = 0;
+    for (int i = threadIdx.x; i < nparts; i += 256) {
+        const v2l p = pp[i];
+        s1 += p[0];
+        s2 += p[1];
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += __shfl_xor(s1, off);
+        s2 += __shfl_xor(s2, off);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wave] = s1;
+        red[1][wave] = s2;
+    }
+    __syncthreads();
+    s1 = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    s2 = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    if (!ok) return;
+    int64_t mu;
+    const int sh = norm_shift_for<V2>(s1, s2, dim, &mu);
+    const int vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o = 0;
+    for (int q = 0; q < 4; ++q)
+        o |= (uint32_t)((int)clamp64(rshr64((int64_t)(vv[q] - mu) * gamma[c + q], sh), -127, 127) & 255) << (8 * q);
+    *reinterpret_cast<uint32_t *>(out + t * dim + c) = o;
+}
+
 // ----------------------------------------------------- conv + squareplus
 constexpr int kConvTT = 16;  // time steps per thread
 
@@ -380,6 +421,28 @@ extern "C" mi_status mi_bitshift_norm(const int32_t *r, const int16_t *gamma, in
 extern "C" mi_status mi_bitshift_norm_v2(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
                                          const int64_t *row_stats, void *stream) {
     return bitshift_norm_impl<true>("mi_bitshift_norm_v2", r, gamma, out, tokens, dim, row_stats, stream);
+}
+
+extern "C" mi_status mi_bitshift_norm_parts(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens,
+                                            int dim, const int64_t *stats_parts, int nparts, int v2, void *stream) {
+    clear_error();
+    MI_REQUIRE(tokens >= 0, MI_ERR_BAD_DIM, "mi_bitshift_norm_parts: negative tokens");
+    MI_REQUIRE(dim >= 4 && dim % 4 == 0 && dim <= 65536, MI_ERR_BAD_DIM,
+               "mi_bitshift_norm_parts: dim=%d must be a multiple of 4 in [4,65536]", dim);
+    MI_REQUIRE(nparts >= 1, MI_ERR_BAD_ARG, "mi_bitshift_norm_parts: nparts=%d must be >= 1", nparts);
+    if (tokens == 0) return MI_OK;
+    MI_REQUIRE(r && gamma && out && stats_parts, MI_ERR_NULL_POINTER,
+               "mi_bitshift_norm_parts: r, gamma, out and stats_parts are required");
+    MI_REQUIRE(aligned(r, 16) && aligned(out, 4) && aligned(stats_parts, 16), MI_ERR_BAD_ALIGNMENT,
+               "mi_bitshift_norm_parts: r and stats_parts 16-byte, out 4-byte aligned");
+    const dim3 grid((unsigned)((dim + 1023) / 1024), (unsigned)tokens);
+    if (v2)
+        hipLaunchKernelGGL(norm_parts_kernel<true>, grid, dim3(256), 0, as_stream(stream), r, gamma, out, stats_parts,
+                           nparts, dim);
+    else
+        hipLaunchKernelGGL(norm_parts_kernel<false>, grid, dim3(256), 0, as_stream(stream), r, gamma, out,
+                           stats_parts, nparts, dim);
+    return check_launch("mi_bitshift_norm_parts");
 }
 
 extern "C" mi_status mi_embed(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab,

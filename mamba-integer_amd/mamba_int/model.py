@@ -181,8 +181,12 @@ class IntegerMambaRunner:
             ops.conv_step_xproj(ws.xz, D, ly.conv_w, ly.conv_b, conv_state, ly.w_x, ly.s_x, dims.xp_width,
                                 xs=ws.xs, xp=ws.xp)
             ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
-            ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                          res_shift=ly.res_shift, row_stats=stats_out)
+            if self._step_parts(ws):
+                # the next norm sums these per-16-feature statistics partials
+                ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)
+            else:
+                ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
+                              res_shift=ly.res_shift, row_stats=stats_out)
             return
         ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
                             state_out=conv_state, out=ws.xs, batch=B)
@@ -224,6 +228,13 @@ class IntegerMambaRunner:
             self.scan_timer[1]()
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
                       res_shift=ly.res_shift, row_stats=stats_out)
+
+    def _step_parts(self, ws: _Workspace) -> bool:
+        """The batched one-token step (conv step + x_proj kernel) hands the row
+        statistics on as out_proj partials (ws.parts), so the norms that follow
+        are elementwise instead of reducing their rows."""
+        return (self._conv_xproj_ok() and ws.parts is not None and ws.T <= 64
+                and self.dims.d_inner % 64 == 0 and not self.dims.ssd)
 
     def _conv_xproj_ok(self) -> bool:
         """mi_conv_step_xproj's limits (d_inner a multiple of 256 up to 8192,
@@ -286,8 +297,7 @@ class IntegerMambaRunner:
         if stats is not None and m * d <= 8 * 1024 and d <= 3072 and d % 64 == 0:
             return ops.norm_bitlinear(r_rows, self.gamma_f, self.w_head, ops.OUT_INT32, self.dims.vocab_size,
                                       out=out, row_stats=stats)
-        # the standalone norm takes full row sums only (not per-block partials)
-        a = ops.bitshift_norm(r_rows, self.gamma_f, row_stats=stats if stats is not None and stats.dim() == 2 else None)
+        a = ops.bitshift_norm(r_rows, self.gamma_f, row_stats=stats)
         V = self.dims.vocab_size
         if out is not None or V % 4 == 0:
             return ops.bitlinear(a, self.w_head, ops.OUT_INT32, V, out=out)
@@ -301,14 +311,17 @@ class IntegerMambaRunner:
         ws = self._workspace(B * L)
         ops.embed(ids.reshape(-1).contiguous(), self.emb, out=ws.r, row_stats=ws.stats[:1])
         decode = L == 1 and not fresh and self._fused_decode_ok(B)
-        self._head_stats = ws.parts if decode else None
+        parts = L == 1 and not fresh and not decode and self._step_parts(ws)
+        self._head_stats = ws.parts if decode or parts else None
         for i, ly in enumerate(self.layers):
             if decode:
                 self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
             else:
                 # prefill: the norm of layer 0 uses the embedding's row statistics; later
-                # norms reduce their rows (atomics over 16k-row tiles cost more than they save)
-                self._layer(ly, ws, B, L, state.conv[i], state.h[i], fresh, ws.stats[0] if i == 0 else None, None)
+                # norms reduce their rows (atomics over 16k-row tiles cost more than they
+                # save) or, after a batched one-token step, sum the out_proj's partials
+                self._layer(ly, ws, B, L, state.conv[i], state.h[i], fresh,
+                            ws.stats[0] if i == 0 else (ws.parts if parts else None), None)
         return ws
 
     # ------------------------------------------------------------ public API
@@ -463,14 +476,16 @@ class IntegerMambaRunner:
         fused = self._fused_decode_ok(B)
         # the fused layers hand row statistics on as out_proj partials
         ops.embed(tok, self.emb, out=ws.r, row_stats=ws.stats[:1])
+        parts = not fused and self._step_parts(ws)
         for i, ly in enumerate(self.layers):
             if fused:
                 self._layer_decode(ly, ws, state.conv[i], state.h[i], i)
             else:
-                # the batched layers' norms reduce their rows (row statistics by
-                # atomics from the out_proj of 64 rows cost more than they save)
-                self._layer(ly, ws, B, 1, state.conv[i], state.h[i], False, ws.stats[0] if i == 0 else None, None)
-        self._head(ws.r, ws.parts if fused else None, out=logits)
+                # the batched layers' norms sum the previous out_proj's statistics
+                # partials, or reduce their rows where the step cannot store them
+                self._layer(ly, ws, B, 1, state.conv[i], state.h[i], False,
+                            ws.stats[0] if i == 0 else (ws.parts if parts else None), None)
+        self._head(ws.r, ws.parts if fused or parts else None, out=logits)
         ops.argmax(logits, out=tok_out)
 
     def _decode_graph(self, B: int, state: DecodeState):

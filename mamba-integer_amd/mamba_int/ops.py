@@ -144,10 +144,18 @@ def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Opt
 
 # ---------------------------------------------------------------- block ops
 def bitshift_norm(r: torch.Tensor, gamma: torch.Tensor, out=None, row_stats=None, v2: bool = False) -> torch.Tensor:
-    """Integer BitShiftNorm of r int32 [T, d]; v2 selects BitShiftNormV2's table."""
+    """Integer BitShiftNorm of r int32 [T, d]; v2 selects BitShiftNormV2's table.  row_stats:
+    full row sums int64 [T, 2], or per-block partials int64 [T, P, 2] (bitlinear_residual_parts)."""
     _req(r, torch.int32, "r"); _req(gamma, torch.int16, "gamma")
     T, d = r.shape
     o = out if out is not None else torch.empty((T, d), dtype=torch.int8, device=r.device)
+    if row_stats is not None and row_stats.dim() == 3:
+        _req(row_stats, torch.int64, "row_stats")
+        if row_stats.shape[0] != T or row_stats.shape[2] != 2:
+            raise ValueError(f"row_stats partials must be [{T}, P, 2], got {tuple(row_stats.shape)}")
+        _lib.call("mi_bitshift_norm_parts", _ptr(r), _ptr(gamma), _ptr(o), T, d, _ptr(row_stats),
+                  row_stats.shape[1], int(v2), _stream())
+        return o
     _lib.call("mi_bitshift_norm_v2" if v2 else "mi_bitshift_norm", _ptr(r), _ptr(gamma), _ptr(o), T, d,
               _ptr(_opt(row_stats, torch.int64, "row_stats")), _stream())
     return o

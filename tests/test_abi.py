@@ -62,6 +62,9 @@ def _fake(n=64):
     (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 1, 16, 64, 1, 0, None, None), 1, "stats_parts"),
     (("mi_dt_scan_step", None, 80, 40, None, 2, None, None, 32, 16, None, 15, 13, None, None, 1, 16, 16, None), 2, "dt_rank"),
     (("mi_argmax_i32", None, 10, None, 1, 20, None), 2, "ld"),
+    (("mi_bitshift_norm_parts", None, None, None, 4, 6, None, 1, 0, None), 2, "multiple of 4"),
+    (("mi_bitshift_norm_parts", None, None, None, 4, 8, None, 0, 0, None), 4, "nparts=0"),
+    (("mi_bitshift_norm_parts", "A16", "A16", "A16", 4, 8, "W4", 2, 0, None), 3, "aligned"),
     (("mi_conv_step_xproj", None, 256, None, None, None, None, None, 5, 80, None, 80, 4, 100, None), 2, "multiple of 256"),
     (("mi_conv_step_xproj", None, 16384, None, None, None, None, None, 5, 80, None, 80, 4, 16384, None), 2, "<= 8192"),
     (("mi_conv_step_xproj", None, 512, None, None, None, None, None, 5, 300, None, 300, 4, 512, None), 2, "nx=300"),

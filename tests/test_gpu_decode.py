@@ -191,6 +191,25 @@ def test_xpart_decode_chain(cuda, m, d, D, N, R, stats):
     assert np.array_equal(H(hg), h_ref)
 
 
+@pytest.mark.parametrize("T_,d,P", [(64, 2048, 128), (8, 768, 48), (3, 1100, 7), (5, 4096, 1), (2, 256, 300)])
+@pytest.mark.parametrize("v2", [False, True])
+def test_norm_from_stats_parts(cuda, T_, d, P, v2):
+    """BitShiftNorm (both tables) from per-block row-statistics partials
+    (mi_bitshift_norm_parts) equals the reducing oracle norm; the partials are an
+    exact random split of each row's (sum, sum of squares), as many as 300 per
+    row, over widths that end inside a 1024-channel block."""
+    from mamba_int import ops
+    rng = np.random.default_rng(T_ * d + P + v2)
+    r = _resid(rng, T_, d) >> int(rng.integers(0, 12))
+    g = rng.integers(-400, 400, size=d, dtype=np.int16)
+    r64 = r.astype(np.int64)
+    full = np.stack([r64.sum(1), (r64 * r64).sum(1)], 1)
+    parts = rng.integers(-(2**40), 2**40, size=(T_, P, 2), dtype=np.int64)
+    parts[:, -1, :] = full - parts[:, :-1, :].sum(1)
+    ref = O.bitshift_norm_v2(r, g) if v2 else O.bitshift_norm(r, g)
+    assert np.array_equal(H(ops.bitshift_norm(T(r), T(g), row_stats=T(parts), v2=v2)), ref)
+
+
 @pytest.mark.parametrize("m,D,N,R", [(64, 4096, 16, 128), (37, 1024, 16, 48), (5, 256, 8, 16), (20, 768, 10, 16),
                                      (1, 8192, 64, 128), (3, 4352, 16, 32)])
 def test_conv_step_xproj_chain(cuda, m, D, N, R):
