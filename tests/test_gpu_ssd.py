@@ -90,6 +90,29 @@ def test_ssd_block_scan_decode_steps(cuda):
     assert np.array_equal(H(h), ref_h)
 
 
+@pytest.mark.parametrize("P", [16, 32, 64])
+@pytest.mark.parametrize("N", [16, 32, 64])
+def test_ssd_one_step_kernel(cuda, P, N):
+    """The one-step form of the SSD block scan (len 1: a block per sequence and
+    head) from a random state in place and from no state, every (d_head,
+    d_state) it takes, against the oracle."""
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(P * 7 + N)
+    B, Hh = 5, 3
+    xs, xp, xz, tab, _ = _inputs(rng, B, 1, Hh, P, N, "random" if N == 32 else "model")
+    D = Hh * P
+    h0 = rng.integers(-(2**25), 2**25, size=(B, D, N), dtype=np.int32)
+    ref_y, ref_h = O.ssd_v2_scan(xs, xp, xz, D, tab, 12, Hh, N, h_state=h0)
+    h = T(h0)
+    y = ops.ssd_block_scan(T(xs), T(xp), T(xz), D, T(tab), Hh, N, 12, h_in=h, h_out=h)
+    assert np.array_equal(H(y), ref_y) and np.array_equal(H(h), ref_h)
+    ref_y0, ref_h0 = O.ssd_v2_scan(xs, xp, xz, D, tab, 12, Hh, N)
+    h1 = torch.full((B, D, N), 3, dtype=torch.int32, device="cuda")
+    y0 = ops.ssd_block_scan(T(xs), T(xp), T(xz), D, T(tab), Hh, N, 12, h_out=h1)
+    assert np.array_equal(H(y0), ref_y0) and np.array_equal(H(h1), ref_h0)
+
+
 def _ssd_params(seed=11, d=128, n_layer=2, V=400, N=16, Hh=4, P=64):
     dims = ModelDims(d_model=d, n_layer=n_layer, vocab_size=V, d_state=N, dt_rank=0, block="ssd", n_heads=Hh,
                      d_head=P)
