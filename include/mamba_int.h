@@ -398,12 +398,16 @@ mi_status mi_decode_workspace_size(const mi_model_params *params, int m, size_t 
 /* One greedy decode step of the whole model for m sequences (the reference's
  * generation step, scripts/inference.py:147-161 over MambaIntegerModel.forward,
  * mamba_integer_model.py:486-495, with recurrent state; the dyadic block runs
- * the three fused stages per layer, the SSD block four): ids int64 [m] in,
- * next_ids int64 [m] out (first maximal logit), logits int32 [m][ld_logits]
- * when non-NULL; conv_state / h_state are HOST arrays of n_layer device
- * pointers (int8 [m][3][d_inner], int32 [m][d_inner][d_state]) updated in
- * place; workspace 256-byte aligned, at least mi_decode_workspace_size bytes.
- * Enqueues only kernels (no allocation, no memset): graph-capturable. */
+ * the three fused stages per layer for d_model <= 1024 and m * d_model^2 <=
+ * 64 * 768^2, otherwise five batched stages (norm from statistics partials,
+ * in_proj GEMV, mi_conv_step_xproj, mi_dt_scan_step, out_proj) where
+ * d_inner % 256 == 0; the SSD block four): ids int64 [m] in, next_ids int64
+ * [m] out (first maximal logit), logits int32 [m][ld_logits] when non-NULL;
+ * conv_state / h_state are HOST arrays of n_layer device pointers (int8
+ * [m][3][d_inner], int32 [m][d_inner][d_state]) updated in place; workspace
+ * 256-byte aligned, at least mi_decode_workspace_size bytes (which depends on
+ * the path).  Enqueues only kernels and device copies (no allocation, no
+ * memset): graph-capturable. */
 mi_status mi_decode_step(const mi_model_params *params, int m, const int64_t *ids, int64_t *next_ids,
                          int32_t *logits, int ld_logits, int8_t *const *conv_state, int32_t *const *h_state,
                          void *workspace, size_t workspace_bytes, void *stream);

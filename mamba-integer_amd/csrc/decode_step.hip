@@ -6,7 +6,11 @@
 // layer the three fused stages (norm + in_proj + conv + x_proj partials;
 // x_proj finish + dt_proj + scan step + gate; out_proj + residual + per-block
 // row-statistics partials, which the next norm sums), then norm + lm_head
-// with the greedy pick fused in, and the pick itself.  Mirrors the reference's
+// with the greedy pick fused in, and the pick itself.  Wide models and large
+// batches (where every fused block would normalize m rows of d_model) run the
+// batched stages instead: norm from the partials, in_proj GEMV, conv step +
+// x_proj, dt_proj + scan step, out_proj with partials; the head as norm,
+// GEMV and argmax.  Mirrors the reference's
 // generation step (scripts/inference.py:147-161 over
 // MambaIntegerModel.forward, src/mamba_integer_model.py:486-495) with the
 // recurrent state of a Mamba decode instead of a full-prefix recompute.
@@ -21,7 +25,7 @@ constexpr size_t kAlign = 256;
 size_t up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t r, stats, parts, xz, xs, xp, yo, xpart, keys, total;
+    size_t r, stats, parts, xz, xs, xp, yo, xpart, keys, a, logits, total;
 };
 
 bool ssd(const mi_model_params &p) { return p.block == MI_BLOCK_SSD; }
@@ -29,6 +33,20 @@ size_t d_inner(const mi_model_params &p) { return ssd(p) ? (size_t)p.n_heads * p
 // x_proj width of the SSD block: planar B, C, dt rounded up to 16 (spec rule 7.3)
 size_t ssd_xp_width(const mi_model_params &p) {
     return ((size_t)2 * p.n_heads * p.d_state + p.n_heads + 15) / 16 * 16;
+}
+
+// x_proj row width of the dyadic block's batched stages (dt_rank + 2*nstate, to 16)
+size_t dyadic_xp_width(const mi_model_params &p) { return ((size_t)p.dt_rank + 2 * p.d_state + 15) / 16 * 16; }
+
+// The dyadic block's fused stages normalize all m rows in every block, so the
+// repeated work grows as m * d^2: the same rule as the Python runner (fused for
+// d_model <= 1024 and m * d^2 <= 64 * 768^2), the batched stages otherwise,
+// where their limits allow (d_inner a multiple of 256 up to 8192).
+bool batched(const mi_model_params &p, int m) {
+    if (ssd(p)) return false;
+    const int64_t d = p.d_model, D = (int64_t)d_inner(p);
+    const bool fused_ok = d <= 1024 && m * d * d <= 64 * 768 * 768;
+    return !fused_ok && D % 256 == 0 && D <= 8192 && p.dt_rank + 2 * p.d_state <= 256;
 }
 
 // Sub-buffer offsets of the decode workspace for batch m.
@@ -45,6 +63,10 @@ WsLayout ws_layout(const mi_model_params &p, int m) {
     w.parts = o; o += up((size_t)m * (d / 16) * 2 * 8);
     if (ssd(p)) {
         w.xp = o; o += up((size_t)m * ssd_xp_width(p));
+    } else if (batched(p, m)) {
+        w.xp = o; o += up((size_t)m * dyadic_xp_width(p));
+        w.a = o; o += up((size_t)m * d);
+        w.logits = o; o += up((size_t)m * ((V + 3) / 4 * 4) * 4);
     } else {
         w.xpart = o; o += up((size_t)m * (D / 16) * (R + 2 * N) * 4);
     }
@@ -150,6 +172,38 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
         MI_STEP(mi_norm_bitlinear_argmax(r, parts, P, p.gamma_f, p.w_head, logits, ld_logits, keys, m, p.vocab_size,
                                          d, stream));
         MI_STEP(mi_argmax_keys(keys, (p.vocab_size + 63) / 64, next_ids, m, stream));
+        return MI_OK;
+    }
+    if (batched(p, m)) {
+        int8_t *xp = reinterpret_cast<int8_t *>(base + w.xp);
+        int8_t *a = reinterpret_cast<int8_t *>(base + w.a);
+        // logits rows at a 16-byte multiple stride in the workspace (the GEMV stores 16 bytes a lane)
+        int32_t *lg = reinterpret_cast<int32_t *>(base + w.logits);
+        const int ldl = (p.vocab_size + 3) / 4 * 4;
+        const int W = (int)dyadic_xp_width(p);
+        for (int l = 0; l < p.n_layer; ++l) {
+            const mi_layer_params &ly = p.layers[l];
+            if (l == 0) MI_STEP(mi_bitshift_norm(r, ly.gamma, a, m, d, stats, stream));
+            else MI_STEP(mi_bitshift_norm_parts(r, ly.gamma, a, m, d, parts, P, 0, stream));
+            MI_STEP(mi_bitlinear_gemv(a, d, ly.w_in, xz, 2 * D, MI_OUT_INT8, m, 2 * D, d, ly.s_in, 0, 0, nullptr, 0.0f,
+                                      nullptr, stream));
+            MI_STEP(mi_conv_step_xproj(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], xs, ly.w_x, ly.s_x, nx, xp, W,
+                                       m, D, stream));
+            MI_STEP(mi_dt_scan_step(xp, W, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base, ly.decay_shift, ly.s_y,
+                                    h_state[l], yo, m, D, N, stream));
+            MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
+                                                stream));
+        }
+        MI_STEP(mi_bitshift_norm_parts(r, p.gamma_f, a, m, d, parts, P, 0, stream));
+        MI_STEP(mi_bitlinear_gemv(a, d, p.w_head, lg, ldl, MI_OUT_INT32, m, p.vocab_size, d, 0, 0, 0, nullptr, 0.0f,
+                                  nullptr, stream));
+        MI_STEP(mi_argmax_i32(lg, ldl, next_ids, m, p.vocab_size, stream));
+        if (logits) {
+            const hipError_t e = hipMemcpy2DAsync(logits, (size_t)ld_logits * 4, lg, (size_t)ldl * 4,
+                                                  (size_t)p.vocab_size * 4, (size_t)m, hipMemcpyDeviceToDevice,
+                                                  as_stream(stream));
+            if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_decode_step: logits copy failed: %s", hipGetErrorString(e));
+        }
         return MI_OK;
     }
     for (int l = 0; l < p.n_layer; ++l) {

@@ -140,6 +140,23 @@ def test_config5_width_model_batch64_decode(cuda):
     run = IntegerMambaRunner(p)
     assert np.array_equal(H(run.generate(T(ids), 3, use_graph=False)), ref)
     assert np.array_equal(H(run.generate(T(ids), 3, use_graph=True)), ref)
+    # the native step takes its batched stages here (d_model 2048)
+    from mamba_int import ops
+    from mamba_int.native import NativeDecoder
+    import torch
+    lg, st = run.prefill(T(ids))
+    dec = NativeDecoder(run, 64)
+    assert np.array_equal(H(dec.generate(ops.argmax(lg), st, 3)), ref)
+    # its logits at an odd row stride equal the runner's step
+    lg, st = run.prefill(T(ids))
+    st2 = st.clone()
+    tok = ops.argmax(lg)
+    buf = torch.zeros((64, 32001), dtype=torch.int32, device="cuda")
+    nxt = torch.empty_like(tok)
+    dec.step(tok, st, nxt, logits=buf[:, :32000])
+    ref_logits = run.decode_step(tok, st2)
+    assert np.array_equal(H(buf[:, :32000]), H(ref_logits))
+    assert np.array_equal(H(nxt), H(ops.argmax(ref_logits)))
 
 
 @pytest.mark.parametrize("B", [40, 64])
