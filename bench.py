@@ -14,6 +14,7 @@ OpenMP on every host core) on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--kernels]
     python bench.py --pmc-probe     # only the dominant kernel + a copy of known size, for rocprofv3 --pmc
+    python bench.py --gemm-probe    # only the config-2 prefill GEMM (20 launches), for rocprofv3 counters
 """
 import argparse
 import json
@@ -148,6 +149,23 @@ def in_proj_stage_launch(run, ws, state):
     ly = run.layers[1]
     return lambda: ops.norm_in_proj_conv(ws.r, ly.gamma, ly.w_in, ly.s_in, ly.conv_w, ly.conv_b, state.conv[1],
                                          ws.xs, ws.xz, row_stats=ws.parts, w_x=ly.w_x, xpart=ws.xpart)
+
+
+def gemm_probe():
+    """For rocprofv3: 20 launches of the config-2 prefill GEMM (M 4096, K 768,
+    N 3072, int8 requant out) on the MFMA tile path."""
+    import numpy as np
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(1)
+    M, K, N = 4096, 768, 3072
+    a = torch.from_numpy(rng.integers(-127, 128, size=(M, K), dtype=np.int8)).to("cuda:0")
+    wp = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(N, K), dtype=np.int8))).to("cuda:0")
+    o = torch.empty((M, N), dtype=torch.int8, device="cuda:0")
+    for _ in range(20):
+        ops.bitlinear(a, wp, ops.OUT_INT8, N, shift=5, out=o, path="gemm")
+    torch.cuda.synchronize()
+    print(json.dumps({"gemm_probe": "done", "launches": 20, "int8_ops_per_launch": 2 * M * N * K}))
 
 
 def pmc_probe():
@@ -314,6 +332,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--kernels", action="store_true", help="also time each config's kernel")
     ap.add_argument("--pmc-probe", action="store_true", help="only the dominant kernel and a copy (for counters)")
+    ap.add_argument("--gemm-probe", action="store_true", help="only the config-2 prefill GEMM (for counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the integer inference path has no "
@@ -328,6 +347,9 @@ def main():
     _lib.load()
     if args.pmc_probe:
         pmc_probe()
+        return
+    if args.gemm_probe:
+        gemm_probe()
         return
     dims = ModelDims(d_model=768, n_layer=24, vocab_size=32000, d_state=16, dt_rank=48)
     B, L, NDEC = 8, 2048, args.decode_steps
