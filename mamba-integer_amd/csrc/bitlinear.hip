@@ -248,18 +248,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                 }
             }
         }
+    } else if constexpr (KIND == MI_OUT_RESIDUAL) {
+        // residual rows read as 16-byte vectors, four token groups' loads issued
+        // before any update (rows past M and groups past N read clamped in-bounds
+        // addresses; their results are not stored)
+        int32_t *ob = (int32_t *)g.out;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v4i old[4][2];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int m = min(m0 + (4 * h + jj) * 16 + l16, g.M - 1);
+                    const int n = n0 + wn * 32 + i * 16 + 4 * lq;
+                    old[jj][i] = *reinterpret_cast<const v4i *>(ob + (int64_t)m * g.ldo + (n < g.N ? n : 0));
+                }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = 4 * h + jj;
+                const int m = m0 + j * 16 + l16;
+                RowStat st{0, 0};
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int n = n0 + wn * 32 + i * 16 + 4 * lq;
+                    if (m < g.M && n < g.N) {
+                        v4i nv;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t delta = rshr64((int64_t)acc[i][j][r] * g.res_mult, g.res_shift);
+                            nv[r] = (int32_t)clamp64((int64_t)old[jj][i][r] + delta, -kResidualLimit, kResidualLimit);
+                        }
+                        int32_t *o = ob + (int64_t)m * g.ldo + n;
+                        if (n + 3 < g.N) {
+                            *reinterpret_cast<v4i *>(o) = nv;
+                        } else {
+                            for (int r = 0; r < 4 && n + r < g.N; ++r) o[r] = nv[r];
+                        }
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (n + r < g.N) {
+                                st.s1 += nv[r];
+                                st.s2 += (int64_t)nv[r] * nv[r];
+                            }
+                        }
+                    }
+                }
+                if (g.row_stats) flush_row_stat(g, st, m, lq);
+            }
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int m = m0 + j * 16 + l16;
-            RowStat st{0, 0};
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const RowStat e = store4<KIND>(g, m, n0 + wn * 32 + i * 16 + 4 * lq, acc[i][j]);
-                st.s1 += e.s1;
-                st.s2 += e.s2;
-            }
-            if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
+            for (int i = 0; i < 2; ++i) store4<KIND>(g, m, n0 + wn * 32 + i * 16 + 4 * lq, acc[i][j]);
         }
     }
 }
