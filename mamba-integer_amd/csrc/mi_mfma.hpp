@@ -27,21 +27,19 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Exact squareplus of spec rule 4.4 on a conv output c (Q10) -> int8 (Q4): a
-// Newton step on the hardware reciprocal-square-root estimate gives
-// sqrt(v^2 + 2^22) within a unit; bounded integer corrections make it the
-// exact floor.
+// Exact squareplus of spec rule 4.4 on a conv output c (Q10) -> int8 (Q4):
+// floor(sqrt(v^2 + 2^22)) from the hardware square root of the float-rounded
+// argument.  With 2^22 <= Y < 2^32, rounding Y to float moves sqrt(Y) by at
+// most 128 / (2 * 2048) < 0.032 and v_sqrt_f32 adds under an ulp (2^-8), so
+// the truncated root is isqrt(Y) or one off; one compare each way makes it
+// exact (s <= 51243, so the 24-bit squares are exact).
 __device__ __forceinline__ int sqp_q(int32_t c) {
     const int32_t v = clamp32(c, -51200, 51200);
     const uint32_t av = (uint32_t)(v < 0 ? -v : v);
     const uint32_t Y = av * av + (1u << 22);  // < 2^32
-    const float yf = (float)Y;
-    float rs = __builtin_amdgcn_rsqf(yf);
-    rs = rs * (1.5f - 0.5f * yf * rs * rs);
-    uint32_t s = (uint32_t)(yf * rs);
-    if (s > 65535u) s = 65535u;
-    for (int it = 0; it < 4 && (uint64_t)s * s > Y; ++it) --s;
-    for (int it = 0; it < 4 && (uint64_t)(s + 1) * (s + 1) <= Y; ++it) ++s;
+    uint32_t s = (uint32_t)__builtin_amdgcn_sqrtf((float)Y);
+    s -= __umul24(s, s) > Y ? 1u : 0u;
+    s += __umul24(s + 1, s + 1) <= Y ? 1u : 0u;
     return clamp32(rshr32(v + (int32_t)s, 7), -127, 127);
 }
 

@@ -122,6 +122,21 @@ def test_gemm_tile_edges(cuda, M, N, K, pad):
     assert np.array_equal(acc[:, :N], O.bitlinear(a, wp, O.OUT_INT32))
 
 
+def test_squareplus_every_input(cuda):
+    """Squareplus over every conv output it can see (the clamp range [-51200,
+    51200] and beyond), through the conv with zero taps and the value in the
+    bias: the device's exact square root against the oracle, exhaustively."""
+    from mamba_int import ops
+    lo, hi = -51300, 51300
+    D = (hi - lo + 1 + 3) // 4 * 4
+    cb = (np.arange(D) + lo).astype(np.int32)
+    cw = np.zeros((D, 4), np.int8)
+    xz = np.zeros((1, 1, 2 * D), np.int8)
+    ref, _ = O.conv_squareplus(xz, D, cw, cb)
+    got = ops.conv_squareplus(T(xz), D, T(cw), T(cb))
+    assert np.array_equal(H(got), ref)
+
+
 def test_act_quant_and_bitlinear_float_face(cuda):
     """Drop-in BitLinear: GPU output bit-identical to the reference's CPU formula
     (rational_bitnet.py:63-111,167-213 evaluated with torch on the CPU)."""
