@@ -100,6 +100,71 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const int32_t *r, const 
     }
 }
 
+// norm_wave_kernel for dim = 256 * J: every load unconditional and issued up
+// front (the row's J int4 per lane and its gains as one 8-byte load per 4
+// channels), so the wave waits once instead of once per conditional load.
+template <bool V2, int J>
+__global__ __launch_bounds__(256) void norm_wave_fixed_kernel(const int32_t *r, const int16_t *gamma, int8_t *out,
+                                                              int tokens) {
+    constexpr int dim = 256 * J;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = min((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), (int64_t)tokens - 1);
+    const int32_t *rr = r + row * dim;
+    int4 v[J];
+    int2 gv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) v[j] = *reinterpret_cast<const int4 *>(rr + 4 * lane + 256 * j);
+#pragma unroll
+    for (int j = 0; j < J; ++j) gv[j] = *reinterpret_cast<const int2 *>(gamma + 4 * lane + 256 * j);
+    int64_t s1 = 0, s2 = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        s1 += (int64_t)v[j].x + v[j].y + v[j].z + v[j].w;
+        s2 += (int64_t)v[j].x * v[j].x + (int64_t)v[j].y * v[j].y + (int64_t)v[j].z * v[j].z +
+              (int64_t)v[j].w * v[j].w;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += __shfl_xor(s1, off);
+        s2 += __shfl_xor(s2, off);
+    }
+    int64_t mu;
+    const int sh = norm_shift_for<V2>(s1, s2, dim, &mu);
+    if ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6) >= tokens) return;  // the clamped duplicate row
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int vv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const int gg[4] = {(int)(int16_t)gv[j].x, gv[j].x >> 16, (int)(int16_t)gv[j].y, gv[j].y >> 16};
+        uint32_t o = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            o |= (uint32_t)((int)clamp64(rshr64((int64_t)(vv[q] - mu) * gg[q], sh), -127, 127) & 255) << (8 * q);
+        *reinterpret_cast<uint32_t *>(out + row * dim + 4 * lane + 256 * j) = o;
+    }
+}
+
+template <bool V2>
+bool launch_norm_wave_fixed(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens, int dim,
+                            hipStream_t st) {
+    if (dim % 256 != 0 || !aligned(gamma, 8)) return false;
+    const dim3 grid((unsigned)((tokens + 3) / 4));
+    switch (dim / 256) {
+#define MI_NWCASE(JJ)                                                                                      \
+    case JJ:                                                                                               \
+        hipLaunchKernelGGL((norm_wave_fixed_kernel<V2, JJ>), grid, dim3(256), 0, st, r, gamma, out, tokens); \
+        return true;
+        MI_NWCASE(1)
+        MI_NWCASE(2)
+        MI_NWCASE(3)
+        MI_NWCASE(4)
+        MI_NWCASE(6)
+        MI_NWCASE(8)
+        MI_NWCASE(12)
+        MI_NWCASE(16)
+#undef MI_NWCASE
+    }
+    return false;
+}
+
 // --------------------------------------------------------------- embedding
 __global__ void embed_kernel(const int64_t *ids, const int8_t *emb, int32_t *r, int tokens, int dim, int vocab) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -402,8 +467,9 @@ mi_status bitshift_norm_impl(const char *fn, const int32_t *r, const int16_t *ga
         hipLaunchKernelGGL(norm_stats_kernel<V2>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                            as_stream(stream), r, gamma, out, row_stats, tokens, dim);
     } else if (dim % 4 == 0 && dim <= 256 * kNormWaveMax && aligned(r, 16) && aligned(out, 4)) {
-        hipLaunchKernelGGL(norm_wave_kernel<V2>, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, as_stream(stream),
-                           r, gamma, out, tokens, dim);
+        if (!launch_norm_wave_fixed<V2>(r, gamma, out, tokens, dim, as_stream(stream)))
+            hipLaunchKernelGGL(norm_wave_kernel<V2>, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0,
+                               as_stream(stream), r, gamma, out, tokens, dim);
     } else {
         hipLaunchKernelGGL(norm_kernel<V2>, dim3((unsigned)tokens), dim3(kNormThreads), 0, as_stream(stream), r, gamma,
                            out, dim);

@@ -165,7 +165,7 @@ def test_act_quant_and_bitlinear_float_face(cuda):
 
 def test_norm(cuda, rng):
     from mamba_int import ops
-    for T_, d in ((37, 768), (5, 2048), (3, 100), (64, 16)):
+    for T_, d in ((37, 768), (5, 2048), (3, 100), (64, 16), (9, 1536), (3, 4096), (3, 256), (6, 3072)):
         r = rng.integers(-(2**23) + 1, 2**23, size=(T_, d), dtype=np.int32)
         r[0] = 0
         r[1] = rng.integers(-3, 4, size=d)
