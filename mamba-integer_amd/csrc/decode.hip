@@ -498,6 +498,7 @@ struct DtScanArgs {
 };
 
 constexpr int kMaxR = 256;
+__constant__ StepTables kStepTables = make_step_tables();
 constexpr int kMaxN = 64;
 
 // Thread quad per channel: lane g of the quad keeps states g, g+4, g+8, ...;
@@ -629,8 +630,14 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     __shared__ int32_t s_xacc[XNT ? 4 : 1][XNT ? 16 * kMaxXTiles : 1];  // XNT < 0: row 0 only
     __shared__ int32_t s_dtq[41];    // dt_q16(dm) for dm in [-20, 20]
     __shared__ int32_t s_gate[256];  // gate_q15(z) for z in [-128, 127] (the block has 256 threads)
-    if (threadIdx.x < 41) s_dtq[threadIdx.x] = dt_q16((int)threadIdx.x - 20);
-    s_gate[threadIdx.x] = gate_q15((int)threadIdx.x - 128);
+    // table entries load with the other independent loads; they reach LDS
+    // just before the first barrier, after every other load has been issued
+    const int32_t tab_dt = kStepTables.dtq[min((int)threadIdx.x, 40)];
+    const int32_t tab_gate = kStepTables.gate[threadIdx.x];
+    auto stage_tables = [&]() {
+        if (threadIdx.x < 41) s_dtq[threadIdx.x] = tab_dt;
+        s_gate[threadIdx.x] = tab_gate;
+    };
     constexpr int kPerLane = NPL > 0 ? NPL : kMaxN / 4;
     const int m = blockIdx.y;
     const int q = threadIdx.x & 3;
@@ -643,8 +650,8 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     const int kw = g.R / 16;
     uint32_t wdt[kMaxR / 64];
 #pragma unroll
-    for (int i = 0; i < kMaxR / 64; ++i)
-        if (4 * i < kw) wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
+    for (int i = 0; i < kMaxR / 64; ++i)  // unconditional (kw >= 1): words past kw are never used
+        wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
     int32_t *hp = g.h + ((int64_t)m * g.D + dd) * g.N;
     const int32_t *bp = g.base + (int64_t)dd * g.N;
     int32_t hv[kPerLane], bv[kPerLane];
@@ -694,6 +701,7 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
             }
             s_xacc[0][sub * NX + n] = sum;
         }
+        stage_tables();
         __syncthreads();
         for (int i = threadIdx.x; i < NX; i += 256) {
             int v = 0;
@@ -705,6 +713,7 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     } else if constexpr (XNT > 0) {
         if (g.x_c16) xproj_token_c16<(XNT > 0 ? XNT : 1)>(g, m, s_xacc);
         else xproj_token<(XNT > 0 ? XNT : 1)>(g, m, s_xacc);
+        stage_tables();
         __syncthreads();
         const int NX = g.R + 2 * g.N;
         for (int i = threadIdx.x; i < NX; i += 256) {
@@ -718,6 +727,7 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
         for (int i = threadIdx.x; i < g.R; i += 256) s_dt[i] = row[i];
         for (int i = threadIdx.x; i < 2 * g.N; i += 256) s_bc[i] = row[g.R + i];
     }
+    if constexpr (XNT == 0) stage_tables();
     __syncthreads();
 
     int acc = 0;
@@ -780,8 +790,8 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_bc[TPB][32];
     __shared__ int32_t s_dtq[41];
     __shared__ int32_t s_gate[256];
-    if (threadIdx.x < 41) s_dtq[threadIdx.x] = dt_q16((int)threadIdx.x - 20);
-    s_gate[threadIdx.x] = gate_q15((int)threadIdx.x - 128);
+    const int32_t tab_dt = kStepTables.dtq[min((int)threadIdx.x, 40)];
+    const int32_t tab_gate = kStepTables.gate[threadIdx.x];
     const int m0 = blockIdx.y * TPB;
     const int q = threadIdx.x & 3;
     const int d = blockIdx.x * 64 + (threadIdx.x >> 2);
@@ -790,8 +800,8 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     const int kw = g.R / 16;
     uint32_t wdt[kMaxR / 64];
 #pragma unroll
-    for (int i = 0; i < kMaxR / 64; ++i)
-        if (4 * i < kw) wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
+    for (int i = 0; i < kMaxR / 64; ++i)  // unconditional (kw >= 1): words past kw are never used
+        wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
     const int4 b4 = *reinterpret_cast<const int4 *>(g.base + (int64_t)dd * 16 + 4 * q);
     int4 h4[TPB];
     int xsv[TPB], zv[TPB];
@@ -802,16 +812,31 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
         xsv[t] = g.xs[(int64_t)mt * g.D + dd];
         zv[t] = g.z[(int64_t)mt * g.z_stride + dd];
     }
+    // the TPB x_proj rows (dt_raw, B, C): every byte load issued before the
+    // first wait, from clamped in-bounds positions; staged into LDS below
     const int nxr = g.R + 32;
-    for (int i = threadIdx.x; i < TPB * nxr; i += 256) {
+    constexpr int kXpLoads = (TPB * (kMaxR + 32) + 255) / 256;
+    int8_t xpv[kXpLoads];
+#pragma unroll
+    for (int u = 0; u < kXpLoads; ++u) {
+        const int i = min((int)threadIdx.x + 256 * u, TPB * nxr - 1);
         const int t = i / nxr, c = i - t * nxr;
-        const int8_t v = g.xp[(int64_t)min(m0 + t, g.M - 1) * g.xp_stride + c];
-        if (c < g.R) s_dt[t][c] = v;
-        else s_bc[t][c - g.R] = v;
+        xpv[u] = g.xp[(int64_t)min(m0 + t, g.M - 1) * g.xp_stride + c];
     }
     v4i wt[kMaxR / 64];
 #pragma unroll
-    for (int i = 0; i < kMaxR / 64; ++i) wt[i] = 4 * i < kw ? unpack16(wdt[i]) : v4i{0, 0, 0, 0};
+    for (int i = 0; i < kMaxR / 64; ++i) wt[i] = unpack16(wdt[i]);  // words past kw are skipped below
+#pragma unroll
+    for (int u = 0; u < kXpLoads; ++u) {
+        const int i = (int)threadIdx.x + 256 * u;
+        if (i < TPB * nxr) {
+            const int t = i / nxr, c = i - t * nxr;
+            if (c < g.R) s_dt[t][c] = xpv[u];
+            else s_bc[t][c - g.R] = xpv[u];
+        }
+    }
+    if (threadIdx.x < 41) s_dtq[threadIdx.x] = tab_dt;
+    s_gate[threadIdx.x] = tab_gate;
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < TPB; ++t) {

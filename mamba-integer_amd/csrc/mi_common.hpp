@@ -24,7 +24,7 @@ inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintp
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // ------------------------------------------------------ integer primitives
-__host__ __device__ __forceinline__ int64_t rshr64(int64_t v, int s) {
+__host__ __device__ __forceinline__ constexpr int64_t rshr64(int64_t v, int s) {
     return s <= 0 ? v : ((v + ((int64_t)1 << (s - 1))) >> s);
 }
 __host__ __device__ __forceinline__ int32_t rshr32(int32_t v, int s) {
@@ -34,7 +34,7 @@ __host__ __device__ __forceinline__ int32_t rshr32(int32_t v, int s) {
 __host__ __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
-__host__ __device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
+__host__ __device__ __forceinline__ constexpr int64_t clamp64(int64_t v, int64_t lo, int64_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 __host__ __device__ __forceinline__ int32_t sat32_64(int64_t v) {
@@ -86,12 +86,58 @@ __host__ __device__ inline int32_t dt_q16(int dm) {
     return (int32_t)clamp64(rshr64(655 * sq, 16), 66, 6554);
 }
 
+// floor(sqrt(v)) digit by digit, for tables built at compile time.
+constexpr uint64_t isqrt64_bitwise(uint64_t v) {
+    uint64_t r = 0, bit = 1ull << 62;
+    while (bit > v) bit >>= 2;
+    while (bit) {
+        if (v >= r + bit) {
+            v -= r + bit;
+            r = (r >> 1) + bit;
+        } else {
+            r >>= 1;
+        }
+        bit >>= 2;
+    }
+    return r;
+}
+
+// dt_q16 in a constant expression (same rule, bitwise square root).
+constexpr int32_t dt_q16_table_entry(int dm) {
+    const int64_t s = (int64_t)dm * 65536 + (int64_t)isqrt64_bitwise((uint64_t)((int64_t)dm * dm) * (1ull << 32) +
+                                                                     (1ull << 34));
+    return (int32_t)clamp64(rshr64(655 * (s >> 1), 16), 66, 6554);
+}
+
 // Gate of spec rule 4.11 (mamba_integer_model.py:124-132), Q15, z in Q4.
-__host__ __device__ inline int32_t gate_q15(int z) {
+__host__ __device__ constexpr int32_t gate_q15(int z) {
     int32_t a = z < 0 ? -z : z;
     int32_t q = (16384 * a) / (16 + a);
     return 16384 + (z < 0 ? -q : q);
 }
+
+// The decode step kernels' lookup tables, built by the compiler: dt_q16(dm)
+// for dm in [-20, 20] and gate_q15(z) for z in [-128, 127].  Blocks copy
+// them into LDS with one load per thread instead of evaluating the rules.
+struct StepTables {
+    int32_t dtq[41];
+    int32_t gate[256];
+};
+constexpr StepTables make_step_tables() {
+    StepTables t{};
+    for (int i = 0; i < 41; ++i) t.dtq[i] = dt_q16_table_entry(i - 20);
+    for (int i = 0; i < 256; ++i) t.gate[i] = gate_q15(i - 128);
+    return t;
+}
+// Position-weighted sums of both tables as the integer oracle computes them
+// (sum (i + 1) * table[i]), so a wrong entry fails the build.
+constexpr int64_t step_table_weighted_sum(const int32_t *t, int n) {
+    int64_t s = 0;
+    for (int i = 0; i < n; ++i) s += (int64_t)(i + 1) * t[i];
+    return s;
+}
+static_assert(step_table_weighted_sum(make_step_tables().dtq, 41) == 3482397, "dt table");
+static_assert(step_table_weighted_sum(make_step_tables().gate, 256) == 756841947, "gate table");
 
 }  // namespace mi
 
