@@ -803,12 +803,12 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     for (int i = 0; i < kMaxR / 64; ++i)  // unconditional (kw >= 1): words past kw are never used
         wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
     const int4 b4 = *reinterpret_cast<const int4 *>(g.base + (int64_t)dd * 16 + 4 * q);
-    int4 h4[TPB];
+    v4i h4[TPB];   // streamed: the whole state is read and written once per step
     int xsv[TPB], zv[TPB];
 #pragma unroll
     for (int t = 0; t < TPB; ++t) {
         const int mt = min(m0 + t, g.M - 1);
-        h4[t] = *reinterpret_cast<const int4 *>(g.h + ((int64_t)mt * g.D + dd) * 16 + 4 * q);
+        h4[t] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(g.h + ((int64_t)mt * g.D + dd) * 16 + 4 * q));
         xsv[t] = g.xs[(int64_t)mt * g.D + dd];
         zv[t] = g.z[(int64_t)mt * g.z_stride + dd];
     }
@@ -856,7 +856,7 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
         acc += __shfl_xor(acc, 2);
         const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
         const int64_t xd = rshr64((int64_t)xsv[t] * s_dtq[dm + 20], 10);
-        const int hv[4] = {h4[t].x, h4[t].y, h4[t].z, h4[t].w};
+        const int hv[4] = {h4[t][0], h4[t][1], h4[t][2], h4[t][3]};
         const int bv[4] = {b4.x, b4.y, b4.z, b4.w};
         int32_t hn[4];
         int64_t y = 0;
@@ -868,7 +868,8 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
             y += (int64_t)s_bc[t][16 + n] * hn[i];
         }
         if (active && m < g.M)
-            *reinterpret_cast<int4 *>(g.h + ((int64_t)m * g.D + d) * 16 + 4 * q) = make_int4(hn[0], hn[1], hn[2], hn[3]);
+            __builtin_nontemporal_store(v4i{hn[0], hn[1], hn[2], hn[3]},
+                                        reinterpret_cast<v4i *>(g.h + ((int64_t)m * g.D + d) * 16 + 4 * q));
         y += __shfl_xor(y, 1);
         y += __shfl_xor(y, 2);
         if (active && q == 0 && m < g.M) {
