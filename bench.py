@@ -188,6 +188,22 @@ def pmc_probe():
     print(json.dumps({"pmc_probe": "done", "kernel_launches": 20, "copy_bytes": 256 << 20, "copies": 3}))
 
 
+def decode5_probe():
+    """For rocprofv3: the d2048 x 48 model (d_inner 4096, dt_rank 128) at batch
+    64: a 16-token prefill, then 4 eager greedy decode steps (every layer's
+    recurrent state, 805 MB in all, streams through HBM each step)."""
+    import torch
+    from mamba_int import ModelDims
+    from mamba_int.model import IntegerMambaRunner, random_device_params
+    dims = ModelDims(d_model=2048, n_layer=48, vocab_size=32000, d_state=16, dt_rank=128)
+    run = IntegerMambaRunner(random_device_params(dims, 5, "cuda:0"), device="cuda:0")
+    ids = torch.randint(0, 32000, (64, 16), device="cuda:0")
+    logits, state = run.prefill(ids)
+    run.decode_loop(logits, state, 4, use_graph=False)
+    torch.cuda.synchronize()
+    print(json.dumps({"decode5_probe": "done", "batch": 64, "decode_steps": 4}))
+
+
 def kernel_table():
     """Per-config kernel timings: config-1 scan, config-2 GEMM and GEMV (weights
     rotated over 512 copies so the GEMV reads HBM, not the 256 MB MALL), the
@@ -333,6 +349,8 @@ def main():
     ap.add_argument("--kernels", action="store_true", help="also time each config's kernel")
     ap.add_argument("--pmc-probe", action="store_true", help="only the dominant kernel and a copy (for counters)")
     ap.add_argument("--gemm-probe", action="store_true", help="only the config-2 prefill GEMM (for counters)")
+    ap.add_argument("--decode5-probe", action="store_true",
+                    help="only 4 eager decode steps of the d2048 x 48 model at batch 64 (for a kernel trace)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the integer inference path has no "
@@ -350,6 +368,9 @@ def main():
         return
     if args.gemm_probe:
         gemm_probe()
+        return
+    if args.decode5_probe:
+        decode5_probe()
         return
     dims = ModelDims(d_model=768, n_layer=24, vocab_size=32000, d_state=16, dt_rank=48)
     B, L, NDEC = 8, 2048, args.decode_steps
