@@ -322,10 +322,23 @@ mi_status mi_conv_step_xproj(const int8_t *xz, int xz_stride, const int8_t *conv
                              int8_t *conv_state, int8_t *xs, const uint8_t *w_x, int s_x, int nx, int8_t *xp,
                              int xp_stride, int m, int d_inner, void *stream);
 
+/* mi_conv_step_xproj with x_proj left as exact int32 partial sums over the
+ * four channel quarters (same reference lines):
+ *   xpart[i, q, n] = sum over c in [q*d_inner/4, (q+1)*d_inner/4) of
+ *                    w_x[n, c] * xs[i, c]
+ * into xpart int32 [m, 4, nx]; xs and conv_state as in mi_conv_step_xproj.
+ * Four blocks per token share its conv operands and x_proj weights.
+ * d_inner a multiple of 1024, <= 8192; nx <= 256.  The partials feed
+ * mi_xpart_dt_scan_step with nblk = 4.  (No reference counterpart of the
+ * split; it replaces the same conv1d_step.cu + x_proj pair.) */
+mi_status mi_conv_step_xpart(const int8_t *xz, int xz_stride, const int8_t *conv_w, const int32_t *conv_b,
+                             int8_t *conv_state, int8_t *xs, const uint8_t *w_x, int nx, int32_t *xpart, int m,
+                             int d_inner, void *stream);
+
 /* mi_dt_scan_step with x_proj finished from those partials:
  * xp[i, n] = sat8(rshr(sum over b < nblk of xpart[i, b, n], s_x)), then
  * dt_rank, B and C as in mi_dt_scan_step.  nblk = d_inner/16 for the
- * partials of mi_norm_in_proj_conv_xpart. */
+ * partials of mi_norm_in_proj_conv_xpart, 4 for mi_conv_step_xpart. */
 mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s_x, int dt_rank, const uint8_t *w_dt,
                                 int s_dt, const int8_t *xs, const int8_t *z, int z_stride, int z_off,
                                 const int32_t *base, int decay_shift, int s_y, int32_t *h_state, int8_t *yo,

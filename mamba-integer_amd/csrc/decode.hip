@@ -500,6 +500,7 @@ struct DtScanArgs {
 constexpr int kMaxR = 256;
 __constant__ StepTables kStepTables = make_step_tables();
 constexpr int kMaxN = 64;
+constexpr int kTokMaxParts = 4;  // x_proj partials per token that dt_scan_tok_kernel sums itself
 
 // Thread quad per channel: lane g of the quad keeps states g, g+4, g+8, ...;
 // every lane computes the channel's dt_proj dot (48-wide at d768), the quad
@@ -784,7 +785,9 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
 // the dt_proj words (unpacked once), the decays and the tables serve all TPB
 // tokens, and each lane keeps TPB int4 state vectors in flight.  Lane q of a
 // channel owns states 4q..4q+3, as in dt_scan_step_kernel<0, 4>.
-template <int TPB>
+// XP: the x_proj rows arrive as nblk <= kTokMaxParts int32 partial sums per
+// token (mi_xpart_dt_scan_step), summed and requantised while staging.
+template <int TPB, bool XP>
 __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_dt[TPB][kMaxR];
     __shared__ __align__(16) int8_t s_bc[TPB][32];
@@ -817,11 +820,19 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     const int nxr = g.R + 32;
     constexpr int kXpLoads = (TPB * (kMaxR + 32) + 255) / 256;
     int8_t xpv[kXpLoads];
+    int32_t xpp[XP ? kXpLoads : 1][XP ? kTokMaxParts : 1];
 #pragma unroll
     for (int u = 0; u < kXpLoads; ++u) {
         const int i = min((int)threadIdx.x + 256 * u, TPB * nxr - 1);
         const int t = i / nxr, c = i - t * nxr;
-        xpv[u] = g.xp[(int64_t)min(m0 + t, g.M - 1) * g.xp_stride + c];
+        const int mt = min(m0 + t, g.M - 1);
+        if constexpr (XP) {
+#pragma unroll
+            for (int b = 0; b < kTokMaxParts; ++b)
+                xpp[u][b] = g.xpart[((int64_t)mt * g.nblk + min(b, g.nblk - 1)) * nxr + c];
+        } else {
+            xpv[u] = g.xp[(int64_t)mt * g.xp_stride + c];
+        }
     }
     v4i wt[kMaxR / 64];
 #pragma unroll
@@ -831,8 +842,17 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
         const int i = (int)threadIdx.x + 256 * u;
         if (i < TPB * nxr) {
             const int t = i / nxr, c = i - t * nxr;
-            if (c < g.R) s_dt[t][c] = xpv[u];
-            else s_bc[t][c - g.R] = xpv[u];
+            int8_t v;
+            if constexpr (XP) {
+                int32_t sum = xpp[u][0];
+#pragma unroll
+                for (int b = 1; b < kTokMaxParts; ++b) sum += b < g.nblk ? xpp[u][b] : 0;
+                v = (int8_t)clamp32(rshr32(sum, g.s_x), -127, 127);
+            } else {
+                v = xpv[u];
+            }
+            if (c < g.R) s_dt[t][c] = v;
+            else s_bc[t][c - g.R] = v;
         }
     }
     if (threadIdx.x < 41) s_dtq[threadIdx.x] = tab_dt;
@@ -1064,7 +1084,7 @@ extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_ran
     // two tokens per block measured fastest at batch 64 (2.40 ms per d2048x48 step
     // against 2.44 with four, 2.54 with eight and 2.46 with one)
     if (vec && m >= 2)
-        hipLaunchKernelGGL((dt_scan_tok_kernel<2>), dim3((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2)),
+        hipLaunchKernelGGL((dt_scan_tok_kernel<2, false>), dim3((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2)),
                            dim3(256), 0, as_stream(stream), g);
     else if (vec) hipLaunchKernelGGL((dt_scan_step_kernel<0, 4>), grid, dim3(256), 0, as_stream(stream), g);
     else hipLaunchKernelGGL((dt_scan_step_kernel<0, 0>), grid, dim3(256), 0, as_stream(stream), g);
@@ -1100,7 +1120,12 @@ extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s
     g.xs = xs; g.z = z + z_off; g.z_stride = z_stride; g.base = base; g.k = decay_shift; g.s_y = s_y;
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
     const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
-    if (nstate == 16 && aligned(h_state, 16) && aligned(base, 16))
+    const bool vec = nstate == 16 && aligned(h_state, 16) && aligned(base, 16);
+    if (vec && nblk <= kTokMaxParts && m >= 2)
+        // few partials (mi_conv_step_xpart's channel quarters): two tokens per block
+        hipLaunchKernelGGL((dt_scan_tok_kernel<2, true>), dim3((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2)),
+                           dim3(256), 0, as_stream(stream), g);
+    else if (vec)
         hipLaunchKernelGGL((dt_scan_step_kernel<-1, 4>), grid, dim3(256), 0, as_stream(stream), g);
     else
         hipLaunchKernelGGL((dt_scan_step_kernel<-1, 0>), grid, dim3(256), 0, as_stream(stream), g);
@@ -1174,6 +1199,7 @@ struct ConvXArgs {
     const uint32_t *w_x;  // [nx][D/16] words
     int8_t *xp;           // [M][xp_stride]
     int64_t xp_stride;
+    int32_t *xpart;       // [M][kConvXParts][nx] (conv_step_xpart_kernel)
     int M, D, nx, s_x;
 };
 
@@ -1250,8 +1276,158 @@ __global__ __launch_bounds__(64 * kConvXWaves) void conv_step_xproj_kernel(ConvX
     }
 }
 
+// conv_step_xpart_kernel: block (quarter q, token m) runs the conv step +
+// squareplus of channels [q*D/4, (q+1)*D/4) and the exact int32 x_proj sum
+// over them, so four blocks share the conv operands and x_proj weights a
+// token needs (212 KB at d_inner 4096) instead of one CU pulling them all.
+// 4 waves; wave w takes the quarter's 256-channel slices w, w+4, ...  The
+// first conv pass's operands and the first slice's weights are loaded before
+// the first wait (clamped in-bounds; unused results are not stored).
+constexpr int kConvXParts = 4;
+static_assert(kConvXParts <= kTokMaxParts, "the scan step sums the quarters itself");
+
+template <int NT>
+__global__ __launch_bounds__(256) void conv_step_xpart_kernel(ConvXArgs g) {
+    __shared__ __align__(16) int8_t s_xs[kConvXMaxD / kConvXParts];
+    __shared__ int32_t s_red[4][16 * NT];
+    constexpr int kPass = 4 * 256;   // channels per conv pass of the block
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = wave_id();
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int part = blockIdx.x, m = blockIdx.y;
+    const int C = g.D / kConvXParts;   // a multiple of 256
+    const int c0 = part * C;
+    const int nsl = C / 256;
+
+    const int8_t *xr = g.xz + (int64_t)m * g.xz_stride + c0;
+    int8_t *st = g.conv_state + (int64_t)m * 3 * g.D + c0;
+    int8_t *xso = g.xs + (int64_t)m * g.D + c0;
+    const int xkw = g.D / 16;
+    const uint32_t *wrow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wrow[t] = g.w_x + (int64_t)min(16 * t + l16, g.nx - 1) * xkw + c0 / 16 + 4 * lq;
+    v4i wv0[NT];
+    {
+        const int sl = min(wave, nsl - 1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wv0[t] = *reinterpret_cast<const v4i *>(wrow[t] + 16 * sl);
+    }
+    struct ConvIn {
+        uint32_t x, s0, s1, s2;
+        v4i cw, cb;
+    };
+    auto conv_load = [&](int ch) {
+        ConvIn c;
+        c.x = *reinterpret_cast<const uint32_t *>(xr + ch);
+        c.s0 = *reinterpret_cast<const uint32_t *>(st + ch);
+        c.s1 = *reinterpret_cast<const uint32_t *>(st + g.D + ch);
+        c.s2 = *reinterpret_cast<const uint32_t *>(st + 2 * g.D + ch);
+        c.cw = *reinterpret_cast<const v4i *>(g.conv_w + (int64_t)(c0 + ch) * 4);
+        c.cb = *reinterpret_cast<const v4i *>(g.conv_b + c0 + ch);
+        return c;
+    };
+    // depthwise conv step (conv1d_step.cu:30-57) + squareplus of 4 channels
+    auto conv_finish = [&](const ConvIn &c, int ch) {
+        uint32_t o = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t w = (uint32_t)c.cw[e];
+            const int32_t acc = c.cb[e] + (int)(int8_t)w * (int)(int8_t)(c.s0 >> (8 * e)) +
+                                (int)(int8_t)(w >> 8) * (int)(int8_t)(c.s1 >> (8 * e)) +
+                                (int)(int8_t)(w >> 16) * (int)(int8_t)(c.s2 >> (8 * e)) +
+                                (int)(int8_t)(w >> 24) * (int)(int8_t)(c.x >> (8 * e));
+            o |= (uint32_t)(sqp_q(acc) & 255) << (8 * e);
+        }
+        *reinterpret_cast<uint32_t *>(xso + ch) = o;
+        *reinterpret_cast<uint32_t *>(st + ch) = c.s1;
+        *reinterpret_cast<uint32_t *>(st + g.D + ch) = c.s2;
+        *reinterpret_cast<uint32_t *>(st + 2 * g.D + ch) = c.x;
+        *reinterpret_cast<uint32_t *>(&s_xs[ch]) = o;
+    };
+    {
+        const ConvIn c = conv_load(min(4 * tid, C - 4));
+        if (4 * tid < C) conv_finish(c, 4 * tid);
+    }
+    for (int ch = 4 * tid + kPass; ch < C; ch += kPass) conv_finish(conv_load(ch), ch);
+    __syncthreads();
+
+    v4i acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
+    auto slice_mfma = [&](const v4i (&wv)[NT], int sl) {
+        const int w0 = 16 * sl + 4 * lq;   // this lane group's 4 words of the slice
+        v4i fb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            fb[j] = l16 == 0 ? *reinterpret_cast<const v4i *>(&s_xs[16 * (w0 + j)]) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t] = mfma_i8(unpack16((uint32_t)wv[t][j]), fb[j], acc[t]);
+    };
+    if (wave < nsl) slice_mfma(wv0, wave);
+    for (int sl = wave + 4; sl < nsl; sl += 4) {
+        v4i wv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wv[t] = *reinterpret_cast<const v4i *>(wrow[t] + 16 * sl);
+        slice_mfma(wv, sl);
+    }
+    // lanes of token column 0 (l16 == 0) hold outputs 16t + 4lq + r
+    if (l16 == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) *reinterpret_cast<v4i *>(&s_red[wave][16 * t + 4 * lq]) = acc[t];
+    }
+    __syncthreads();
+    const int used = min(4, nsl);
+    int32_t *dst = g.xpart + ((int64_t)m * kConvXParts + part) * g.nx;
+    for (int n = tid; n < g.nx; n += 256) {
+        int v = 0;
+        for (int w = 0; w < used; ++w) v += s_red[w][n];
+        dst[n] = v;
+    }
+}
+
 }  // namespace
 }  // namespace mi
+
+extern "C" mi_status mi_conv_step_xpart(const int8_t *xz, int xz_stride, const int8_t *conv_w,
+                                        const int32_t *conv_b, int8_t *conv_state, int8_t *xs,
+                                        const uint8_t *w_x, int nx, int32_t *xpart, int m, int d_inner,
+                                        void *stream) {
+    using namespace mi;
+    clear_error();
+    MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_conv_step_xpart: negative size");
+    MI_REQUIRE(d_inner % (256 * kConvXParts) == 0 && d_inner <= kConvXMaxD, MI_ERR_BAD_DIM,
+               "mi_conv_step_xpart: d_inner=%d must be a multiple of %d and <= %d", d_inner, 256 * kConvXParts,
+               kConvXMaxD);
+    MI_REQUIRE(nx >= 1 && nx <= 16 * kMaxXTiles, MI_ERR_BAD_DIM, "mi_conv_step_xpart: nx=%d outside [1,%d]", nx,
+               16 * kMaxXTiles);
+    MI_REQUIRE(xz_stride >= d_inner && xz_stride % 4 == 0, MI_ERR_BAD_DIM,
+               "mi_conv_step_xpart: xz_stride=%d must be >= d_inner and a multiple of 4", xz_stride);
+    if ((int64_t)m * d_inner == 0) return MI_OK;
+    MI_REQUIRE(xz && conv_w && conv_b && conv_state && xs && w_x && xpart, MI_ERR_NULL_POINTER,
+               "mi_conv_step_xpart: a required pointer is NULL");
+    MI_REQUIRE(aligned(xz, 4) && aligned(conv_w, 16) && aligned(conv_b, 16) && aligned(conv_state, 4) &&
+                   aligned(xs, 4) && aligned(w_x, 16) && aligned(xpart, 4),
+               MI_ERR_BAD_ALIGNMENT,
+               "mi_conv_step_xpart: xz, conv_state, xs, xpart 4-byte, conv_w, conv_b, w_x 16-byte aligned");
+    ConvXArgs g{};
+    g.xz = xz; g.xz_stride = xz_stride; g.conv_w = conv_w; g.conv_b = conv_b; g.conv_state = conv_state; g.xs = xs;
+    g.w_x = reinterpret_cast<const uint32_t *>(w_x); g.xpart = xpart;
+    g.M = m; g.D = d_inner; g.nx = nx;
+    const dim3 grid((unsigned)kConvXParts, (unsigned)m), block(256);
+    const hipStream_t hs = as_stream(stream);
+    const int nt = (nx + 15) / 16;
+    if (nt <= 2) hipLaunchKernelGGL(conv_step_xpart_kernel<2>, grid, block, 0, hs, g);
+    else if (nt <= 4) hipLaunchKernelGGL(conv_step_xpart_kernel<4>, grid, block, 0, hs, g);
+    else if (nt <= 6) hipLaunchKernelGGL(conv_step_xpart_kernel<6>, grid, block, 0, hs, g);
+    else if (nt <= 8) hipLaunchKernelGGL(conv_step_xpart_kernel<8>, grid, block, 0, hs, g);
+    else if (nt <= 10) hipLaunchKernelGGL(conv_step_xpart_kernel<10>, grid, block, 0, hs, g);
+    else if (nt <= 12) hipLaunchKernelGGL(conv_step_xpart_kernel<12>, grid, block, 0, hs, g);
+    else hipLaunchKernelGGL(conv_step_xpart_kernel<16>, grid, block, 0, hs, g);
+    return check_launch("mi_conv_step_xpart");
+}
 
 extern "C" mi_status mi_conv_step_xproj(const int8_t *xz, int xz_stride, const int8_t *conv_w,
                                         const int32_t *conv_b, int8_t *conv_state, int8_t *xs,

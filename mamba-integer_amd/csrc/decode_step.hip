@@ -25,7 +25,7 @@ constexpr size_t kAlign = 256;
 size_t up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct WsLayout {
-    size_t r, stats, parts, xz, xs, xp, yo, xpart, keys, a, logits, total;
+    size_t r, stats, parts, xz, xs, xp, yo, xpart, keys, a, logits, xq, total;
 };
 
 bool ssd(const mi_model_params &p) { return p.block == MI_BLOCK_SSD; }
@@ -49,6 +49,10 @@ bool batched(const mi_model_params &p, int m) {
     return !fused_ok && D % 256 == 0 && D <= 8192 && p.dt_rank + 2 * p.d_state <= 256;
 }
 
+// The batched stages' conv step leaves x_proj as int32 sums over four channel
+// quarters (mi_conv_step_xpart) where d_inner is a multiple of 1024.
+bool quarters(const mi_model_params &p) { return d_inner(p) % 1024 == 0; }
+
 // Sub-buffer offsets of the decode workspace for batch m.
 WsLayout ws_layout(const mi_model_params &p, int m) {
     const size_t d = p.d_model, D = d_inner(p), N = p.d_state, R = p.dt_rank, V = p.vocab_size;
@@ -67,6 +71,9 @@ WsLayout ws_layout(const mi_model_params &p, int m) {
         w.xp = o; o += up((size_t)m * dyadic_xp_width(p));
         w.a = o; o += up((size_t)m * d);
         w.logits = o; o += up((size_t)m * ((V + 3) / 4 * 4) * 4);
+        if (quarters(p)) {
+            w.xq = o; o += up((size_t)m * 4 * (R + 2 * N) * 4);
+        }
     } else {
         w.xpart = o; o += up((size_t)m * (D / 16) * (R + 2 * N) * 4);
     }
@@ -177,6 +184,7 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
     if (batched(p, m)) {
         int8_t *xp = reinterpret_cast<int8_t *>(base + w.xp);
         int8_t *a = reinterpret_cast<int8_t *>(base + w.a);
+        int32_t *xq = quarters(p) ? reinterpret_cast<int32_t *>(base + w.xq) : nullptr;
         // logits rows at a 16-byte multiple stride in the workspace (the GEMV stores 16 bytes a lane)
         int32_t *lg = reinterpret_cast<int32_t *>(base + w.logits);
         const int ldl = (p.vocab_size + 3) / 4 * 4;
@@ -187,10 +195,17 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
             else MI_STEP(mi_bitshift_norm_parts(r, ly.gamma, a, m, d, parts, P, 0, stream));
             MI_STEP(mi_bitlinear_gemv(a, d, ly.w_in, xz, 2 * D, MI_OUT_INT8, m, 2 * D, d, ly.s_in, 0, 0, nullptr, 0.0f,
                                       nullptr, stream));
-            MI_STEP(mi_conv_step_xproj(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], xs, ly.w_x, ly.s_x, nx, xp, W,
-                                       m, D, stream));
-            MI_STEP(mi_dt_scan_step(xp, W, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base, ly.decay_shift, ly.s_y,
-                                    h_state[l], yo, m, D, N, stream));
+            if (quarters(p)) {
+                MI_STEP(mi_conv_step_xpart(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], xs, ly.w_x, nx, xq, m, D,
+                                           stream));
+                MI_STEP(mi_xpart_dt_scan_step(xq, 4, ly.s_x, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base,
+                                              ly.decay_shift, ly.s_y, h_state[l], yo, m, D, N, stream));
+            } else {
+                MI_STEP(mi_conv_step_xproj(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], xs, ly.w_x, ly.s_x, nx, xp,
+                                           W, m, D, stream));
+                MI_STEP(mi_dt_scan_step(xp, W, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base, ly.decay_shift, ly.s_y,
+                                        h_state[l], yo, m, D, N, stream));
+            }
             MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
                                                 stream));
         }

@@ -50,6 +50,7 @@ SIGNATURES = {
     "mi_xpart_dt_scan_step": [P, I, I, I, P, I, P, P, I, I, P, I, I, P, P, I, I, I, P],
     "mi_bitshift_norm_parts": [P, P, P, I, I, P, I, I, P],
     "mi_conv_step_xproj": [P, I, P, P, P, P, P, I, I, P, I, I, I, P],
+    "mi_conv_step_xpart": [P, I, P, P, P, P, P, I, P, I, I, P],
     "mi_norm_bitlinear_argmax": [P, P, I, P, P, P, I, P, I, I, I, P],
     "mi_argmax_keys": [P, I, P, I, P],
     "mi_embed_argmax": [P, I, P, P, P, I, I, I, P, I, P],

@@ -113,6 +113,9 @@ class _Workspace:
         nx = dims.dt_rank + 2 * dims.d_state
         self.xpart = (torch.empty((T, D // 16, nx), dtype=torch.int32, device=device)
                       if T <= 64 and (D // 16) * nx <= 8192 else None)
+        # the batched decode step's x_proj sums over the four channel quarters
+        self.xq = (torch.empty((T, 4, nx), dtype=torch.int32, device=device)
+                   if T <= 1024 and D % 1024 == 0 and D <= 8192 and nx <= 256 else None)
 
 
 class IntegerMambaRunner:
@@ -176,11 +179,19 @@ class IntegerMambaRunner:
         ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
         step = L == 1 and not fresh
         if step and self._conv_xproj_ok():
-            # one recurrent step per sequence: conv step + x_proj (one block per token),
+            # one recurrent step per sequence: conv step + x_proj (four blocks per token
+            # leaving int32 partials where d_inner allows, else one block per token),
             # then dt_proj + scan step + gate
-            ops.conv_step_xproj(ws.xz, D, ly.conv_w, ly.conv_b, conv_state, ly.w_x, ly.s_x, dims.xp_width,
-                                xs=ws.xs, xp=ws.xp)
-            ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
+            if ws.xq is not None:
+                ops.conv_step_xpart(ws.xz, D, ly.conv_w, ly.conv_b, conv_state, ly.w_x, dims.xp_width,
+                                    xs=ws.xs, xpart=ws.xq)
+                ops.xpart_dt_scan_step(ws.xq, ly.s_x, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k,
+                                       ly.s_y, h_state, ws.yo)
+            else:
+                ops.conv_step_xproj(ws.xz, D, ly.conv_w, ly.conv_b, conv_state, ly.w_x, ly.s_x, dims.xp_width,
+                                    xs=ws.xs, xp=ws.xp)
+                ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state,
+                                 ws.yo)
             if self._step_parts(ws):
                 # the next norm sums these per-16-feature statistics partials
                 ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)

@@ -314,6 +314,25 @@ def conv_step_xproj(xz, d_inner: int, conv_w, conv_b, conv_state, w_x, s_x: int,
     return xs, xp
 
 
+def conv_step_xpart(xz, d_inner: int, conv_w, conv_b, conv_state, w_x, nx: int, xs=None, xpart=None):
+    """Decode stage: conv step + squareplus of the x half of xz (int8 [m, >= d_inner]) with
+    the conv state updated in place -> xs, and the exact int32 x_proj sums over the four
+    channel quarters -> xpart [m, 4, nx] (finished by xpart_dt_scan_step)."""
+    _req(xz, torch.int8, "xz"); _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
+    _req(conv_state, torch.int8, "conv_state"); _req(w_x, torch.uint8, "w_x")
+    m = xz.shape[0]
+    if xs is None:
+        xs = torch.empty((m, d_inner), dtype=torch.int8, device=xz.device)
+    if xpart is None:
+        xpart = torch.empty((m, 4, nx), dtype=torch.int32, device=xz.device)
+    _req(xs, torch.int8, "xs"); _req(xpart, torch.int32, "xpart")
+    if tuple(xs.shape) != (m, d_inner) or tuple(xpart.shape) != (m, 4, nx):
+        raise ValueError(f"xs must be [{m}, {d_inner}] and xpart [{m}, 4, {nx}]")
+    _lib.call("mi_conv_step_xpart", _ptr(xz), xz.shape[-1], _ptr(conv_w), _ptr(conv_b), _ptr(conv_state), _ptr(xs),
+              _ptr(w_x), nx, _ptr(xpart), m, d_inner, _stream())
+    return xs, xpart
+
+
 def xpart_dt_scan_step(xpart, s_x: int, dt_rank: int, w_dt, s_dt: int, xs, z, z_off: int, base,
                        decay_shift: int, s_y: int, h_state, yo) -> None:
     """Decode stage: x_proj from per-block partials + dt_proj + decay + dt + scan step + gate -> yo."""

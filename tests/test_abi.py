@@ -70,6 +70,12 @@ def _fake(n=64):
     (("mi_conv_step_xproj", None, 512, None, None, None, None, None, 5, 300, None, 300, 4, 512, None), 2, "nx=300"),
     (("mi_conv_step_xproj", None, 512, None, None, None, None, None, 31, 80, None, 80, 4, 512, None), 4, "s_x=31"),
     (("mi_conv_step_xproj", None, 512, None, None, None, None, None, 5, 80, None, 80, 4, 512, None), 1, "required"),
+    (("mi_conv_step_xpart", None, 512, None, None, None, None, None, 80, None, 4, 512, None), 2, "multiple of 1024"),
+    (("mi_conv_step_xpart", None, 16384, None, None, None, None, None, 80, None, 4, 16384, None), 2, "<= 8192"),
+    (("mi_conv_step_xpart", None, 1024, None, None, None, None, None, 300, None, 4, 1024, None), 2, "nx=300"),
+    (("mi_conv_step_xpart", None, 1000, None, None, None, None, None, 80, None, 4, 1024, None), 2, "xz_stride=1000"),
+    (("mi_conv_step_xpart", None, 1024, None, None, None, None, None, 80, None, 4, 1024, None), 1, "required"),
+    (("mi_conv_step_xpart", "A16", 1024, "W4", "A16", "A16", "A16", "A16", 80, "A16", 4, 1024, None), 3, "aligned"),
 ])
 def test_argument_validation(call, status, needle):
     from mamba_int import _lib

@@ -253,6 +253,51 @@ def test_conv_step_xproj_chain(cuda, m, D, N, R):
     assert np.array_equal(H(hg), h_ref)
 
 
+@pytest.mark.parametrize("m,D,N,R", [(64, 4096, 16, 128), (2, 1024, 16, 48), (5, 2048, 8, 16), (3, 8192, 16, 128),
+                                     (1, 1024, 16, 32), (9, 3072, 16, 64), (7, 1024, 10, 48), (33, 2048, 16, 128)])
+def test_conv_step_xpart_chain(cuda, m, D, N, R):
+    """The batched decode's conv step with x_proj left as int32 sums over four
+    channel quarters (mi_conv_step_xpart, four blocks per token), then the scan
+    step from those sums (mi_xpart_dt_scan_step, nblk 4), equals the unfused
+    oracle chain.  Covers quarters of one to eight 256-channel slices (fewer
+    slices than waves at D 1024 and 3072, two conv passes at D 8192), x_proj
+    rows not a multiple of 16, odd batches, one token, and nstate other than 16."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(7 * m + D + N + R)
+    NX = R + 2 * N
+    xz = i8(rng, m, 2 * D, lo=-128)
+    cw = i8(rng, D, 4)
+    cb = rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, m, 3, D)
+    wx_t = rng.integers(-1, 2, size=(NX, D), dtype=np.int8)
+    wx = pack_ternary(wx_t)
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    h0 = rng.integers(-(2**22), 2**22, size=(m, D, N), dtype=np.int32)
+    xs_ref, st_ref = O.conv_squareplus(xz.reshape(m, 1, 2 * D), D, cw, cb, st)
+    xs_ref = xs_ref[:, 0]
+    part_ref = np.einsum("nqc,iqc->iqn", wx_t.reshape(NX, 4, D // 4).astype(np.int64),
+                         xs_ref.reshape(m, 4, D // 4).astype(np.int64))
+    xp_ref = O.bitlinear(xs_ref, wx, O.OUT_INT8, 5)
+    dm = O.bitlinear(np.ascontiguousarray(xp_ref[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs_ref.reshape(m, 1, D), dm.reshape(m, 1, D), xp_ref.reshape(m, 1, NX), R,
+                                 xz.reshape(m, 1, 2 * D), D, base, 15, 13, h_state=h0)
+    stg = T(st)
+    xzg = T(xz)
+    xs = torch.full((m, D), 5, dtype=torch.int8, device="cuda")
+    xq = torch.full((m, 4, NX), 7, dtype=torch.int32, device="cuda")
+    ops.conv_step_xpart(xzg, D, T(cw), T(cb), stg, T(wx), NX, xs=xs, xpart=xq)
+    assert np.array_equal(H(xs), xs_ref)
+    assert np.array_equal(H(stg), st_ref)
+    assert np.array_equal(H(xq), part_ref)
+    hg = T(h0)
+    yo = T(np.zeros((m, D), np.int8))
+    ops.xpart_dt_scan_step(xq, 5, R, T(wdt), 2, xs, xzg, D, T(base), 15, 13, hg, yo)
+    assert np.array_equal(H(yo), yo_ref[:, 0])
+    assert np.array_equal(H(hg), h_ref)
+
+
 @pytest.mark.parametrize("m,n,k", [(8, 768, 1536), (1, 768, 1536), (16, 100, 512), (3, 2048, 4096), (5, 20, 256),
                                    (16, 64, 256 * 13), (4, 96, 1600)])
 def test_decode_residual_gemv(cuda, m, n, k):
