@@ -817,42 +817,54 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     }
     // the TPB x_proj rows (dt_raw, B, C): every byte load issued before the
     // first wait, from clamped in-bounds positions; staged into LDS below
+    // (XP: thread i < TPB*nxr/4 loads outputs 4i..4i+3 of every partial as
+    // 16-byte vectors; nxr is a multiple of 16, so a group never straddles
+    // two tokens or the dt_raw / B boundary)
     const int nxr = g.R + 32;
-    constexpr int kXpLoads = (TPB * (kMaxR + 32) + 255) / 256;
+    constexpr int kXpLoads = XP ? 1 : (TPB * (kMaxR + 32) + 255) / 256;
+    static_assert(!XP || TPB * (kMaxR + 32) / 4 <= 256, "one 4-output group per thread");
     int8_t xpv[kXpLoads];
-    int32_t xpp[XP ? kXpLoads : 1][XP ? kTokMaxParts : 1];
-#pragma unroll
-    for (int u = 0; u < kXpLoads; ++u) {
-        const int i = min((int)threadIdx.x + 256 * u, TPB * nxr - 1);
-        const int t = i / nxr, c = i - t * nxr;
+    v4i xq4[XP ? kTokMaxParts : 1];
+    if constexpr (XP) {
+        const int gi = min((int)threadIdx.x, TPB * nxr / 4 - 1);
+        const int t = 4 * gi / nxr, c = 4 * gi - t * nxr;
         const int mt = min(m0 + t, g.M - 1);
-        if constexpr (XP) {
 #pragma unroll
-            for (int b = 0; b < kTokMaxParts; ++b)
-                xpp[u][b] = g.xpart[((int64_t)mt * g.nblk + min(b, g.nblk - 1)) * nxr + c];
-        } else {
-            xpv[u] = g.xp[(int64_t)mt * g.xp_stride + c];
+        for (int b = 0; b < kTokMaxParts; ++b)
+            xq4[b] = *reinterpret_cast<const v4i *>(g.xpart + ((int64_t)mt * g.nblk + min(b, g.nblk - 1)) * nxr + c);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kXpLoads; ++u) {
+            const int i = min((int)threadIdx.x + 256 * u, TPB * nxr - 1);
+            const int t = i / nxr, c = i - t * nxr;
+            xpv[u] = g.xp[(int64_t)min(m0 + t, g.M - 1) * g.xp_stride + c];
         }
     }
     v4i wt[kMaxR / 64];
 #pragma unroll
     for (int i = 0; i < kMaxR / 64; ++i) wt[i] = unpack16(wdt[i]);  // words past kw are skipped below
+    if constexpr (XP) {
+        const int gi = (int)threadIdx.x;
+        if (gi < TPB * nxr / 4) {
+            const int t = 4 * gi / nxr, c = 4 * gi - t * nxr;
+            v4i sum = xq4[0];
 #pragma unroll
-    for (int u = 0; u < kXpLoads; ++u) {
-        const int i = (int)threadIdx.x + 256 * u;
-        if (i < TPB * nxr) {
-            const int t = i / nxr, c = i - t * nxr;
-            int8_t v;
-            if constexpr (XP) {
-                int32_t sum = xpp[u][0];
+            for (int b = 1; b < kTokMaxParts; ++b)
+                if (b < g.nblk) sum += xq4[b];
+            uint32_t q = 0;
 #pragma unroll
-                for (int b = 1; b < kTokMaxParts; ++b) sum += b < g.nblk ? xpp[u][b] : 0;
-                v = (int8_t)clamp32(rshr32(sum, g.s_x), -127, 127);
-            } else {
-                v = xpv[u];
+            for (int r = 0; r < 4; ++r) q |= (uint32_t)(clamp32(rshr32(sum[r], g.s_x), -127, 127) & 255) << (8 * r);
+            *reinterpret_cast<uint32_t *>(c < g.R ? &s_dt[t][c] : &s_bc[t][c - g.R]) = q;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kXpLoads; ++u) {
+            const int i = (int)threadIdx.x + 256 * u;
+            if (i < TPB * nxr) {
+                const int t = i / nxr, c = i - t * nxr;
+                if (c < g.R) s_dt[t][c] = xpv[u];
+                else s_bc[t][c - g.R] = xpv[u];
             }
-            if (c < g.R) s_dt[t][c] = v;
-            else s_bc[t][c - g.R] = v;
         }
     }
     if (threadIdx.x < 41) s_dtq[threadIdx.x] = tab_dt;
@@ -1121,7 +1133,7 @@ extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
     const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
     const bool vec = nstate == 16 && aligned(h_state, 16) && aligned(base, 16);
-    if (vec && nblk <= kTokMaxParts && m >= 2)
+    if (vec && nblk <= kTokMaxParts && m >= 2 && aligned(xpart, 16))
         // few partials (mi_conv_step_xpart's channel quarters): two tokens per block
         hipLaunchKernelGGL((dt_scan_tok_kernel<2, true>), dim3((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2)),
                            dim3(256), 0, as_stream(stream), g);

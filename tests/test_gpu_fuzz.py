@@ -122,3 +122,57 @@ def test_norm_and_conv_random_shapes(cuda, seed):
     sg = T(s0)
     xs = ops.conv_squareplus(T(xz), D, T(cw), T(cb), state_in=sg, state_out=sg)
     assert np.array_equal(H(xs), ref_xs) and np.array_equal(H(sg), ref_st)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_batched_decode_step_random_shapes(cuda, seed):
+    """The batched decode's conv + x_proj stages and the scan step that
+    finishes them: the int8-row form (mi_conv_step_xproj + mi_dt_scan_step)
+    at any d_inner multiple of 256, and the channel-quarter form
+    (mi_conv_step_xpart + mi_xpart_dt_scan_step) where d_inner is a multiple
+    of 1024, both against the unfused oracle chain with state carried."""
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(4000 + seed)
+    m = int(rng.integers(1, 65))
+    D = 256 * int(rng.integers(1, 17))
+    if seed % 2 == 0:
+        D = 1024 * int(rng.integers(1, 5))
+    N = int(rng.choice([8, 16, 16, 32]))
+    R = 16 * int(rng.integers(1, (256 - 2 * N) // 16 + 1))
+    NX = R + 2 * N
+    s_x, s_dt, s_y = int(rng.integers(2, 8)), int(rng.integers(0, 4)), int(rng.integers(8, 16))
+    xz = i8(rng, m, 2 * D, lo=-128)
+    cw = i8(rng, D, 4)
+    cb = rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, m, 3, D)
+    wx_t = rng.integers(-1, 2, size=(NX, D), dtype=np.int8)
+    wx = pack_ternary(wx_t)
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    h0 = rng.integers(-(2**24), 2**24, size=(m, D, N), dtype=np.int32)
+    xs_ref, st_ref = O.conv_squareplus(xz.reshape(m, 1, 2 * D), D, cw, cb, st)
+    xs_ref = xs_ref[:, 0]
+    xp_ref = O.bitlinear(xs_ref, wx, O.OUT_INT8, s_x)
+    dm = O.bitlinear(np.ascontiguousarray(xp_ref[:, :R]), wdt, O.OUT_DECAY_MOD, s_dt)
+    yo_ref, h_ref = O.block_scan(xs_ref.reshape(m, 1, D), dm.reshape(m, 1, D), xp_ref.reshape(m, 1, NX), R,
+                                 xz.reshape(m, 1, 2 * D), D, base, 15, s_y, h_state=h0)
+    forms = ["row"] + (["quarters"] if D % 1024 == 0 else [])
+    for form in forms:
+        stg, xzg = T(st), T(xz)
+        xs = torch.zeros((m, D), dtype=torch.int8, device="cuda")
+        hg = T(h0)
+        yo = T(np.zeros((m, D), np.int8))
+        if form == "row":
+            xp = torch.zeros((m, NX), dtype=torch.int8, device="cuda")
+            ops.conv_step_xproj(xzg, D, T(cw), T(cb), stg, T(wx), s_x, NX, xs=xs, xp=xp)
+            assert np.array_equal(H(xp), xp_ref), (form, m, D, N, R)
+            ops.dt_scan_step(xp, R, T(wdt), s_dt, xs, xzg, D, T(base), 15, s_y, hg, yo)
+        else:
+            xq = torch.zeros((m, 4, NX), dtype=torch.int32, device="cuda")
+            ops.conv_step_xpart(xzg, D, T(cw), T(cb), stg, T(wx), NX, xs=xs, xpart=xq)
+            ops.xpart_dt_scan_step(xq, s_x, R, T(wdt), s_dt, xs, xzg, D, T(base), 15, s_y, hg, yo)
+        assert np.array_equal(H(xs), xs_ref), (form, m, D, N, R)
+        assert np.array_equal(H(stg), st_ref), (form, m, D, N, R)
+        assert np.array_equal(H(yo), yo_ref[:, 0]), (form, m, D, N, R)
+        assert np.array_equal(H(hg), h_ref), (form, m, D, N, R)
