@@ -353,8 +353,8 @@ def main():
                     help="only 4 eager decode steps of the d2048 x 48 model at batch 64 (for a kernel trace)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs on one GPU only (the integer inference path has no "
-              "multi-GPU code; sharding is described in DESIGN.md)", file=sys.stderr)
+        print("bench.py: runs on one GPU only (the integer inference path has no multi-GPU code; "
+              "each GPU would decode its own batch slice of a replicated model)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

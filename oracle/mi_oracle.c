@@ -1,7 +1,7 @@
 /*
  * mi_oracle.c — CPU restatement of the integer Mamba inference path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: only tests/,
+ * TEST INFRASTRUCTURE ONLY. This library is the test oracle: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The
  * product (libmamba_int.so) never links, calls or falls back to it.
  *

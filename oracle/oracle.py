@@ -1,7 +1,7 @@
 """Python face of the CPU oracle (``mi_oracle.c``) — TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
-leg may import this module, and only as the checker or the timed CPU baseline.
+leg may import this module, and only as the test oracle or the timed CPU baseline.
 The product package never imports it.
 
 Each wrapper takes and returns numpy arrays; ``OracleModel`` orchestrates the
