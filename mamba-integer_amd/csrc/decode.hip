@@ -326,14 +326,16 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g0) {
         }
     }
 
-    // x_proj words of this block's 16 channels (x-blocks, wave 0)
+    // x_proj words of this block's 16 channels (x-blocks; wave w takes the 16-row tiles w, w+4, ...)
     const bool xpart = CONV && !WIDE && g.xpart != nullptr && n0 < g.conv_d;
-    uint32_t wx[kMaxXTiles];
-    if (xpart && wave == 0) {
+    uint32_t wx[kMaxXTiles / 4];
+    if (xpart) {
         const int xkw = g.conv_d / 16;
 #pragma unroll
-        for (int t = 0; t < kMaxXTiles; ++t)
-            wx[t] = 16 * t < g.nx ? g.w_x[(int64_t)min(16 * t + l16, g.nx - 1) * xkw + n0 / 16] : 0u;
+        for (int u = 0; u < kMaxXTiles / 4; ++u) {
+            const int t = 4 * u + wave;
+            wx[u] = 16 * t < g.nx ? g.w_x[(int64_t)min(16 * t + l16, g.nx - 1) * xkw + n0 / 16] : 0u;
+        }
     }
 
     stage_norm_rows(g, a, pitch, sp);
@@ -387,32 +389,33 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g0) {
         __shared__ uint32_t s_xs[16][4];
         reinterpret_cast<int8_t *>(&s_xs[m][lq])[wave] = (int8_t)xsv;
         __syncthreads();
-        if (wave != 0) return;
         const v4i fb = v4i{(int)s_xs[l16][lq], 0, 0, 0};
         const uint32_t lut = 0xFFFE0100u;
         const int nblk = g.conv_d / 16;
         int32_t *dst = g.xpart + ((int64_t)m * nblk + blockIdx.x) * g.nx;
         // every product first, then the stores back to back (a store between
         // two MFMAs would make the next wait on its completion)
-        v4i d[kMaxXTiles];
+        v4i d[kMaxXTiles / 4];
 #pragma unroll
-        for (int t = 0; t < kMaxXTiles; ++t) {
+        for (int u = 0; u < kMaxXTiles / 4; ++u) {
+            const int t = 4 * u + wave;
             if (16 * t < g.nx) {
-                const v4i fa = v4i{(int)__builtin_amdgcn_perm(lut, lut, (wx[t] >> (2 * lq)) & 0x03030303u), 0, 0, 0};
-                d[t] = mfma_i8(fa, fb, v4i{0, 0, 0, 0});
+                const v4i fa = v4i{(int)__builtin_amdgcn_perm(lut, lut, (wx[u] >> (2 * lq)) & 0x03030303u), 0, 0, 0};
+                d[u] = mfma_i8(fa, fb, v4i{0, 0, 0, 0});
             }
         }
         // lane (token l16, group lq) holds rows 16t + 4lq + r
         if (m < g.M) {
 #pragma unroll
-            for (int t = 0; t < kMaxXTiles; ++t) {
+            for (int u = 0; u < kMaxXTiles / 4; ++u) {
+                const int t = 4 * u + wave;
                 const int row = 16 * t + 4 * lq;
                 if (16 * t < g.nx) {
                     if ((g.nx & 3) == 0 && row + 3 < g.nx) {
-                        *reinterpret_cast<v4i *>(dst + row) = d[t];
+                        *reinterpret_cast<v4i *>(dst + row) = d[u];
                     } else {
                         for (int r = 0; r < 4; ++r)
-                            if (row + r < g.nx) dst[row + r] = d[t][r];
+                            if (row + r < g.nx) dst[row + r] = d[u][r];
                     }
                 }
             }
