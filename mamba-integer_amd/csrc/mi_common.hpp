@@ -60,7 +60,11 @@ __host__ __device__ __forceinline__ uint64_t isqrt64(uint64_t v) {
 // KMAX / KMIN: the table's count of "var >= 4^j" and "var < 4^-j" steps.
 template <int KMAX, int KMIN>
 __host__ __device__ __forceinline__ int norm_shift_tab(int64_t s1, int64_t s2, int dim, int64_t *mu_out) {
-    const int64_t mu = s1 >= 0 ? s1 / dim : -((-s1 + dim - 1) / dim);
+    // floor(s1 / dim) through one double division: |s1| < 2^36 (|r| < 2^23,
+    // dim <= 8192), so the rounded quotient is within 2^-17 of the exact one,
+    // which is an integer or at least 1/dim >= 2^-13 away from one; the floor
+    // is exact (and far shorter on the GPU than a 64-bit integer division)
+    const int64_t mu = (int64_t)floor((double)s1 / (double)dim);
     const int64_t S = s2 - 2 * mu * s1 + (int64_t)dim * mu * mu;
     int kk = 0;
     for (int j = 1; j <= KMAX; ++j) kk += S >= ((int64_t)dim << (2 * (j + 8)));
