@@ -72,10 +72,8 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 // LDS meanwhile.  Without: one wave per row sums the row in one pass.
 // Threads per row of the stats-driven staging: rows padded to a power of two
 // Mp, TPR = 256/Mp threads each.
-__device__ __forceinline__ int norm_tpr(int M) {
-    const int Mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
-    return 256 / Mp;
-}
+__device__ __forceinline__ int norm_tpr_log2(int M) { return M <= 1 ? 8 : M <= 2 ? 7 : M <= 4 ? 6 : M <= 8 ? 5 : 4; }
+__device__ __forceinline__ int norm_tpr(int M) { return 1 << norm_tpr_log2(M); }
 
 // Row statistics from stats_parts partials [M][P][2]: the RG = min(TPR, 64)
 // lanes of a row's lane group (aligned to RG within the wave) each take the
@@ -161,8 +159,8 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, con
     if (g.row_stats) {
         // TPR threads per row, each with its row's (mu, shift) in registers
         // and groups tr, tr+TPR, ...
-        const int TPR = norm_tpr(g.M);
-        const int m = (int)threadIdx.x / TPR, tr = (int)threadIdx.x - m * TPR;
+        const int lt = norm_tpr_log2(g.M), TPR = 1 << lt;   // shifts, not divides: ahead of the first loads
+        const int m = (int)threadIdx.x >> lt, tr = (int)threadIdx.x & (TPR - 1);
         const int mr = min(m, g.M - 1);
         const int K4 = g.K / 4;
         constexpr int kC = 8;
@@ -184,7 +182,7 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, con
         const int sh = norm_shift_args(g, s1, s2, &mu64);
         const int32_t mu = (int32_t)mu64;
         const int64_t rnd = (int64_t)1 << (sh - 1);
-        const int ngrp = (K4 + TPR - 1) / TPR;
+        const int ngrp = (K4 + TPR - 1) >> lt;
         for (int j0 = 0; j0 < ngrp; j0 += kC) {
             if (j0 > 0) load_chunk(j0);
 #pragma unroll
@@ -272,7 +270,7 @@ __global__ __launch_bounds__(256) void norm_gemv_kernel(NormGemvArgs g0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int l16 = lane & 15, lq = lane >> 4;
     // the row statistics of this thread's staging row, before any other load
-    const StatParts sp = load_stat_parts(g, min(tid / norm_tpr(g.M), g.M - 1));
+    const StatParts sp = load_stat_parts(g, min(tid >> norm_tpr_log2(g.M), g.M - 1));
     const int n0 = WIDE ? blockIdx.x * 64 + wave * 16 : blockIdx.x * 16;
     const int n = n0 + l16;
     const int nsuper = (g.kw + 15) / 16;
