@@ -281,7 +281,8 @@ mi_status mi_norm_v2_in_proj_conv(const int32_t *r, const int64_t *row_stats, in
  * [0,dt_rank), B, C after it); w_dt packed [d_inner, dt_rank/4]; xs int8
  * [m,d_inner]; z int8 [m,z_stride] at column z_off; base int32
  * [d_inner,nstate]; h_state int32 [m,d_inner,nstate] updated in place;
- * yo int8 [m,d_inner].  dt_rank % 16 == 0, <= 256; nstate <= 64. */
+ * yo int8 [m,d_inner].  dt_rank % 16 == 0, <= 256; nstate <= 64; m <= 65535
+ * (also for mi_xpart_dt_scan_step, mi_xproj_dt_scan_step, mi_conv_step_xpart). */
 mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_rank, const uint8_t *w_dt, int s_dt,
                           const int8_t *xs, const int8_t *z, int z_stride, int z_off, const int32_t *base,
                           int decay_shift, int s_y, int32_t *h_state, int8_t *yo, int m, int d_inner,

@@ -1076,6 +1076,7 @@ extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_ran
                                      int nstate, void *stream) {
     clear_error();
     MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_dt_scan_step: negative size");
+    MI_REQUIRE(m <= 65535, MI_ERR_BAD_DIM, "mi_dt_scan_step: m=%d exceeds 65535 tokens", m);
     MI_REQUIRE(dt_rank >= 16 && dt_rank % 16 == 0 && dt_rank <= kMaxR, MI_ERR_BAD_DIM,
                "mi_dt_scan_step: dt_rank=%d must be a multiple of 16 in [16,%d]", dt_rank, kMaxR);
     MI_REQUIRE(nstate >= 1 && nstate <= kMaxN, MI_ERR_BAD_DIM, "mi_dt_scan_step: nstate=%d outside [1,%d]", nstate,
@@ -1111,6 +1112,7 @@ extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s
                                            void *stream) {
     clear_error();
     MI_REQUIRE(m >= 0 && d_inner >= 0 && nblk >= 1, MI_ERR_BAD_DIM, "mi_xpart_dt_scan_step: bad size");
+    MI_REQUIRE(m <= 65535, MI_ERR_BAD_DIM, "mi_xpart_dt_scan_step: m=%d exceeds 65535 tokens", m);
     MI_REQUIRE(dt_rank >= 16 && dt_rank % 16 == 0 && dt_rank <= kMaxR, MI_ERR_BAD_DIM,
                "mi_xpart_dt_scan_step: dt_rank=%d must be a multiple of 16 in [16,%d]", dt_rank, kMaxR);
     MI_REQUIRE(nstate >= 1 && nstate <= kMaxN, MI_ERR_BAD_DIM, "mi_xpart_dt_scan_step: nstate=%d outside [1,%d]",
@@ -1151,6 +1153,7 @@ extern "C" mi_status mi_xproj_dt_scan_step(const int8_t *xs, const uint8_t *w_x,
                                            int8_t *yo, int m, int d_inner, int nstate, void *stream) {
     clear_error();
     MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_xproj_dt_scan_step: negative size");
+    MI_REQUIRE(m <= 65535, MI_ERR_BAD_DIM, "mi_xproj_dt_scan_step: m=%d exceeds 65535 tokens", m);
     MI_REQUIRE(d_inner % 32 == 0, MI_ERR_BAD_DIM, "mi_xproj_dt_scan_step: d_inner=%d must be a multiple of 32",
                d_inner);
     MI_REQUIRE(dt_rank >= 16 && dt_rank % 16 == 0 && dt_rank <= kMaxR, MI_ERR_BAD_DIM,
@@ -1411,6 +1414,7 @@ extern "C" mi_status mi_conv_step_xpart(const int8_t *xz, int xz_stride, const i
     using namespace mi;
     clear_error();
     MI_REQUIRE(m >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "mi_conv_step_xpart: negative size");
+    MI_REQUIRE(m <= 65535, MI_ERR_BAD_DIM, "mi_conv_step_xpart: m=%d exceeds 65535 tokens", m);
     MI_REQUIRE(d_inner % (256 * kConvXParts) == 0 && d_inner <= kConvXMaxD, MI_ERR_BAD_DIM,
                "mi_conv_step_xpart: d_inner=%d must be a multiple of %d and <= %d", d_inner, 256 * kConvXParts,
                kConvXMaxD);

@@ -75,6 +75,11 @@ def _fake(n=64):
     (("mi_conv_step_xpart", None, 1024, None, None, None, None, None, 300, None, 4, 1024, None), 2, "nx=300"),
     (("mi_conv_step_xpart", None, 1000, None, None, None, None, None, 80, None, 4, 1024, None), 2, "xz_stride=1000"),
     (("mi_conv_step_xpart", None, 1024, None, None, None, None, None, 80, None, 4, 1024, None), 1, "required"),
+    (("mi_conv_step_xpart", None, 1024, None, None, None, None, None, 80, None, 70000, 1024, None), 2, "65535"),
+    (("mi_dt_scan_step", None, 80, 48, None, 2, None, None, 3072, 1536, None, 15, 12, None, None, 70000, 1536, 16,
+      None), 2, "65535"),
+    (("mi_xpart_dt_scan_step", None, 96, 5, 48, None, 2, None, None, 3072, 1536, None, 15, 12, None, None, 70000,
+      1536, 16, None), 2, "65535"),
     (("mi_conv_step_xpart", "A16", 1024, "W4", "A16", "A16", "A16", "A16", 80, "A16", 4, 1024, None), 3, "aligned"),
 ])
 def test_argument_validation(call, status, needle):
