@@ -492,7 +492,8 @@ extern "C" mi_status mi_bitshift_norm_v2(const int32_t *r, const int16_t *gamma,
 extern "C" mi_status mi_bitshift_norm_parts(const int32_t *r, const int16_t *gamma, int8_t *out, int tokens,
                                             int dim, const int64_t *stats_parts, int nparts, int v2, void *stream) {
     clear_error();
-    MI_REQUIRE(tokens >= 0, MI_ERR_BAD_DIM, "mi_bitshift_norm_parts: negative tokens");
+    MI_REQUIRE(tokens >= 0 && tokens <= 65535, MI_ERR_BAD_DIM,
+               "mi_bitshift_norm_parts: tokens=%d outside [0,65535] (the grid's y dimension)", tokens);
     MI_REQUIRE(dim >= 4 && dim % 4 == 0 && dim <= 65536, MI_ERR_BAD_DIM,
                "mi_bitshift_norm_parts: dim=%d must be a multiple of 4 in [4,65536]", dim);
     MI_REQUIRE(nparts >= 1, MI_ERR_BAD_ARG, "mi_bitshift_norm_parts: nparts=%d must be >= 1", nparts);

@@ -171,8 +171,11 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
     in.d_model = (int)dm; in.n_layer = (int)nl; in.vocab_size = (int)vs; in.d_state = (int)ds; in.dt_rank = (int)dr;
     in.block = (int)blk; in.n_heads = ssd ? (int)nh : 0; in.d_head = ssd ? (int)dh : 0;
     MI_REQUIRE(in.logit_scale > 0.0f, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: logit_scale must be positive", path);
-    MI_REQUIRE(toff >= kHeaderBytes && toff + (uint64_t)nt * kEntryBytes <= b.size(), MI_ERR_BAD_ARG,
+    // range checks are written as subtractions so that no sum of header fields can wrap
+    const uint64_t size = b.size();
+    MI_REQUIRE(toff >= kHeaderBytes && toff <= size && (uint64_t)nt <= (size - toff) / kEntryBytes, MI_ERR_BAD_ARG,
                "mi_checkpoint_open: %s: tensor table outside the file", path);
+    const uint64_t table_end = toff + (uint64_t)nt * kEntryBytes;
     MI_REQUIRE(crc32_ieee(&b[toff], (size_t)nt * kEntryBytes) == tcrc, MI_ERR_BAD_ARG,
                "mi_checkpoint_open: %s: tensor table CRC mismatch", path);
 
@@ -193,12 +196,16 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
         MI_REQUIRE(t.ndim >= 1 && t.ndim <= 4 && elem_bytes(t.dtype) != 0, MI_ERR_BAD_ARG,
                    "mi_checkpoint_open: %s: tensor '%s': dtype %u / ndim %u invalid", path, name, t.dtype, t.ndim);
         uint64_t count = 1;
-        for (uint32_t j = 0; j < t.ndim; ++j) count *= t.shape[j];
-        MI_REQUIRE(t.nbytes == count * elem_bytes(t.dtype), MI_ERR_BAD_ARG,
+        bool fits = true;
+        for (uint32_t j = 0; j < t.ndim; ++j) {
+            fits = fits && (t.shape[j] == 0 || count <= UINT64_MAX / 8 / t.shape[j]);
+            count *= t.shape[j];
+        }
+        MI_REQUIRE(fits && t.nbytes == count * elem_bytes(t.dtype), MI_ERR_BAD_ARG,
                    "mi_checkpoint_open: %s: tensor '%s': %llu bytes for its shape", path, name,
                    (unsigned long long)t.nbytes);
-        MI_REQUIRE(t.offset % kDataAlign == 0 && t.offset >= toff + (uint64_t)nt * kEntryBytes &&
-                       t.offset + t.nbytes <= b.size(),
+        MI_REQUIRE(t.offset % kDataAlign == 0 && t.offset >= table_end && t.offset <= size &&
+                       t.nbytes <= size - t.offset,
                    MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: tensor '%s' at offset %llu: misaligned or outside the "
                    "file", path, name, (unsigned long long)t.offset);
         MI_REQUIRE(crc32_ieee(&b[t.offset], (size_t)t.nbytes) == crc, MI_ERR_BAD_ARG,

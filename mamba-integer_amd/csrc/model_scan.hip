@@ -644,11 +644,9 @@ hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z
     a.B = B; a.L = L; a.D = D; a.s_y = s_y;
     // lanes per channel: 8 at N=16 (1536 waves at d_inner 1536 x batch 8; measured
     // 0.39 ms against 0.44 ms at 4 and 0.41 ms at 16), otherwise the smallest
-    // split whose LDS staging fits; MI_SCAN_G overrides
+    // split whose LDS staging fits
     const int gmin = N <= 16 ? 4 : (N <= 32 ? 8 : 16);
-    const char *env = getenv("MI_SCAN_G");
-    int G = env ? atoi(env) : (N == 16 ? 8 : gmin);
-    if ((G != 4 && G != 8 && G != 16) || G < gmin) G = gmin;
+    const int G = N == 16 ? 8 : gmin;
     switch (N) {
         case 16: return launch_model_n<16>(G, a, st);
         case 32: return launch_model_n<32>(G, a, st);

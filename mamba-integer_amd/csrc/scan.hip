@@ -348,17 +348,8 @@ __global__ __launch_bounds__(256) void scan_generic_kernel(ScanArgs a, int N) {
 }
 
 // ------------------------------------------------------------- dispatch
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
-
-// Lanes per channel: enough waves to cover the 1024 SIMDs when possible,
-// overridable with MI_SCAN_G for tuning.
+// Lanes per channel: enough waves to cover the 1024 SIMDs when possible.
 int pick_g(int N, int64_t channels) {
-    int forced = env_int("MI_SCAN_G", 0);
-    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)
-        if (N % forced == 0 && N / forced <= 32) return forced;
     int g = 1;
     while (g < 16 && N % (2 * g) == 0 && (N / g > 32 || channels * g / 64 < 1024)) g *= 2;
     return g;
@@ -409,9 +400,7 @@ bool fast_shape(int N, int P, int k, int mode) {
     // k = 15 only: hl*n < 2^15 * (2^15 + 1) < 2^31, so the product's sign bit is
     // clear (the compiler lowers the unsigned shift of the 24-bit product to an
     // arithmetic shift, which is exact only then), and sum C*hh stays in int32.
-    if (k != 15) return false;
-    if (getenv("MI_SCAN_GENERIC")) return false;
-    return true;
+    return k == 15;
 }
 
 // ------------------------------------------------ float-compat reference
@@ -539,7 +528,7 @@ extern "C" mi_status mi_block_scan(const int8_t *xs, const int8_t *dm, const int
                       aligned(a.z, 16) && aligned(a.bsrc, 16) && aligned(a.csrc, 16) && aligned(yo, 16) &&
                       xp_stride % 16 == 0 && z_stride % 16 == 0;
     hipError_t e;
-    if (fast && nstate != 128 && !getenv("MI_MODEL_SCAN_V1"))
+    if (fast && nstate != 128)
         e = launch_model_scan(xs, dm, a.z, a.bsrc, a.csrc, base, yo, h_in, h_out, d_inner, z_stride, xp_stride, batch,
                               len, d_inner, nstate, s_y, as_stream(stream));
     else

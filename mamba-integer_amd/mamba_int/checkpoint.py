@@ -172,7 +172,7 @@ def load(path: str) -> Tuple[ModelParams, float]:
             raise CheckpointError(f"{path}: tensor {name!r}: dtype {code} / ndim {ndim} invalid")
         shape = (s0, s1, s2, s3)[:ndim]
         dt = np.dtype(_DTYPES[code]).newbyteorder("<")
-        if nbytes != int(np.prod(shape)) * dt.itemsize:
+        if nbytes != math.prod(shape) * dt.itemsize:
             raise CheckpointError(f"{path}: tensor {name!r}: {nbytes} bytes for its shape")
         if off % ALIGN or off < toff + nt * _ENTRY.size or off + nbytes > len(b):
             raise CheckpointError(f"{path}: tensor {name!r}: misaligned or outside the file")

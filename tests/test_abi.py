@@ -63,6 +63,7 @@ def _fake(n=64):
     (("mi_dt_scan_step", None, 80, 40, None, 2, None, None, 32, 16, None, 15, 13, None, None, 1, 16, 16, None), 2, "dt_rank"),
     (("mi_argmax_i32", None, 10, None, 1, 20, None), 2, "ld"),
     (("mi_bitshift_norm_parts", None, None, None, 4, 6, None, 1, 0, None), 2, "multiple of 4"),
+    (("mi_bitshift_norm_parts", None, None, None, 70000, 8, None, 1, 0, None), 2, "65535"),
     (("mi_bitshift_norm_parts", None, None, None, 4, 8, None, 0, 0, None), 4, "nparts=0"),
     (("mi_bitshift_norm_parts", "A16", "A16", "A16", 4, 8, "W4", 2, 0, None), 3, "aligned"),
     (("mi_conv_step_xproj", None, 256, None, None, None, None, None, 5, 80, None, 80, 4, 100, None), 2, "multiple of 256"),

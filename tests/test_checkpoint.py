@@ -125,6 +125,51 @@ def test_corrupt_files_are_rejected(tmp_path, case, needle):
     assert st != 0 and needle in msg, msg
 
 
+@pytest.mark.parametrize("nt", [200_000, 40_000_000])
+def test_wrapping_table_offset_is_rejected(tmp_path, nt):
+    """A table offset chosen so that offset + count * 96 wraps past 2^64 to a
+    small number is refused as outside the file, before any byte of the table
+    is read (the CRC pass would otherwise read far outside the buffer)."""
+    p = _params()
+    path = tmp_path / "m.miq"
+    ckpt.save(p, str(path), 1.0)
+    b = bytearray(path.read_bytes())
+    struct.pack_into("<I", b, 52, nt)
+    struct.pack_into("<Q", b, 56, (1 << 64) - nt * 96 + 128)
+    path.write_bytes(bytes(b))
+    with pytest.raises(ckpt.CheckpointError, match="outside the file"):
+        ckpt.load(str(path))
+    st, msg = _native_open(path)
+    assert st != 0 and "outside the file" in msg, msg
+
+
+@pytest.mark.parametrize("what", ["offset", "shape"])
+def test_wrapping_tensor_entry_is_rejected(tmp_path, what):
+    """A table entry whose offset + bytes, or whose shape product, wraps past
+    2^64 is refused (the table CRC is rewritten, so only the range checks stand
+    in the way)."""
+    p = _params()
+    path = tmp_path / "m.miq"
+    ckpt.save(p, str(path), 1.0)
+    b = bytearray(path.read_bytes())
+    toff, nt = struct.unpack_from("<Q", b, 56)[0], struct.unpack_from("<I", b, 52)[0]
+    e = list(ckpt._ENTRY.unpack_from(b, toff))
+    if what == "offset":
+        e[7] = (1 << 64) - 256                   # offset + bytes wraps to bytes - 256
+        needle = "outside the file"
+    else:
+        e[2], e[3:7] = 4, [1 << 31, 1 << 31, 1 << 31, 1 << 3]   # product 2^96 wraps to 0
+        e[8] = 0
+        needle = "bytes for its shape"
+    ckpt._ENTRY.pack_into(b, toff, *e)
+    struct.pack_into("<I", b, 76, zlib.crc32(bytes(b[toff:toff + 96 * nt])))
+    path.write_bytes(bytes(b))
+    with pytest.raises(ckpt.CheckpointError, match=needle):
+        ckpt.load(str(path))
+    st, msg = _native_open(path)
+    assert st != 0 and needle in msg, msg
+
+
 def test_rewritten_tensor_with_valid_crc_loads(tmp_path):
     """_rewrite (used to plant damage behind valid CRCs) keeps a file valid when
     it changes nothing, and the readers see a changed but valid byte."""
