@@ -284,6 +284,40 @@ def embed(ids, emb):
 
 
 # ------------------------------------------------------------------ model
+# Wiring mutations of OracleModel (tests plant them to show that the
+# whole-model fixtures catch each one; never set outside tests):
+#   "swap_xz"        the conv takes the z half and the gate the x half
+#   "norm_f_v2"      the final norm uses the BitShiftNormV2 table
+#   "block_norm_v1"  the SSD block's norm uses the BitShiftNorm table
+#   "no_residual"    a block returns out * res_gate without the residual
+#   "conv_reset"     the recurrent step forgets the conv ring
+_WIRING = {"swap_xz", "norm_f_v2", "block_norm_v1", "no_residual", "conv_reset"}
+_wiring_mutation: Optional[str] = None
+
+
+def set_wiring_mutation(m: Optional[str]) -> None:
+    global _wiring_mutation
+    if m is not None and m not in _WIRING:
+        raise ValueError(f"unknown wiring mutation {m!r}")
+    _wiring_mutation = m
+
+
+def _xz_wired(xz: np.ndarray, D: int) -> np.ndarray:
+    if _wiring_mutation == "swap_xz":
+        return np.ascontiguousarray(np.concatenate([xz[..., D:], xz[..., :D]], axis=-1))
+    return xz
+
+
+def _residual(r: np.ndarray) -> np.ndarray:
+    return np.zeros_like(r) if _wiring_mutation == "no_residual" else r
+
+
+def _conv_in(state: Optional["LayerState"]):
+    if state is None or _wiring_mutation == "conv_reset":
+        return None
+    return state.conv
+
+
 @dataclass
 class LayerState:
     conv: np.ndarray   # int8 [B,3,D]
@@ -305,29 +339,27 @@ class OracleModel:
         if dm_.ssd:
             return self._layer_ssd(lp, r, B, L, state)
         a = bitshift_norm(r, lp.gamma)
-        xz = bitlinear(a, lp.w_in, OUT_INT8, lp.s_in)                       # [T, 2D]
-        xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b,
-                                         None if state is None else state.conv)
+        xz = _xz_wired(bitlinear(a, lp.w_in, OUT_INT8, lp.s_in), D)        # [T, 2D]
+        xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b, _conv_in(state))
         xp = bitlinear(xs.reshape(T, D), lp.w_x, OUT_INT8, lp.s_x)          # [T, R+2N]
         dmod = bitlinear(np.ascontiguousarray(xp[:, :R]), lp.w_dt, OUT_DECAY_MOD, lp.s_dt)
         yo, h = block_scan(xs, dmod.reshape(B, L, D), xp.reshape(B, L, -1), R,
                            xz.reshape(B, L, 2 * D), D, lp.base, lp.k, lp.s_y,
                            None if state is None else state.h)
-        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=r,
+        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=_residual(r),
                       res_mult=lp.res_mult, res_shift=lp.res_shift)
         return r, LayerState(conv=conv_state, h=h)
 
     def _layer_ssd(self, lp, r, B, L, state: Optional[LayerState]):
         """MambaIntegerBlockV2 (spec section 7)."""
         D, T = self.dims.d_inner, B * L
-        a = bitshift_norm_v2(r, lp.gamma)
-        xz = bitlinear(a, lp.w_in, OUT_INT8, lp.s_in)
-        xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b,
-                                         None if state is None else state.conv)
+        a = (bitshift_norm if _wiring_mutation == "block_norm_v1" else bitshift_norm_v2)(r, lp.gamma)
+        xz = _xz_wired(bitlinear(a, lp.w_in, OUT_INT8, lp.s_in), D)
+        xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b, _conv_in(state))
         xp = bitlinear(xs.reshape(T, D), lp.w_x, OUT_INT8, lp.s_x)
         yo, h = ssd_v2_scan(xs, xp.reshape(B, L, -1), xz.reshape(B, L, 2 * D), D, lp.decay_tab, lp.s_y,
                             self.dims.n_heads, self.dims.d_state, None if state is None else state.h)
-        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=r,
+        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=_residual(r),
                       res_mult=lp.res_mult, res_shift=lp.res_shift)
         return r, LayerState(conv=conv_state, h=h)
 
@@ -341,7 +373,7 @@ class OracleModel:
             new_states.append(st)
         if last_only:
             r = np.ascontiguousarray(r.reshape(B, L, -1)[:, -1, :])
-        a = bitshift_norm(r, self.p.gamma_f)
+        a = (bitshift_norm_v2 if _wiring_mutation == "norm_f_v2" else bitshift_norm)(r, self.p.gamma_f)
         logits = bitlinear(a, self.p.w_head, OUT_INT32)
         return logits, new_states
 

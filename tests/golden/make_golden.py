@@ -132,6 +132,281 @@ def block_scan(xs, dm, xp, R, z, base, k, s_y, h0):
     return yo, hs.astype(np.int32)
 
 
+# --------------------------------------------------------------- whole model
+# A second statement of the model's composition, in Python integers and lists,
+# following the reference forward passes line by line:
+#   MambaIntegerModel.forward     mamba_integer_model.py:486-495
+#   MambaIntegerBlock.forward     mamba_integer_model.py:396-447
+#   MambaIntegerBlockV2.forward   ssd_multihead.py:523-592
+# with every float op replaced by its integer rule.  Generation recomputes the
+# whole prefix for every new token, as scripts/inference.py:147-161 does, so
+# the fixture also checks the recurrent decode (state carried across calls)
+# against a path that carries no state at all.
+
+def norm_row(row, gamma, v2):
+    """BitShiftNorm (mamba_integer_model.py:449-464, 144-184) or BitShiftNormV2
+    (ssd_multihead.py:595-632) of one residual row (Q8) -> int8 Q4."""
+    d = len(row)
+    mu = sum(row) // d                                   # x - x.mean()  (:463)
+    xc = [v - mu for v in row]
+    S = sum(v * v for v in xc)                           # var = mean(x^2) -> S = d * var * 2^16
+    up, down = (6, 2) if v2 else (8, 3)                  # table length of each variant
+    k = sum(1 for j in range(1, up + 1) if S >= d * 4 ** (j + 8)) - \
+        sum(1 for j in range(1, down + 1) if S < d * 4 ** (8 - j))
+    NORM_K_SEEN.add((v2, k))
+    return [sat(rshr(v * g, 12 + k), -127, 127) for v, g in zip(xc, gamma)]
+
+
+NORM_K_SEEN = set()   # (table, shift) pairs met while writing a fixture
+NORM_F_K = set()      # shifts of the final norm
+RES_SAT = [0]         # residual updates that hit the saturation bound
+
+
+def ternary_rows(a_rows, w):
+    """int8 rows x ternary [N][K] -> exact int32 rows (F.linear, rational_bitnet.py:204)."""
+    return [[sum(x * wv for x, wv in zip(a, wr) if wv) for wr in w] for a in a_rows]
+
+
+def depthwise_causal_conv(xcols, w, bias):
+    """nn.Conv1d(D, D, 4, groups=D, padding=3)(x)[..., :L] (mamba_integer_model.py:378,404)
+    over one sequence's rows [L][D]: position t sees x[t-3..t], zeros before 0."""
+    L, D = len(xcols), len(xcols[0])
+    out = []
+    for t in range(L):
+        row = []
+        for ch in range(D):
+            acc = bias[ch]
+            for j in range(4):
+                s = t - 3 + j
+                if s >= 0:
+                    acc += w[ch][j] * xcols[s][ch]
+            row.append(acc)
+        out.append(row)
+    return out
+
+
+def unit_q7(v):
+    """B / (||B|| + 1e-6) (ssd_multihead.py:552-553) as Q7 int8."""
+    S = sum(x * x for x in v)
+    if S == 0:
+        return [0] * len(v)
+    inv = (1 << 30) // math.isqrt(S << 16)
+    return [sat(rshr(x * inv, 15), -127, 127) for x in v]
+
+
+def block_dyadic(P, rows_seq):
+    """MambaIntegerBlock.forward (mamba_integer_model.py:396-447) on one
+    sequence of residual rows [L][d] (Q8); returns the new rows."""
+    D, N, R = P["D"], P["N"], P["R"]
+    hs = [norm_row(r, P["gamma"], False) for r in rows_seq]                       # :398
+    xz = [[sat(rshr(v, P["s_in"]), -127, 127) for v in row] for row in ternary_rows(hs, P["w_in"])]   # :400
+    x = [row[:D] for row in xz]                                                   # :401 x, z = chunk(2)
+    z = [row[D:] for row in xz]
+    xc = depthwise_causal_conv(x, P["conv_w"], P["conv_b"])                       # :404
+    xs = [[squareplus(v) for v in row] for row in xc]                             # :410-411 (clamp inside)
+    xp = [[sat(rshr(v, P["s_x"]), -127, 127) for v in row] for row in ternary_rows(xs, P["w_x"])]   # :414
+    dt = [row[:R] for row in xp]                                                  # :415 split dt, B, C
+    Bm = [row[R:R + N] for row in xp]
+    Cm = [row[R + N:R + 2 * N] for row in xp]
+    dmod = [[sat(rshr(v, P["s_dt"]), -20, 20) for v in row] for row in ternary_rows(dt, P["w_dt"])]   # :419-422
+    h = [[0] * N for _ in range(D)]
+    out_rows = []
+    for t in range(len(rows_seq)):
+        yo = []
+        for ch in range(D):
+            dm = dmod[t][ch]
+            dtq = dt_q16(dm)                                                      # :427
+            xd = rshr(xs[t][ch] * dtq, 10)                                        # :428 u = x*dt (x) B
+            y = 0
+            for n in range(N):
+                nt = sat(P["base"][ch][n] + dm, 0, 32000)                         # :424
+                h[ch][n] = sat((h[ch][n] * nt) // (1 << P["k"]) + Bm[t][n] * xd, -2**31, 2**31 - 1)   # :436
+                y += Cm[t][n] * h[ch][n]                                          # :440 y = h @ C
+            y = sat(y, -2**31, 2**31 - 1)
+            yg = (y * gate_q15(z[t][ch])) >> 15                                   # :441-444
+            yo.append(sat(rshr(yg, P["s_y"]), -127, 127))
+        out_rows.append(yo)
+    acc = ternary_rows(out_rows, P["w_out"])                                      # :446 out_proj
+    return residual_update(rows_seq, acc, P)                                      # :447 residual + out*gate
+
+
+def residual_update(rows_seq, acc, P):
+    """residual + out * res_gate: Q8 rows, saturated to +-(2^23 - 1)."""
+    lim = (1 << 23) - 1
+    out = []
+    for rr, ar in zip(rows_seq, acc):
+        row = []
+        for r, a in zip(rr, ar):
+            v = r + rshr(a * P["res_mult"], P["res_shift"])
+            RES_SAT[0] += abs(v) > lim
+            row.append(sat(v, -lim, lim))
+        out.append(row)
+    return out
+
+
+def block_ssd(P, rows_seq):
+    """MambaIntegerBlockV2.forward (ssd_multihead.py:523-592) on one sequence
+    of residual rows [L][d] (Q8)."""
+    H, Pd, N = P["H"], P["Pd"], P["N"]
+    D = H * Pd
+    hs = [norm_row(r, P["gamma"], True) for r in rows_seq]                        # :528
+    xz = [[sat(rshr(v, P["s_in"]), -127, 127) for v in row] for row in ternary_rows(hs, P["w_in"])]   # :531
+    x = [row[:D] for row in xz]                                                   # :532
+    z = [row[D:] for row in xz]
+    xs = [[squareplus(v) for v in row] for row in depthwise_causal_conv(x, P["conv_w"], P["conv_b"])]   # :535-538
+    xp = [[sat(rshr(v, P["s_x"]), -127, 127) for v in row] for row in ternary_rows(xs, P["w_x"])]   # :541
+    h = [[[0] * N for _ in range(Pd)] for _ in range(H)]
+    lim_y = 100 << 18                                                             # :582 clamp(y, -100, 100)
+    out_rows = []
+    for t in range(len(rows_seq)):
+        yo = [0] * D
+        for hd in range(H):
+            bq = unit_q7(xp[t][hd * N:hd * N + N])                                # :546, :552
+            cq = unit_q7(xp[t][H * N + hd * N:H * N + hd * N + N])                # :547, :553
+            dec = P["decay_tab"][hd][xp[t][2 * H * N + hd] + 127]                 # :555-570 exp(A * softplus(dt))
+            for p in range(Pd):
+                ch = hd * Pd + p
+                y = 0
+                for n in range(N):
+                    h[hd][p][n] = sat((h[hd][p][n] * dec) // (1 << 15) + bq[n] * xs[t][ch], -2**31, 2**31 - 1)
+                    y += cq[n] * h[hd][p][n]
+                y = sat(sat(y, -2**31, 2**31 - 1), -lim_y, lim_y)
+                yg = (y * gate_q15(z[t][ch])) >> 15                               # :585 y * sigmoid_gate(z)
+                yo[ch] = sat(rshr(yg, P["s_y"]), -127, 127)
+        out_rows.append(yo)
+    acc = ternary_rows(out_rows, P["w_out"])                                      # :588
+    return residual_update(rows_seq, acc, P)                                      # :592
+
+
+def model_logits(M, ids_seq):
+    """MambaIntegerModel.forward (mamba_integer_model.py:486-495) on one
+    sequence: int32 logits at every position."""
+    rows = [[e << 4 for e in M["emb"][i]] for i in ids_seq]                       # :487 embedding (Q4 -> Q8)
+    for P in M["layers"]:                                                         # :488-491
+        rows = block_ssd(P, rows) if M["ssd"] else block_dyadic(P, rows)
+    seen = set(NORM_K_SEEN)
+    NORM_K_SEEN.clear()
+    a = [norm_row(r, M["gamma_f"], False) for r in rows]                          # :492 norm_f is a BitShiftNorm
+    NORM_F_K.update(k for _, k in NORM_K_SEEN)
+    NORM_K_SEEN.update(seen)
+    return ternary_rows(a, M["w_head"])                                           # :494 lm_head (scale > 0)
+
+
+def model_generate(M, ids_seq, n_new):
+    """Greedy continuation by full recompute of the prefix per token
+    (scripts/inference.py:148-160, argmax as sft_mamba_integer.py:138-141)."""
+    seq = list(ids_seq)
+    out = []
+    for _ in range(n_new):
+        last = model_logits(M, seq)[-1]
+        nxt = max(range(len(last)), key=lambda i: (last[i], -i))                  # first maximal index
+        out.append(nxt)
+        seq.append(nxt)
+    return out
+
+
+def decay_table(a_log):
+    """Per-head decay numerators for dt = q/16, q in [-127, 127]: round_half_even(
+    exp(A) * 2^15), A = clamp(clamp(A_log, -2.3, -0.01) * clamp(softplus(clamp(dt,
+    +-10)), 0.01, 10), -20, -0.001) (ssd_multihead.py:555-570), in Python floats."""
+    tab = []
+    for al in a_log:
+        a = min(max(al, -2.3), -0.01)
+        row = []
+        for q in range(-127, 128):
+            dt = min(max(q / 16.0, -10.0), 10.0)
+            sp = min(max(math.log1p(math.exp(dt)), 0.01), 10.0)
+            A = min(max(a * sp, -20.0), -0.001)
+            row.append(round(math.exp(A) * 32768.0))                               # round() is half to even
+        tab.append(row)
+    return tab
+
+
+def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
+    """A 2-layer model of one block type, its all-position logits on two
+    12-token prompts, and 8 greedy tokens per prompt.  res_shifts sets how
+    strongly each layer updates the residual."""
+    rng = np.random.default_rng(seed)
+    d, V, nl, L, n_new = 32, 96, 2, 12, 8
+    if ssd:
+        H, Pd, N = 2, 16, 16
+        D = H * Pd
+        W = -(-(2 * H * N + H) // 16) * 16
+    else:
+        D, N, R = 2 * d, 16, 16
+        W = R + 2 * N
+
+    def tern(n, k):
+        return rng.integers(-1, 2, size=(n, k), dtype=np.int8)
+
+    # half the vocabulary embeds to nearly constant rows (variance below 1/64,
+    # the low end of the norm tables), half to rows of full spread
+    emb = rng.integers(-64, 65, size=(V, d), dtype=np.int8)
+    emb[V // 2:] = np.clip(rng.integers(-60, 61, size=(V - V // 2, 1)) + rng.integers(-1, 2, size=(V - V // 2, d)),
+                           -127, 127)
+    arrays = {"emb": emb,
+              "gamma_f": rng.integers(200, 320, size=d, dtype=np.int16), "w_head": tern(V, d)}
+    M = {"ssd": ssd, "emb": arrays["emb"].tolist(), "gamma_f": arrays["gamma_f"].tolist(),
+         "w_head": arrays["w_head"].tolist(), "layers": []}
+    for i in range(nl):
+        la = {"gamma": rng.integers(200, 320, size=d, dtype=np.int16), "w_in": tern(2 * D, d),
+              "conv_w": rng.integers(-32, 33, size=(D, 4), dtype=np.int8),
+              "conv_b": rng.integers(-512, 513, size=D, dtype=np.int32), "w_out": tern(d, D)}
+        sc = {"s_in": 3, "s_x": 3, "s_y": s_y, "res_mult": res_mults[i], "res_shift": res_shifts[i]}
+        if ssd:
+            wx = tern(W, D)
+            wx[2 * H * N + H:] = 0
+            la["w_x"] = wx
+            la["a_log"] = rng.uniform(-2.3, -0.01, size=H)
+            la["decay_tab"] = np.array(decay_table(la["a_log"].tolist()), np.int32)
+            P = {"H": H, "Pd": Pd, "N": N, "k": 15}
+        else:
+            la["w_x"] = tern(W, D)
+            la["w_dt"] = tern(D, R)
+            la["base"] = rng.integers(16384, 32001, size=(D, N), dtype=np.int32)
+            sc["s_dt"] = 5
+            P = {"D": D, "N": N, "R": R, "k": 15}
+        P.update({k: v.tolist() for k, v in la.items() if k != "a_log"})
+        P.update(sc)
+        M["layers"].append(P)
+        for k, v in la.items():
+            arrays[f"l{i}_{k}"] = v
+        arrays[f"l{i}_scalars"] = np.array([sc[k] for k in sorted(sc)], np.int64)
+    ids = rng.integers(0, V, size=(2, L))
+    NORM_K_SEEN.clear()
+    NORM_F_K.clear()
+    RES_SAT[0] = 0
+    logits = np.array([model_logits(M, list(map(int, s))) for s in ids], np.int64)
+    logits_fk = set(NORM_F_K)          # final-norm shifts of the stored logits
+    gen = np.array([model_generate(M, list(map(int, s)), n_new) for s in ids], np.int64)
+    assert np.abs(logits).max() < 2**31
+    # packed forms for the loaders (2-bit layout of the packing fixture)
+    for k in list(arrays):
+        if k == "w_head" or k.endswith(("w_in", "w_x", "w_dt", "w_out")):
+            arrays[k + "_packed"] = pack(arrays[k])
+    arrays["scalar_names"] = np.array(sorted(sc))
+    np.savez_compressed(os.path.join(HERE, name), ids=ids, logits=logits.astype(np.int32), gen=gen, **arrays)
+    print(name, "distinct greedy tokens:", sorted(set(gen.ravel().tolist())), "norm shifts (v2, k):",
+          sorted(NORM_K_SEEN), "final norm k of the logits:", sorted(logits_fk), "saturated residual updates:", RES_SAT[0])
+    return NORM_K_SEEN, logits_fk, RES_SAT[0]
+
+
+def main_models():
+    # "small": varied greedy tokens that depend on the history; the final norm
+    # meets the bottom threshold (k = -3), where the two norm tables differ
+    _, fk, _ = model_fixture("model_dyadic_small.npz", False, 7307, (10, 9))
+    assert -3 in fk
+    _, fk, _ = model_fixture("model_ssd_small.npz", True, 7322, (12, 11))
+    assert -3 in fk
+    # "wide": strong residual updates that saturate, and final-norm shifts past
+    # the BitShiftNormV2 table's top (k = 7, 8); the greedy tokens of such a
+    # random model settle on one id, so the logits carry this fixture
+    ks, fk, nsat = model_fixture("model_dyadic_wide.npz", False, 7301, (6, 0), (4719, 32767), 10)
+    assert max(fk) >= 7 and nsat > 0
+    ks, fk, nsat = model_fixture("model_ssd_wide.npz", True, 7302, (8, 0), (4719, 32767), 10)
+    assert max(fk) >= 7 and nsat > 0
+
+
 def main():
     rng = np.random.default_rng(20261201)
 
@@ -192,3 +467,4 @@ def main():
 
 if __name__ == "__main__":
     main()
+    main_models()
