@@ -15,6 +15,7 @@ OpenMP on every host core) on a bounded sample of the same workload.
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--kernels]
     python bench.py --pmc-probe     # only the dominant kernel + a copy of known size, for rocprofv3 --pmc
     python bench.py --gemm-probe    # only the config-2 prefill GEMM (20 launches), for rocprofv3 counters
+    python bench.py --scan-probe    # only the scan kernels at their benchmark shapes, for rocprofv3 counters
 """
 import argparse
 import json
@@ -188,6 +189,47 @@ def pmc_probe():
     print(json.dumps({"pmc_probe": "done", "kernel_launches": 20, "copy_bytes": 256 << 20, "copies": 3}))
 
 
+def scan_probe():
+    """For rocprofv3 --pmc: the scan kernels at their benchmark shapes, each
+    launched a few times: the fused prefill block scan (B8, L2048, d_inner
+    1536, N16), the config-4 chunked scan (B4, L8192, 24 heads of 64, N128,
+    chunk 256) and the batch-64 decode scan step of the d2048 model (d_inner
+    4096, N16, x_proj from four channel-quarter partials)."""
+    import numpy as np
+    import torch
+    from mamba_int import ops, pack_ternary
+    dev = "cuda:0"
+    rng = np.random.default_rng(11)
+
+    def t8(*shape, lo=-127, hi=127):
+        return torch.from_numpy(rng.integers(lo, hi + 1, size=shape, dtype=np.int8)).to(dev)
+    B, L, D, N, R = 8, 2048, 1536, 16, 48
+    xs, dm, xp, z = t8(B, L, D, lo=0), t8(B, L, D, lo=-20, hi=20), t8(B, L, R + 2 * N), t8(B, L, 2 * D)
+    base = torch.from_numpy(rng.integers(16384, 32001, size=(D, N), dtype=np.int32)).to(dev)
+    h = torch.zeros((B, D, N), dtype=torch.int32, device=dev)
+    yo = torch.empty((B, L, D), dtype=torch.int8, device=dev)
+    for _ in range(5):
+        ops.block_scan(xs, dm, xp, R, z, D, base, 15, 14, h_out=h, out=yo)
+    B4, L4, H4, P4, N4 = 4, 8192, 24, 64, 128
+    x4, b4, c4 = t8(B4, L4, H4, P4), t8(B4, L4, H4, N4), t8(B4, L4, H4, N4)
+    n4 = torch.from_numpy(rng.integers(24576, 32768, size=(H4,), dtype=np.int32)).to(dev)
+    for _ in range(3):
+        ops.ssd_chunked_scan(x4, b4, c4, n4, 15, 256)
+    m, D5, R5 = 64, 4096, 128
+    xpart = torch.from_numpy(rng.integers(-3000, 3000, size=(m, 4, R5 + 32), dtype=np.int32)).to(dev)
+    w_dt = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(D5, R5), dtype=np.int8))).to(dev)
+    xs5, z5 = t8(m, D5, lo=0), t8(m, 2 * D5)
+    base5 = torch.from_numpy(rng.integers(16384, 32001, size=(D5, 16), dtype=np.int32)).to(dev)
+    h5 = torch.zeros((m, D5, 16), dtype=torch.int32, device=dev)
+    yo5 = torch.empty((m, D5), dtype=torch.int8, device=dev)
+    for _ in range(10):
+        ops.xpart_dt_scan_step(xpart, 8, R5, w_dt, 6, xs5, z5, D5, base5, 15, 14, h5, yo5)
+    torch.cuda.synchronize()
+    print(json.dumps({"scan_probe": "done", "block_scan_launches": 5, "block_scan_updates": B * L * D * N,
+                      "chunked_scan_launches": 3, "chunked_scan_updates": B4 * L4 * H4 * P4 * N4,
+                      "decode_scan_step_launches": 10, "decode_scan_step_updates": m * D5 * 16}))
+
+
 def decode5_probe():
     """For rocprofv3: the d2048 x 48 model (d_inner 4096, dt_rank 128) at batch
     64: a 16-token prefill, then 4 eager greedy decode steps (every layer's
@@ -349,6 +391,8 @@ def main():
     ap.add_argument("--kernels", action="store_true", help="also time each config's kernel")
     ap.add_argument("--pmc-probe", action="store_true", help="only the dominant kernel and a copy (for counters)")
     ap.add_argument("--gemm-probe", action="store_true", help="only the config-2 prefill GEMM (for counters)")
+    ap.add_argument("--scan-probe", action="store_true", help="only the scan kernels at their benchmark shapes "
+                    "(for counters)")
     ap.add_argument("--decode5-probe", action="store_true",
                     help="only 4 eager decode steps of the d2048 x 48 model at batch 64 (for a kernel trace)")
     args = ap.parse_args()
@@ -371,6 +415,9 @@ def main():
         return
     if args.decode5_probe:
         decode5_probe()
+        return
+    if args.scan_probe:
+        scan_probe()
         return
     dims = ModelDims(d_model=768, n_layer=24, vocab_size=32000, d_state=16, dt_rank=48)
     B, L, NDEC = 8, 2048, args.decode_steps

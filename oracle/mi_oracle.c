@@ -163,6 +163,39 @@ void mo_dyadic_scan_elementwise(const int32_t *u, const int32_t *n, int k, int32
     }
 }
 
+/* Chunked elementwise scan with the outputs of ssd_chunked_scan_forward
+ * (ssd_chunked_scan.py:382-422; chunk loop of ssd_intra_chunk_matmul_kernel,
+ * :346-379): h[t] = sat32(floor(h[t-1]*n[t] / 2^k) + u[t]) per (b, channel)
+ * over u, n int32 [B,L,C]; final_h[B,nc,C] (nullable) is h at the last step of
+ * every chunk of cs steps; decay_to_end[B,nc,C] (nullable) is the chunk's
+ * cumulative decay prod n[t]/2^k in Q30, rounded down after every step:
+ * p = 2^30, p = sat32(floor(p*n[t] / 2^k)) over the chunk's steps.
+ * hstate[B,C] nullable in/out. */
+void mo_dyadic_chunked_scan(const int32_t *u, const int32_t *n, int k, int cs, int32_t *h, int32_t *final_h,
+                            int32_t *decay_to_end, int32_t *hstate, int B, int L, int C) {
+    const int nc = (L + cs - 1) / cs;
+#pragma omp parallel for collapse(2) num_threads(g_threads) schedule(static)
+    for (int b = 0; b < B; ++b) {
+        for (int c = 0; c < C; ++c) {
+            int32_t s = hstate ? hstate[(int64_t)b * C + c] : 0;
+            for (int ci = 0; ci < nc; ++ci) {
+                int32_t p = 1 << 30;
+                const int t1 = (ci + 1) * cs < L ? (ci + 1) * cs : L;
+                for (int t = ci * cs; t < t1; ++t) {
+                    int64_t off = ((int64_t)b * L + t) * C + c;
+                    s = scan_step(s, n[off], k, u[off]);
+                    h[off] = s;
+                    p = sat32(floor_shr((int64_t)p * n[off], k));
+                }
+                int64_t co = ((int64_t)b * nc + ci) * C + c;
+                if (final_h) final_h[co] = s;
+                if (decay_to_end) decay_to_end[co] = p;
+            }
+            if (hstate) hstate[(int64_t)b * C + c] = s;
+        }
+    }
+}
+
 /* Chunked multi-head scan (config 4). x[B,L,H,P] i8, Bm/Cm[B,L,H,N] i8,
  * ndec[H] per-head decay numerator, shift k, chunk length cs.
  * y[B,L,H,P] i32; chunk_states[B,nc,H,P,N] (nullable) receives the state at
@@ -245,6 +278,7 @@ int mo_pack_ternary(const int8_t *w, uint8_t *p, int N, int K) {
     return bad;
 }
 void mo_unpack_ternary(const uint8_t *p, int8_t *w, int N, int K) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t n = 0; n < N; ++n)
         for (int wd = 0; wd < K / 16; ++wd) {
             const uint8_t *src = p + n * (K / 4) + 4 * wd;
@@ -269,6 +303,9 @@ static int32_t dot_i8(const int8_t *a, const int8_t *w, int K) {
  * F.linear on integer-valued fp32, rational_bitnet.py:204), then the output
  * kind of spec rule 3.  out: int32/int8/float [M,N] or the int32 residual
  * [M,N] updated in place.  x_scale[M] and w_scale only for MO_OUT_FLOAT. */
+void mo_bitlinear_unpacked(const int8_t *a, const int8_t *wu, void *out, int kind, int M, int N, int K, int shift,
+                           int32_t res_mult, int res_shift, const float *x_scale, float w_scale);
+
 void mo_bitlinear(const int8_t *a, const uint8_t *wp, void *out, int kind, int M, int N, int K,
                   int shift, int32_t res_mult, int res_shift, const float *x_scale, float w_scale) {
     int8_t *wu = (int8_t *)malloc((size_t)N * K);
@@ -281,7 +318,17 @@ void mo_bitlinear(const int8_t *a, const uint8_t *wp, void *out, int kind, int M
                 q[3] = t0;
             }
     }
-#pragma omp parallel for num_threads(g_threads) schedule(static)
+    mo_bitlinear_unpacked(a, wu, out, kind, M, N, K, shift, res_mult, res_shift, x_scale, w_scale);
+    free(wu);
+}
+
+/* The same with the weights already unpacked to int8 [N][K] (a caller that
+ * applies one matrix many times unpacks it once). */
+void mo_bitlinear_unpacked(const int8_t *a, const int8_t *wu, void *out, int kind, int M, int N, int K, int shift,
+                           int32_t res_mult, int res_shift, const float *x_scale, float w_scale) {
+    /* (row, output) pairs are independent: one flat loop keeps every thread busy
+     * at a single row (decode) as well as at many */
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
     for (int m = 0; m < M; ++m) {
         for (int n = 0; n < N; ++n) {
             int32_t acc = dot_i8(a + (int64_t)m * K, wu + (int64_t)n * K, K);
@@ -303,7 +350,6 @@ void mo_bitlinear(const int8_t *a, const uint8_t *wp, void *out, int kind, int M
             }
         }
     }
-    free(wu);
 }
 
 /* activation_quant_dynamic, 8 bits (rational_bitnet.py:102-111), fp32:

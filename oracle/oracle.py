@@ -58,9 +58,11 @@ def lib() -> ctypes.CDLL:
         L.mo_dyadic_scan_f32.argtypes = [P, P, P, P, I, I, I, I]
         L.mo_dyadic_scan_elementwise.argtypes = [P, P, I, P, P, I, I, I]
         L.mo_ssd_chunked_scan.argtypes = [P, P, P, P, I, P, P, P, I, I, I, I, I, I]
+        L.mo_dyadic_chunked_scan.argtypes = [P, P, I, I, P, P, P, P, I, I, I]
         L.mo_pack_ternary.argtypes = [P, P, I, I]
         L.mo_unpack_ternary.argtypes = [P, P, I, I]
         L.mo_bitlinear.argtypes = [P, P, P, I, I, I, I, I, ctypes.c_int32, I, P, ctypes.c_float]
+        L.mo_bitlinear_unpacked.argtypes = [P, P, P, I, I, I, I, I, ctypes.c_int32, I, P, ctypes.c_float]
         L.mo_act_quant_f32.argtypes = [P, P, P, I, I]
         L.mo_bitshift_norm.argtypes = [P, P, P, I, I]
         L.mo_squareplus_q.argtypes = [ctypes.c_int32]
@@ -130,6 +132,21 @@ def dyadic_scan_elementwise(u, n, k, h_state=None):
     return (h, hs) if h_state is not None else h
 
 
+def dyadic_chunked_scan(u, n, k, chunk, h_state=None):
+    """Chunked elementwise scan (the outputs of ssd_chunked_scan_forward): u, n
+    int32 [B,L,C] -> h [B,L,C], final_h [B,nc,C], decay_to_end [B,nc,C] (Q30),
+    and the final state when h_state is given."""
+    u, n = _c(u, np.int32), _c(n, np.int32)
+    B, L, C = u.shape
+    nc = -(-L // chunk)
+    h = np.empty_like(u)
+    fh = np.empty((B, nc, C), np.int32)
+    dte = np.empty((B, nc, C), np.int32)
+    hs = None if h_state is None else _c(h_state, np.int32).copy()
+    lib().mo_dyadic_chunked_scan(_p(u), _p(n), k, chunk, _p(h), _p(fh), _p(dte), _p(hs), B, L, C)
+    return (h, fh, dte, hs) if h_state is not None else (h, fh, dte)
+
+
 def ssd_chunked_scan(x, Bm, Cm, ndec, k, chunk, want_chunk_states=False, h_state=None):
     x, Bm, Cm, ndec = _c(x, np.int8), _c(Bm, np.int8), _c(Cm, np.int8), _c(ndec, np.int32)
     B, L, H, P = x.shape
@@ -170,7 +187,11 @@ def unpack_ternary(p, K):
 
 def bitlinear(a, wp, kind, shift=0, residual=None, res_mult=0, res_shift=0,
               x_scale=None, w_scale=0.0):
-    a, wp = _c(a, np.int8), _c(wp, np.uint8)
+    """BitLinear of int8 rows a [M,K] against packed ternary wp [N,K/4], or
+    against weights already unpacked to int8 [N,K] (same result)."""
+    a = _c(a, np.int8)
+    unpacked = wp.dtype == np.int8
+    wp = _c(wp, np.int8 if unpacked else np.uint8)
     M, K = a.shape
     N = wp.shape[0]
     if kind == OUT_INT32:
@@ -182,8 +203,8 @@ def bitlinear(a, wp, kind, shift=0, residual=None, res_mult=0, res_shift=0,
     else:
         out = np.empty((M, N), np.float32)
     xs = None if x_scale is None else _c(x_scale, np.float32)
-    lib().mo_bitlinear(_p(a), _p(wp), _p(out), kind, M, N, K, shift, int(res_mult), res_shift,
-                       _p(xs), ctypes.c_float(w_scale))
+    fn = lib().mo_bitlinear_unpacked if unpacked else lib().mo_bitlinear
+    fn(_p(a), _p(wp), _p(out), kind, M, N, K, shift, int(res_mult), res_shift, _p(xs), ctypes.c_float(w_scale))
     return out
 
 
@@ -331,6 +352,17 @@ class OracleModel:
     def __init__(self, params: ModelParams):
         self.p = params
         self.dims = params.dims
+        self._wu = {}   # packed matrix -> its int8 unpacking, made on first use
+
+    def _w(self, wp: np.ndarray) -> np.ndarray:
+        """The unpacked int8 form of a packed weight matrix of this model (the
+        model's parameters do not change during its life)."""
+        key = id(wp)
+        hit = self._wu.get(key)
+        if hit is None or hit[0] is not wp:
+            hit = (wp, unpack_ternary(wp, wp.shape[1] * 4))
+            self._wu[key] = hit
+        return hit[1]
 
     def _layer(self, lp, r, B, L, state: Optional[LayerState]):
         dm_ = self.dims
@@ -339,14 +371,14 @@ class OracleModel:
         if dm_.ssd:
             return self._layer_ssd(lp, r, B, L, state)
         a = bitshift_norm(r, lp.gamma)
-        xz = _xz_wired(bitlinear(a, lp.w_in, OUT_INT8, lp.s_in), D)        # [T, 2D]
+        xz = _xz_wired(bitlinear(a, self._w(lp.w_in), OUT_INT8, lp.s_in), D)        # [T, 2D]
         xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b, _conv_in(state))
-        xp = bitlinear(xs.reshape(T, D), lp.w_x, OUT_INT8, lp.s_x)          # [T, R+2N]
-        dmod = bitlinear(np.ascontiguousarray(xp[:, :R]), lp.w_dt, OUT_DECAY_MOD, lp.s_dt)
+        xp = bitlinear(xs.reshape(T, D), self._w(lp.w_x), OUT_INT8, lp.s_x)          # [T, R+2N]
+        dmod = bitlinear(np.ascontiguousarray(xp[:, :R]), self._w(lp.w_dt), OUT_DECAY_MOD, lp.s_dt)
         yo, h = block_scan(xs, dmod.reshape(B, L, D), xp.reshape(B, L, -1), R,
                            xz.reshape(B, L, 2 * D), D, lp.base, lp.k, lp.s_y,
                            None if state is None else state.h)
-        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=_residual(r),
+        r = bitlinear(yo.reshape(T, D), self._w(lp.w_out), OUT_RESIDUAL, residual=_residual(r),
                       res_mult=lp.res_mult, res_shift=lp.res_shift)
         return r, LayerState(conv=conv_state, h=h)
 
@@ -354,12 +386,12 @@ class OracleModel:
         """MambaIntegerBlockV2 (spec section 7)."""
         D, T = self.dims.d_inner, B * L
         a = (bitshift_norm if _wiring_mutation == "block_norm_v1" else bitshift_norm_v2)(r, lp.gamma)
-        xz = _xz_wired(bitlinear(a, lp.w_in, OUT_INT8, lp.s_in), D)
+        xz = _xz_wired(bitlinear(a, self._w(lp.w_in), OUT_INT8, lp.s_in), D)
         xs, conv_state = conv_squareplus(xz.reshape(B, L, 2 * D), D, lp.conv_w, lp.conv_b, _conv_in(state))
-        xp = bitlinear(xs.reshape(T, D), lp.w_x, OUT_INT8, lp.s_x)
+        xp = bitlinear(xs.reshape(T, D), self._w(lp.w_x), OUT_INT8, lp.s_x)
         yo, h = ssd_v2_scan(xs, xp.reshape(B, L, -1), xz.reshape(B, L, 2 * D), D, lp.decay_tab, lp.s_y,
                             self.dims.n_heads, self.dims.d_state, None if state is None else state.h)
-        r = bitlinear(yo.reshape(T, D), lp.w_out, OUT_RESIDUAL, residual=_residual(r),
+        r = bitlinear(yo.reshape(T, D), self._w(lp.w_out), OUT_RESIDUAL, residual=_residual(r),
                       res_mult=lp.res_mult, res_shift=lp.res_shift)
         return r, LayerState(conv=conv_state, h=h)
 
@@ -374,7 +406,7 @@ class OracleModel:
         if last_only:
             r = np.ascontiguousarray(r.reshape(B, L, -1)[:, -1, :])
         a = (bitshift_norm_v2 if _wiring_mutation == "norm_f_v2" else bitshift_norm)(r, self.p.gamma_f)
-        logits = bitlinear(a, self.p.w_head, OUT_INT32)
+        logits = bitlinear(a, self._w(self.p.w_head), OUT_INT32)
         return logits, new_states
 
     def forward(self, ids) -> np.ndarray:

@@ -327,9 +327,9 @@ def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
     12-token prompts, and 8 greedy tokens per prompt.  res_shifts sets how
     strongly each layer updates the residual."""
     rng = np.random.default_rng(seed)
-    d, V, nl, L, n_new = 32, 96, 2, 12, 8
+    d, V, nl, L, n_new = 64, 96, 2, 12, 8
     if ssd:
-        H, Pd, N = 2, 16, 16
+        H, Pd, N = 4, 16, 16
         D = H * Pd
         W = -(-(2 * H * N + H) // 16) * 16
     else:
@@ -394,9 +394,9 @@ def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
 def main_models():
     # "small": varied greedy tokens that depend on the history; the final norm
     # meets the bottom threshold (k = -3), where the two norm tables differ
-    _, fk, _ = model_fixture("model_dyadic_small.npz", False, 7307, (10, 9))
+    _, fk, _ = model_fixture("model_dyadic_small.npz", False, 7305, (11, 10))
     assert -3 in fk
-    _, fk, _ = model_fixture("model_ssd_small.npz", True, 7322, (12, 11))
+    _, fk, _ = model_fixture("model_ssd_small.npz", True, 7302, (12, 11))
     assert -3 in fk
     # "wide": strong residual updates that saturate, and final-norm shifts past
     # the BitShiftNormV2 table's top (k = 7, 8); the greedy tokens of such a
