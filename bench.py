@@ -32,6 +32,10 @@ HBM_PEAK_GBS = 8000.0
 # same counters on a 256 MiB device copy (FETCH x 2.000, WRITE x 1.000)
 IN_PROJ_STAGE_TRAFFIC_B8 = 2059174
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 39321.6 G/s
+# VALU lane-ops the prefill block scan issues per state update at the bench
+# shape, measured with rocprofv3 --pmc SQ_INSTS_VALU (wave64 instructions x 64
+# / updates; profiles/scan_kernels_valu_pmc.md)
+SCAN_LANE_OPS_PER_UPDATE = 18.43
 
 
 def scan_bytes(B, L, D, N):
@@ -95,6 +99,61 @@ def cpu_baseline(params, threads):
         "sample": "oracle C/OpenMP: batch 8 x 2048-token prefill + 48 decode steps of the d768x24 model "
                   f"({t2 - t0:.1f} s), decode extrapolated to 256 steps",
         "prefill_tok_s": 1.0 / t_tok_prefill, "decode_tok_s": 8.0 / t_decode_step,
+    }
+
+
+def cpu_model_name():
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_reference_structure(threads, dims, B=8, L=2048, n_dec=256, sub_layers=2):
+    """The reference's own float inference structure on PyTorch-CPU
+    (oracle/reference_cpu.py: per-timestep scan loop, fp32 F.linear BitLinear,
+    decoding by re-running the whole prefix) on a declared subset: the first
+    `sub_layers` of the 24 layers, timed over the full batch 8 x 2048 prefill
+    and over one full-recompute decode step (a forward over 2049 positions).
+    Scaling: layer time x (n_layer / sub_layers) + embedding and head time;
+    the 256 decode steps cost sum over prefix lengths 2049..2304 of one
+    forward each, taken as linear in the length (256 x t(2049) x 2176.5/2049)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import torch
+    import reference_cpu as R
+    torch.set_num_threads(threads)
+    m = R.RefCpuModel(dims.d_model, sub_layers, dims.vocab_size, dims.d_state, dims.dt_rank, seed=3)
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, dims.vocab_size, (B, L + 1), generator=g)
+
+    def timed(tokens):
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            x = m.emb[tokens]
+            for P in m.layers:
+                x = m.block(P, x)
+            t1 = time.perf_counter()
+            R.bitlinear(R.bitshift_norm(x, m.gamma_f), m.w_head) * m.out_scale
+            t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+    pl, ph = timed(ids[:, :L])
+    dl, dh = timed(ids)
+    scale = dims.n_layer / sub_layers
+    t_prefill = pl * scale + ph
+    t_step = dl * scale + dh
+    t_decode = n_dec * t_step * (L + 1 + (n_dec - 1) / 2) / (L + 1)
+    return {
+        "value": (B * L + B * n_dec) / (t_prefill + t_decode), "unit": "tok/s", "cores": threads,
+        "kind": "port", "prefill_tok_s": B * L / t_prefill, "decode_tok_s": B * n_dec / t_decode,
+        "sample": f"reference float structure on PyTorch-CPU (oracle/reference_cpu.py), {sub_layers} of "
+                  f"{dims.n_layer} layers: batch {B} x {L} prefill ({pl + ph:.1f} s) and one full-recompute decode "
+                  f"step over {L + 1} positions ({dl + dh:.1f} s); layer time scaled x{scale:g}, decode steps "
+                  f"summed over prefix lengths {L + 1}..{L + n_dec} as linear in the length",
     }
 
 
@@ -523,13 +582,20 @@ def main():
             "bound": "valu", "bytes_per_launch": sbytes, "avg_launch_ms": scan_avg_ms,
             "launches_timed": len(scan_ms), "hbm_GB_s": achieved, "hbm_frac": achieved / HBM_PEAK_GBS,
             "updates_per_s": updates / (scan_avg_ms * 1e-3),
+            "lane_ops_per_update": SCAN_LANE_OPS_PER_UPDATE,
+            "valu_frac": SCAN_LANE_OPS_PER_UPDATE * updates / (scan_avg_ms * 1e-3) / (VALU_PEAK_GOPS * 1e9),
         },
     }
     if args.kernels:
         line["kernels"] = kernel_table()
     if not args.no_cpu:
         threads = len(os.sched_getaffinity(0))
-        line["cpu_baseline"] = cpu_baseline(params, threads)
+        base = cpu_baseline(params, threads)
+        base["cpu_model"] = cpu_model_name()
+        # the reference's own structure (float, per-step scan loop, full-recompute
+        # decode) on the same cores, beside the integer oracle
+        base["reference_structure"] = cpu_reference_structure(threads, dims)
+        line["cpu_baseline"] = base
     print(json.dumps(line), flush=True)
 
 

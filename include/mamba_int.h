@@ -18,6 +18,7 @@
  *   launch_dyadic_scan           src/cuda_kernels/dyadic_mamba_kernel.cu:135-153
  *   DyadicScanFunction.apply     src/mamba_integer_model.py:260-316
  *   ssd_chunked_scan_forward     src/triton_kernels/ssd_chunked_scan.py:382-422
+ *   ssd_multihead_forward        src/triton_kernels/ssd_multihead.py:92-244
  *   BitLinear.forward            src/rational_bitnet.py:167-213
  *   activation_quant_dynamic     src/rational_bitnet.py:88-111
  *   get_ternary_weights          src/rational_bitnet.py:215-219
@@ -91,8 +92,30 @@ mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t *nums, int 
                                      int32_t *h, const int32_t *h_in, int32_t *h_out,
                                      int batch, int len, int channels, void *stream);
 
-/* Chunked multi-head scan, config-4 layout (replaces ssd_chunked_scan_forward,
- * ssd_chunked_scan.py:382-422, head layout of ssd_multihead.py:541-566).
+/* Chunked elementwise recurrence with the outputs of ssd_chunked_scan_forward
+ * (ssd_chunked_scan.py:382-422, chunk loop of :346-379): u, nums int32
+ * [batch,len,channels] (per-step decay numerators), one decay_shift (the
+ * reference reads shifts[0], :406-409), chunk >= 1.  Outputs:
+ *   h            int32 [batch,len,channels]: the state after every step,
+ *                sat32(floor(h_prev*num / 2^shift) + u) (the reference's `h`);
+ *   final_h      int32 [batch,ceil(len/chunk),channels], nullable: the state at
+ *                the last step of each chunk (the reference's `final_h`);
+ *   decay_to_end int32 [batch,ceil(len/chunk),channels], nullable: the chunk's
+ *                cumulative decay prod(num/2^shift) (the reference's float
+ *                `decay_to_end`) in Q30, rounded down after every step:
+ *                p = 2^30; p = sat32(floor(p*num / 2^shift)) per step.  With
+ *                0 <= num <= 2^shift it lies within len*2^-30 below the exact
+ *                product (the floor recurrence has no exact product form).
+ * h_in / h_out int32 [batch,channels] nullable (state before / after). */
+mi_status mi_dyadic_chunked_scan(const int32_t *u, const int32_t *nums, int decay_shift, int chunk,
+                                 int32_t *h, int32_t *final_h, int32_t *decay_to_end,
+                                 const int32_t *h_in, int32_t *h_out, int batch, int len, int channels,
+                                 void *stream);
+
+/* Chunked multi-head scan, config-4 layout: the integer form of the SSD scan
+ * of ssd_multihead_forward (ssd_multihead.py:92-244: X [B,L,H,P], B/C
+ * [B,L,H,N], one decay per head, chunks with the state carried from chunk to
+ * chunk, :196-216), with a constant per-head decay numerator.
  * x int8 [batch,len,heads,head_dim]; b, c int8 [batch,len,heads,nstate];
  * decay_num int32 [heads] in [0, 2^decay_shift]; y int32
  * [batch,len,heads,head_dim]; chunk_states int32

@@ -441,6 +441,58 @@ __global__ __launch_bounds__(256) void scan_elem_kernel(const int32_t *u, const 
     if (h_out) h_out[idx] = s;
 }
 
+// Chunked elementwise recurrence with the per-chunk outputs of
+// ssd_chunked_scan_forward (ssd_chunked_scan.py:382-422): one lane per
+// (b, channel), its steps in order.  The operands of kAhead steps are loaded
+// before the dependent chain runs over them, from clamped in-bounds addresses
+// (no per-lane condition, so the loads issue back to back); a step past the
+// end is skipped by a branch that is uniform across the block.  At the end of
+// each chunk the lane stores its state and the chunk's cumulative decay in
+// Q30 (2^30 decayed by the chunk's steps, rounded down after each step).
+constexpr int kAhead = 8;
+__global__ __launch_bounds__(64) void chunked_scan_kernel(const int32_t *__restrict__ u, const int32_t *__restrict__ n,
+                                                          int k, int cs, int32_t *__restrict__ h,
+                                                          int32_t *__restrict__ final_h, int32_t *__restrict__ dte,
+                                                          const int32_t *h_in, int32_t *h_out, int B, int L, int C,
+                                                          int nc) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)B * C) return;
+    const int c = (int)(idx % C);
+    const int b = (int)(idx / C);
+    const int64_t base = (int64_t)b * L * C + c;
+    int32_t s = h_in ? h_in[idx] : 0;
+    int32_t p = 1 << 30;
+    int left = cs;     // steps left in the current chunk
+    int chunk = 0;
+    for (int t0 = 0; t0 < L; t0 += kAhead) {
+        int32_t uu[kAhead], nn[kAhead];
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+            const int64_t off = base + (int64_t)min(t0 + j, L - 1) * C;
+            uu[j] = u[off];
+            nn[j] = n[off];
+        }
+#pragma unroll
+        for (int j = 0; j < kAhead; ++j) {
+            const int t = t0 + j;
+            if (t < L) {
+                s = sat32_64((((int64_t)s * nn[j]) >> k) + (int64_t)uu[j]);
+                h[base + (int64_t)t * C] = s;
+                p = sat32_64(((int64_t)p * nn[j]) >> k);
+                if (--left == 0 || t + 1 == L) {
+                    const int64_t co = ((int64_t)b * nc + chunk) * C + c;
+                    if (final_h) final_h[co] = s;
+                    if (dte) dte[co] = p;
+                    p = 1 << 30;
+                    left = cs;
+                    ++chunk;
+                }
+            }
+        }
+    }
+    if (h_out) h_out[idx] = s;
+}
+
 }  // namespace
 
 hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z, const int8_t *bsrc,
@@ -593,4 +645,21 @@ extern "C" mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t 
     hipLaunchKernelGGL(scan_elem_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, as_stream(stream), u,
                        nums, decay_shift, h, h_in, h_out, batch, len, channels);
     return check_launch("mi_dyadic_scan_elementwise");
+}
+
+extern "C" mi_status mi_dyadic_chunked_scan(const int32_t *u, const int32_t *nums, int decay_shift, int chunk,
+                                            int32_t *h, int32_t *final_h, int32_t *decay_to_end, const int32_t *h_in,
+                                            int32_t *h_out, int batch, int len, int channels, void *stream) {
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && channels >= 0, MI_ERR_BAD_DIM, "mi_dyadic_chunked_scan: negative size");
+    MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG,
+               "mi_dyadic_chunked_scan: decay_shift=%d outside [1,30]", decay_shift);
+    MI_REQUIRE(chunk >= 1, MI_ERR_BAD_ARG, "mi_dyadic_chunked_scan: chunk=%d must be >= 1", chunk);
+    if ((int64_t)batch * channels == 0 || len == 0) return MI_OK;
+    MI_REQUIRE(u && nums && h, MI_ERR_NULL_POINTER, "mi_dyadic_chunked_scan: u, nums and h are required");
+    const int64_t lanes = (int64_t)batch * channels;
+    const int nc = (int)((len + (int64_t)chunk - 1) / chunk);
+    hipLaunchKernelGGL(chunked_scan_kernel, dim3((unsigned)((lanes + 63) / 64)), dim3(64), 0, as_stream(stream), u,
+                       nums, decay_shift, chunk, h, final_h, decay_to_end, h_in, h_out, batch, len, channels, nc);
+    return check_launch("mi_dyadic_chunked_scan");
 }

@@ -27,6 +27,7 @@ SIGNATURES = {
     "mi_dyadic_scan": [P, P, P, P, I, P, P, P, I, I, I, I, P],
     "mi_dyadic_scan_f32": [P, P, P, P, I, I, I, I, P],
     "mi_dyadic_scan_elementwise": [P, P, I, P, P, P, I, I, I, P],
+    "mi_dyadic_chunked_scan": [P, P, I, I, P, P, P, P, P, I, I, I, P],
     "mi_ssd_chunked_scan": [P, P, P, P, I, P, P, P, P, I, I, I, I, I, I, P],
     "mi_pack_ternary": [P, P, I, I, P],
     "mi_act_quant_f32": [P, P, P, I, I, P],

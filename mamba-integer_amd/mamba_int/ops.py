@@ -76,6 +76,26 @@ def dyadic_scan_elementwise(u, nums, decay_shift: int, h_in=None, h_out=None):
     return h
 
 
+def dyadic_chunked_scan(u, nums, decay_shift: int, chunk: int, h_in=None, h_out=None):
+    """Chunked elementwise recurrence (mi_dyadic_chunked_scan): u, nums int32
+    [B,L,C] -> (h [B,L,C], final_h [B,nc,C], decay_to_end [B,nc,C] in Q30),
+    nc = ceil(L / chunk)."""
+    _req(u, torch.int32, "u"); _req(nums, torch.int32, "nums")
+    if nums.shape != u.shape:
+        raise ValueError(f"nums {tuple(nums.shape)} must match u {tuple(u.shape)}")
+    if chunk < 1:
+        raise ValueError(f"chunk={chunk} must be >= 1")
+    B, L, C = u.shape
+    nc = -(-L // chunk)
+    h = torch.empty_like(u)
+    final_h = torch.empty((B, nc, C), dtype=torch.int32, device=u.device)
+    decay_to_end = torch.empty((B, nc, C), dtype=torch.int32, device=u.device)
+    _lib.call("mi_dyadic_chunked_scan", _ptr(u), _ptr(nums), decay_shift, chunk, _ptr(h), _ptr(final_h),
+              _ptr(decay_to_end), _ptr(_opt(h_in, torch.int32, "h_in")), _ptr(_opt(h_out, torch.int32, "h_out")),
+              B, L, C, _stream())
+    return h, final_h, decay_to_end
+
+
 def ssd_chunked_scan(x, b, c, decay_num, decay_shift: int, chunk: int, chunk_states=None,
                      h_in=None, h_out=None):
     """Config-4 scan: x int8 [B,L,H,P], b/c int8 [B,L,H,N], decay_num int32 [H] -> y int32 [B,L,H,P]."""
