@@ -16,6 +16,9 @@
 // recurrent state of a Mamba decode instead of a full-prefix recompute.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "mi_common.hpp"
 
 namespace mi {
@@ -102,6 +105,46 @@ mi_status check_model(const char *fn, const mi_model_params *p, int m) {
     }
     MI_REQUIRE(p->emb && p->layers && p->gamma_f && p->w_head, MI_ERR_NULL_POINTER,
                "%s: emb, layers, gamma_f and w_head are required", fn);
+    return MI_OK;
+}
+
+// The workspace of mi_decode_step_static: one array in device memory per GPU,
+// held by the loaded library until the process ends (no allocation call).
+// Host code never uses the name `scratch` as an address (on the host it is a
+// stand-in symbol); it uses the per-device address hipGetSymbolAddress returns.
+constexpr size_t kStaticScratchBytes = (size_t)16 << 20;
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+}  // namespace
+}  // namespace mi
+
+static __device__ __align__(256) unsigned char scratch[mi::kStaticScratchBytes];
+
+namespace mi {
+namespace {
+
+// The current device's address of `scratch`, looked up once per device.
+mi_status static_scratch(const char *fn, void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+    MI_REQUIRE(dev >= 0 && dev < kMaxDevices, MI_ERR_BAD_ARG, "%s: device %d beyond the %d this library tracks", fn,
+               dev, kMaxDevices);
+    void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!ptr) {
+            e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !ptr)
+                return fail(MI_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", fn, dev,
+                            hipGetErrorString(e));
+            g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+        }
+    }
+    *out = ptr;
     return MI_OK;
 }
 
@@ -239,4 +282,24 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
     MI_STEP(mi_argmax_keys(keys, (p.vocab_size + 63) / 64, next_ids, m, stream));
 #undef MI_STEP
     return MI_OK;
+}
+
+
+extern "C" mi_status mi_decode_step_static(const mi_model_params *params, int m, const int64_t *ids,
+                                           int64_t *next_ids, int32_t *logits, int ld_logits,
+                                           int8_t *const *conv_state, int32_t *const *h_state, void *stream) {
+    clear_error();
+    mi_status st = check_model("mi_decode_step_static", params, m);
+    if (st != MI_OK) return st;
+    const size_t need = ws_layout(*params, m).total;
+    MI_REQUIRE(need <= kStaticScratchBytes, MI_ERR_BAD_DIM,
+               "mi_decode_step_static: this model at m=%d needs %zu bytes of workspace; the static scratch holds %zu "
+               "(call mi_decode_step with a workspace of your own)", m, need, kStaticScratchBytes);
+    MI_REQUIRE(ids && next_ids && conv_state && h_state, MI_ERR_NULL_POINTER,
+               "mi_decode_step_static: ids, next_ids, conv_state and h_state are required");
+    void *ws = nullptr;
+    st = static_scratch("mi_decode_step_static", &ws);
+    if (st != MI_OK) return st;
+    return mi_decode_step(params, m, ids, next_ids, logits, ld_logits, conv_state, h_state, ws, kStaticScratchBytes,
+                          stream);
 }

@@ -57,6 +57,7 @@ SIGNATURES = {
     "mi_embed_argmax": [P, I, P, P, P, I, I, I, P, I, P],
     "mi_decode_workspace_size": [P, I, P],
     "mi_decode_step": [P, I, P, P, P, I, P, P, P, ctypes.c_size_t, P],
+    "mi_decode_step_static": [P, I, P, P, P, I, P, P, P],
     "mi_checkpoint_open": [ctypes.c_char_p, P],
     "mi_checkpoint_get_info": [P, P],
     "mi_checkpoint_upload": [P, P, ctypes.c_size_t, P, P, I, P],
