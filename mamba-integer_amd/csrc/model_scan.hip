@@ -2,18 +2,22 @@
 // decay from base + dm, dt from dm, input xs*dt (x) B, the exact floor
 // recurrence, y = C.h, the gate by z and the requant of the out_proj input.
 //
-// Layout: a block owns CH = 256/G channels of one sequence; G adjacent lanes
-// share a channel and keep S = N/G states each in VGPRs as h = hh*2^15 + hl.
-// Per chunk of 64 steps the block stages xs, dm, z (transposed to
-// channel-major bytes) and B, C (widened to int32 so a state reads its
-// coefficients with one ds_read_b128 per four states) through LDS, prefetching
-// the next chunk into registers while it computes the current one.
+// Layout: a block of NT threads owns CH = NT/G channels of one sequence; G
+// adjacent lanes share a channel and keep S = N/G states each in VGPRs as
+// h = hh*2^15 + hl.  Per chunk of 64 steps the block stages xs, dm, z
+// (transposed to channel-major bytes) and B, C (widened to int32 so a state
+// reads its coefficients with one ds_read_b128 per four states) through LDS,
+// in two buffers where they fit: chunk c+1 is staged right after chunk c's
+// steps, and its global loads were issued a whole chunk earlier.
 //
 // The per-step work of a lane is only the recurrence and two exact int32
-// partial sums of y; the lane quad/octet combines them with DPP adds and one
-// lane parks (yhi, ylo) in LDS.  The epilogue (recombine, saturate, gate,
-// requant) runs once per (step, channel) at the end of the chunk, spread over
-// all 256 threads, instead of redundantly in every lane every step.
+// partial sums of y.  Steps run in groups of four: the next group's B and C
+// are read from LDS into the other of two register sets while this group's
+// recurrence runs, and the group's eight partial sums are combined over the
+// channel's G lanes stage by stage across all eight (DPP adds whose sources
+// were written several instructions earlier, so no wait states).  The
+// epilogue (recombine, saturate, gate, requant) runs once per (step, channel)
+// at the end of the chunk, spread over all threads.
 // Per update: decay term 3 (v_mul_u32_u24, shift, v_mad_i32_i24), input 1,
 // saturating add 1, split 2, y partials 2, decay clamp 0-2 (skipped when every
 // base of the wave lies at least 20 inside [0, 32000], where base + dm cannot
@@ -53,24 +57,47 @@ struct MScanArgs {
     int B, L, D, s_y;
 };
 
-template <int N, int G>
-__global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
+// DPP sums of K independent values over the G lanes of a channel, stage by
+// stage across all K values: a DPP add then reads a register written K
+// instructions earlier, so no wait states are needed between the stages.
+template <int G, int K>
+__device__ __forceinline__ void msum_all(int (&v)[K]) {
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if constexpr (G >= 2) v[k] += __builtin_amdgcn_update_dpp(0, v[k], 0xB1, 0xF, 0xF, true);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if constexpr (G >= 4) v[k] += __builtin_amdgcn_update_dpp(0, v[k], 0x4E, 0xF, 0xF, true);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if constexpr (G >= 8) v[k] += __builtin_amdgcn_update_dpp(0, v[k], 0x141, 0xF, 0xF, true);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if constexpr (G >= 16) v[k] += __builtin_amdgcn_update_dpp(0, v[k], 0x140, 0xF, 0xF, true);
+}
+
+template <int N, int G, int NT>
+__global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     constexpr int S = N / G;
-    constexpr int CH = kMThreads / G;
+    constexpr int CH = NT / G;
     constexpr int XP = kMTC + 4;
     constexpr int X16 = CH / 16;
     constexpr int XPIECES = kMTC * X16;
-    constexpr int XPER = (XPIECES + kMThreads - 1) / kMThreads;
+    constexpr int XPER = (XPIECES + NT - 1) / NT;
     constexpr int BC16 = N / 16;
     constexpr int BCPIECES = kMTC * BC16;
-    constexpr int BCPER = (BCPIECES + kMThreads - 1) / kMThreads;
-    static_assert(N % 16 == 0 && (S == 1 || S == 2 || S % 4 == 0), "state split");
-    static_assert(2 * CH * XP + CH * XP * 2 + 2 * kMTC * N * 4 + kMTC * CH * 9 + 297 * 4 <= 65536, "LDS budget");
+    constexpr int BCPER = (BCPIECES + NT - 1) / NT;
+    static_assert(N % 16 == 0 && CH % 16 == 0 && (S == 1 || S == 2 || S % 4 == 0), "state split");
+    // staging buffers: two (chunk c + 1 is staged while chunk c's epilogue runs)
+    // where they fit in 64 KB of LDS, else one
+    constexpr int kStage = 2 * CH * XP + CH * XP * 2 + 2 * kMTC * N * 4;
+    constexpr int NB = 2 * kStage + kMTC * CH * 9 + 297 * 4 <= 65536 ? 2 : 1;
+    static_assert(NB * kStage + kMTC * CH * 9 + 297 * 4 <= 65536, "LDS budget");
 
-    __shared__ __align__(16) int8_t s_x[2][CH][XP];        // dm, z (channel-major)
-    __shared__ __align__(16) int16_t s_xd[CH][XP];          // rshr(xs * dt(dm), 10), |xd| <= 813
-    __shared__ __align__(16) int32_t s_b[kMTC][N];
-    __shared__ __align__(16) int32_t s_c[kMTC][N];
+    __shared__ __align__(16) int8_t s_x[NB][2][CH][XP];    // dm, z (channel-major)
+    __shared__ __align__(16) int16_t s_xd[NB][CH][XP];      // rshr(xs * dt(dm), 10), |xd| <= 813
+    __shared__ __align__(16) int32_t s_b[NB][kMTC][N];
+    __shared__ __align__(16) int32_t s_c[NB][kMTC][N];
     __shared__ __align__(16) int2 s_y[kMTC][CH];            // (yhi, ylo) per step and channel
     __shared__ __align__(16) int8_t s_o[kMTC][CH];
     __shared__ int32_t s_dt[41];
@@ -84,8 +111,8 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
     const int p = p0 + ch;
     const bool active = p < a.D;
 
-    for (int i = tid; i < 41; i += kMThreads) s_dt[i] = dt_q16(i - 20);
-    for (int i = tid; i < 256; i += kMThreads) s_gate[i] = gate_q15(i - 128);
+    for (int i = tid; i < 41; i += NT) s_dt[i] = dt_q16(i - 20);
+    for (int i = tid; i < 256; i += NT) s_gate[i] = gate_q15(i - 128);
 
     int32_t base[S], hh[S], hl[S];
     bool safe = true;
@@ -109,7 +136,7 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
     const int64_t row0 = (int64_t)b * a.L;
     auto prefetch = [&](int t0) {
         for (int j = 0; j < XPER; ++j) {
-            const int i = tid + j * kMThreads;
+            const int i = tid + j * NT;
             const int tt = i / X16, c16 = i % X16;
             const bool ok = i < XPIECES && t0 + tt < a.L && p0 + c16 * 16 < a.D;
             const int64_t rr = row0 + t0 + tt;
@@ -119,7 +146,7 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             rx[2][j] = ok ? *reinterpret_cast<const v4i *>(a.z + rr * a.z_row + p0 + c16 * 16) : zero;
         }
         for (int j = 0; j < BCPER; ++j) {
-            const int i = tid + j * kMThreads;
+            const int i = tid + j * NT;
             const int tt = i / BC16, c16 = i % BC16;
             const bool ok = i < BCPIECES && t0 + tt < a.L;
             const int64_t off = (row0 + t0 + tt) * a.bc_row + c16 * 16;
@@ -127,9 +154,9 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             rc[j] = ok ? *reinterpret_cast<const v4i *>(a.csrc + off) : v4i{0, 0, 0, 0};
         }
     };
-    auto stash = [&]() {
+    auto stash = [&](int bf) {
         for (int j = 0; j < XPER; ++j) {
-            const int i = tid + j * kMThreads;
+            const int i = tid + j * NT;
             if (i >= XPIECES) break;
             const int tt = i / X16, c16 = i % X16;
             const uint32_t wx[4] = {(uint32_t)rx[0][j][0], (uint32_t)rx[0][j][1], (uint32_t)rx[0][j][2],
@@ -141,43 +168,52 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int dmv = clamp32(sb(wd[e >> 2], e & 3), -20, 20);
-                s_x[0][c16 * 16 + e][tt] = (int8_t)dmv;
-                s_x[1][c16 * 16 + e][tt] = (int8_t)sb(wz[e >> 2], e & 3);
-                s_xd[c16 * 16 + e][tt] = (int16_t)((sb(wx[e >> 2], e & 3) * s_dt[dmv + 20] + 512) >> 10);
+                s_x[bf][0][c16 * 16 + e][tt] = (int8_t)dmv;
+                s_x[bf][1][c16 * 16 + e][tt] = (int8_t)sb(wz[e >> 2], e & 3);
+                s_xd[bf][c16 * 16 + e][tt] = (int16_t)((sb(wx[e >> 2], e & 3) * s_dt[dmv + 20] + 512) >> 10);
             }
         }
         for (int j = 0; j < BCPER; ++j) {
-            const int i = tid + j * kMThreads;
+            const int i = tid + j * NT;
             if (i >= BCPIECES) break;
             const int tt = i / BC16, c16 = i % BC16;
             const uint32_t wb[4] = {(uint32_t)rb[j][0], (uint32_t)rb[j][1], (uint32_t)rb[j][2], (uint32_t)rb[j][3]};
             const uint32_t wc[4] = {(uint32_t)rc[j][0], (uint32_t)rc[j][1], (uint32_t)rc[j][2], (uint32_t)rc[j][3]};
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                s_b[tt][c16 * 16 + e] = sb(wb[e >> 2], e & 3);
-                s_c[tt][c16 * 16 + e] = sb(wc[e >> 2], e & 3);
+                s_b[bf][tt][c16 * 16 + e] = sb(wb[e >> 2], e & 3);
+                s_c[bf][tt][c16 * 16 + e] = sb(wc[e >> 2], e & 3);
             }
         }
     };
 
-    // one recurrence step of this lane's S states; CLAMP selects the decay clamp
-    auto step = [&](int t, int xd, int dmv, auto clamp_tag) {
-        constexpr bool CLAMP = decltype(clamp_tag)::value;
-        int bv[S], cv[S];
+    // this lane's S coefficients of B and C for step t (LDS row t < kMTC)
+    auto load_bc = [&](int bf, int t, int (&bv)[S], int (&cv)[S]) {
         if constexpr (S >= 4) {
+#pragma unroll
             for (int q = 0; q < S / 4; ++q) {
-                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[t][g * S + 4 * q]);
-                const int4 c4 = *reinterpret_cast<const int4 *>(&s_c[t][g * S + 4 * q]);
+                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[bf][t][g * S + 4 * q]);
+                const int4 c4 = *reinterpret_cast<const int4 *>(&s_c[bf][t][g * S + 4 * q]);
                 bv[4 * q] = b4.x; bv[4 * q + 1] = b4.y; bv[4 * q + 2] = b4.z; bv[4 * q + 3] = b4.w;
                 cv[4 * q] = c4.x; cv[4 * q + 1] = c4.y; cv[4 * q + 2] = c4.z; cv[4 * q + 3] = c4.w;
             }
+        } else if constexpr (S == 2) {
+            const int2 b2 = *reinterpret_cast<const int2 *>(&s_b[bf][t][g * S]);
+            const int2 c2 = *reinterpret_cast<const int2 *>(&s_c[bf][t][g * S]);
+            bv[0] = b2.x; bv[1] = b2.y; cv[0] = c2.x; cv[1] = c2.y;
         } else {
-            for (int s = 0; s < S; ++s) {
-                bv[s] = s_b[t][g * S + s];
-                cv[s] = s_c[t][g * S + s];
-            }
+            bv[0] = s_b[bf][t][g];
+            cv[0] = s_c[bf][t][g];
         }
-        int yhi = 0, ylo = 0;
+    };
+    // the recurrence of this lane's S states for one step: returns the exact
+    // int32 partials (sum C*hh, sum C*hl) of y over the lane's states
+    auto update = [&](int xd, int dmv, const int (&bv)[S], const int (&cv)[S], int &yhi, int &ylo,
+                      auto clamp_tag) {
+        constexpr bool CLAMP = decltype(clamp_tag)::value;
+        yhi = 0;
+        ylo = 0;
+#pragma unroll
         for (int s = 0; s < S; ++s) {
             const int nt = CLAMP ? clamp32(base[s] + dmv, 0, 32000) : base[s] + dmv;
             const int u = __mul24(bv[s], xd);
@@ -189,44 +225,73 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             yhi += __mul24(cv[s], hh[s]);
             ylo += __mul24(cv[s], hl[s]);
         }
-        yhi = msum<G>(yhi);
-        ylo = msum<G>(ylo);
-        s_y[t][ch] = make_int2(yhi, ylo);  // all G lanes hold the same sums: no branch
     };
 
+    // Per chunk: the steps of chunk c, (two buffers) the staging of chunk c+1,
+    // a barrier, the epilogue of chunk c (recombine, saturate, gate, requant)
+    // into s_o, a barrier, the 16-byte stores of chunk c and the global loads
+    // of the chunk after next.  One buffer: chunk c+1 is staged after the
+    // stores, behind a third barrier.
     const int nchunks = (a.L + kMTC - 1) / kMTC;
     prefetch(0);
+    stash(0);
+    if (nchunks > 1) prefetch(kMTC);
+    __syncthreads();
     for (int cidx = 0; cidx < nchunks; ++cidx) {
         const int t0 = cidx * kMTC;  // chunk start
         const int tn = min(kMTC, a.L - t0);
-        __syncthreads();
-        stash();
-        __syncthreads();
-        if (cidx + 1 < nchunks) prefetch(t0 + kMTC);
+        const int cur = NB == 2 ? (cidx & 1) : 0;
 
         auto run_chunk = [&](auto clamp_tag) {
-            for (int t4 = 0; t4 < tn; t4 += 4) {
-                const uint32_t dw = *reinterpret_cast<const uint32_t *>(&s_x[0][ch][t4]);
-                const uint2 xw = *reinterpret_cast<const uint2 *>(&s_xd[ch][t4]);
-                const int xdv[4] = {(int)(int16_t)xw.x, (int)xw.x >> 16, (int)(int16_t)xw.y, (int)xw.y >> 16};
-                if (t4 + 4 <= tn) {
+            const int t4n = tn & ~3;  // steps in whole groups of four
+            // groups of four steps: the next group's coefficients are read from
+            // LDS while this group's recurrence runs, and the y partials of the
+            // four steps are reduced together afterwards; two register sets of
+            // coefficients alternate between the groups of a pair
+            auto group = [&](int t4, const int (&bq)[4][S], const int (&cq)[4][S], int (&bn)[4][S],
+                             int (&cn)[4][S]) {
 #pragma unroll
-                    for (int tt = 0; tt < 4; ++tt) step(t4 + tt, xdv[tt], sb(dw, tt), clamp_tag);
-                } else {
-                    for (int tt = 0; tt < tn - t4; ++tt) step(t4 + tt, xdv[tt], sb(dw, tt), clamp_tag);
-                }
+                for (int tt = 0; tt < 4; ++tt) load_bc(cur, min(t4 + 4 + tt, kMTC - 1), bn[tt], cn[tt]);
+                const uint32_t dw = *reinterpret_cast<const uint32_t *>(&s_x[cur][0][ch][t4]);
+                const uint2 xw = *reinterpret_cast<const uint2 *>(&s_xd[cur][ch][t4]);
+                const int xdv[4] = {(int)(int16_t)xw.x, (int)xw.x >> 16, (int)(int16_t)xw.y, (int)xw.y >> 16};
+                int y[8];
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt)
+                    update(xdv[tt], sb(dw, tt), bq[tt], cq[tt], y[2 * tt], y[2 * tt + 1], clamp_tag);
+                msum_all<G>(y);
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][ch] = make_int2(y[2 * tt], y[2 * tt + 1]);
+            };
+            int b0[4][S], c0[4][S], b1[4][S], c1[4][S];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) load_bc(cur, tt, b0[tt], c0[tt]);
+            for (int t4 = 0; t4 < t4n; t4 += 8) {
+                group(t4, b0, c0, b1, c1);
+                if (t4 + 4 < t4n) group(t4 + 4, b1, c1, b0, c0);
+            }
+            for (int t = t4n; t < tn; ++t) {
+                int bv[S], cv[S];
+                load_bc(cur, t, bv, cv);
+                const int dmv = s_x[cur][0][ch][t];
+                int y[2];
+                update(s_xd[cur][ch][t], dmv, bv, cv, y[0], y[1], clamp_tag);
+                msum_all<G>(y);
+                s_y[t][ch] = make_int2(y[0], y[1]);  // all G lanes hold the same sums: no branch
             }
         };
         if (wave_safe) run_chunk(std::false_type{});
         else run_chunk(std::true_type{});
+        if constexpr (NB == 2)
+            if (cidx + 1 < nchunks) stash(cur ^ 1);
         __syncthreads();
         // epilogue of the chunk: y = sat32(yhi*2^15 + ylo), gate, requant
-        for (int i = tid; i < kMTC * CH; i += kMThreads) {
+        for (int i = tid; i < kMTC * CH; i += NT) {
             const int tt = i / CH, cc = i % CH;
             if (tt < tn) {
                 const int2 yv = s_y[tt][cc];
                 const int32_t y32 = sat32_64(((int64_t)yv.x << 15) + yv.y);
-                const int zv = s_x[1][cc][tt];
+                const int zv = s_x[cur][1][cc][tt];
                 const int32_t gt = s_gate[zv + 128];
                 // floor(y32 * gt / 2^15) with 32-bit pieces: y32 = yh*2^15 + yl, 0 <= yl < 2^15
                 const int32_t yh = y32 >> 15, yl = y32 & 0x7fff;
@@ -235,11 +300,18 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
             }
         }
         __syncthreads();
-        for (int i = tid; i < kMTC * X16; i += kMThreads) {
+        for (int i = tid; i < kMTC * X16; i += NT) {
             const int tt = i / X16, c16 = i % X16;
             if (tt < tn && p0 + c16 * 16 < a.D)
                 *reinterpret_cast<uint4 *>(a.yo + (row0 + t0 + tt) * a.x_row + p0 + c16 * 16) =
                     *reinterpret_cast<const uint4 *>(&s_o[tt][c16 * 16]);
+        }
+        if constexpr (NB == 2) {
+            if (cidx + 2 < nchunks) prefetch(t0 + 2 * kMTC);
+        } else if (cidx + 1 < nchunks) {
+            stash(0);
+            if (cidx + 2 < nchunks) prefetch(t0 + 2 * kMTC);
+            __syncthreads();
         }
     }
     if (a.h_out && active) {
@@ -248,23 +320,25 @@ __global__ __launch_bounds__(kMThreads) void model_scan_kernel(MScanArgs a) {
     }
 }
 
-template <int N>
-hipError_t launch_model_n(int G, const MScanArgs &a, hipStream_t st) {
-    auto grid = [&](int ch) { return dim3((unsigned)((a.D + ch - 1) / ch), (unsigned)a.B); };
-    switch (G) {
-#define MI_MCASE(GG)                                                                                    \
-    case GG:                                                                                            \
-        if constexpr (4 * (kMThreads / GG) * (kMTC + 4) + 2 * kMTC * N * 4 + kMTC * (kMThreads / GG) * 9 + \
-                          297 * 4 <= 65536) {                                                           \
-            hipLaunchKernelGGL((model_scan_kernel<N, GG>), grid(kMThreads / GG), dim3(kMThreads), 0, st, a); \
-            return hipGetLastError();                                                                   \
-        }                                                                                               \
-        break;
-        MI_MCASE(4)
-        MI_MCASE(8)
-        MI_MCASE(16)
-#undef MI_MCASE
+template <int N, int G, int NT>
+hipError_t launch_model_ngt(const MScanArgs &a, hipStream_t st) {
+    constexpr int CH = NT / G;
+    if constexpr (4 * CH * (kMTC + 4) + 2 * kMTC * N * 4 + kMTC * CH * 9 + 297 * 4 <= 65536) {
+        // (one staging buffer fits; the kernel doubles it where two fit)
+        hipLaunchKernelGGL((model_scan_kernel<N, G, NT>), dim3((unsigned)((a.D + CH - 1) / CH), (unsigned)a.B),
+                           dim3(NT), 0, st, a);
+        return hipGetLastError();
     }
+    return hipErrorInvalidValue;
+}
+
+template <int N>
+hipError_t launch_model_n(int G, int NT, const MScanArgs &a, hipStream_t st) {
+#define MI_MCASE(GG, TT) \
+    if (G == GG && NT == TT) return launch_model_ngt<N, GG, TT>(a, st);
+    MI_MCASE(8, 256)
+    MI_MCASE(16, 256)
+#undef MI_MCASE
     return hipErrorInvalidValue;
 }
 
@@ -642,15 +716,13 @@ hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z
     a.xs = xs; a.dm = dm; a.z = z; a.bsrc = bsrc; a.csrc = csrc; a.base = base; a.yo = yo;
     a.h_in = h_in; a.h_out = h_out; a.x_row = x_row; a.z_row = z_row; a.bc_row = bc_row;
     a.B = B; a.L = L; a.D = D; a.s_y = s_y;
-    // lanes per channel: 8 at N=16 (1536 waves at d_inner 1536 x batch 8; measured
-    // 0.39 ms against 0.44 ms at 4 and 0.41 ms at 16), otherwise the smallest
-    // split whose LDS staging fits
-    const int gmin = N <= 16 ? 4 : (N <= 32 ? 8 : 16);
-    const int G = N == 16 ? 8 : gmin;
+    // lanes per channel and block size, measured at d_inner 1536 x batch 8 x
+    // L2048, N16 (ms per launch): G8/256 threads 0.333, G8/128 0.337, G4/64
+    // 0.373, G4/256 0.369, G16/256 0.356, G4/128 0.531
     switch (N) {
-        case 16: return launch_model_n<16>(G, a, st);
-        case 32: return launch_model_n<32>(G, a, st);
-        case 64: return launch_model_n<64>(G, a, st);
+        case 16: return launch_model_n<16>(8, 256, a, st);
+        case 32: return launch_model_n<32>(8, 256, a, st);
+        case 64: return launch_model_n<64>(16, 256, a, st);
     }
     return hipErrorInvalidValue;
 }
