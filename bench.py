@@ -35,7 +35,7 @@ VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 393
 # VALU lane-ops the prefill block scan issues per state update at the bench
 # shape, measured with rocprofv3 --pmc SQ_INSTS_VALU (wave64 instructions x 64
 # / updates; profiles/scan_kernels_valu_pmc.md)
-SCAN_LANE_OPS_PER_UPDATE = 18.43
+SCAN_LANE_OPS_PER_UPDATE = 17.71
 
 
 def scan_bytes(B, L, D, N):

@@ -107,6 +107,10 @@ constexpr int kBM = 128, kBN = 128, kBK = 128;
 constexpr int kApitch = kBK + 16;       // bytes per staged activation row (bank-conflict free b128 reads)
 constexpr int kWpitch = kBK / 16 + 4;   // words per staged weight row (conflict free b32 reads)
 constexpr int kA2pitch = kBK + 32;      // activation row pitch of gemm_kernel (160 B)
+// gemm_kernel's tiles per wave along n (measured at M 4096, K 768, N 3072:
+// 2 -> 14.6 us, 4 -> 15.5 us, 8 -> 20.7 us; pitch 144 B instead of 160 B:
+// 15.6 us)
+constexpr int kGemmNI = 2;
 constexpr int kOpitch = 144;            // int8 output tile pitch in LDS (conflict-free dword writes)
 
 // gemm_kernel: 128(n) x 128(m) block tile, 4 waves stacked along n (each 32
@@ -128,8 +132,14 @@ struct GemmStage {
     int wmask;   // 0 for the weight words of a K tail beyond k
 };
 
-template <int KIND, bool LDSOUT>
+template <int KIND, bool LDSOUT, int NI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs g) {
+    // each wave computes NI x MJ tiles of 16 x 16 outputs: NI along n (weight
+    // rows), MJ along m (tokens); the four waves tile the 128 x 128 block as
+    // WN x WM
+    constexpr int MJ = 16 / NI;
+    constexpr int WN = 8 / NI, WM = 4 / WN;
+    static_assert(NI * MJ == 16 && WN * WM == 4 && WN * NI == 8 && WM * MJ == 8, "wave tiling");
     __shared__ __align__(16) int8_t sA[2][kBM * kA2pitch];
     __shared__ __align__(16) uint32_t sW[2][kBN * kWpitch];
     static_assert(kBM * kOpitch <= kBM * kA2pitch, "output tile must fit one activation buffer");
@@ -137,7 +147,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wn = wave_id();
+    const int wid = wave_id();
+    const int wn = wid / WM, wm = wid % WM;
     const int l16 = lane & 15, lq = lane >> 4;
 
     // blockIdx.x walks m-tiles fastest so the blocks that share a weight tile run together
@@ -175,11 +186,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         *reinterpret_cast<v4i *>(&sW[buf][wrow * kWpitch + wh * 4]) = S.w & S.wmask;
     };
 
-    v4i acc[2][8];
+    v4i acc[NI][MJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < MJ; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
     load(0);
     store_stage(0);
@@ -188,39 +199,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         const int buf = kt & 1;
         if (kt + 1 < nk) load(kt + 1);
         {
-            // the two 64-deep halves of the stage: all four weight words and the
+            // the two 64-deep halves of the stage: all weight words and the
             // first half's activation fragments up front; each fragment of the
             // second half is read into the register its first-half twin frees
-            const uint32_t *wr = &sW[buf][(wn * 32 + l16) * kWpitch + lq];
-            const uint32_t w00 = wr[0], w01 = wr[16 * kWpitch], w10 = wr[4], w11 = wr[16 * kWpitch + 4];
-            const int8_t *ar = &sA[buf][l16 * kA2pitch + lq * 16];
-            v4i fa[8];
+            const uint32_t *wr = &sW[buf][(wn * NI * 16 + l16) * kWpitch + lq];
+            uint32_t w0[NI], w1[NI];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) fa[j] = *reinterpret_cast<const v4i *>(ar + j * 16 * kA2pitch);
-            const v4i f0 = unpack16(w00), f1 = unpack16(w01);
-            const v4i h0 = unpack16(w10), h1 = unpack16(w11);
+            for (int i = 0; i < NI; ++i) {
+                w0[i] = wr[i * 16 * kWpitch];
+                w1[i] = wr[i * 16 * kWpitch + 4];
+            }
+            const int8_t *ar = &sA[buf][(wm * MJ * 16 + l16) * kA2pitch + lq * 16];
+            v4i fa[MJ];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[0][j] = mfma_i8(f0, fa[j], acc[0][j]);
-                acc[1][j] = mfma_i8(f1, fa[j], acc[1][j]);
+            for (int j = 0; j < MJ; ++j) fa[j] = *reinterpret_cast<const v4i *>(ar + j * 16 * kA2pitch);
+            v4i f[NI], h[NI];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                f[i] = unpack16(w0[i]);
+                h[i] = unpack16(w1[i]);
+            }
+#pragma unroll
+            for (int j = 0; j < MJ; ++j) {
+#pragma unroll
+                for (int i = 0; i < NI; ++i) acc[i][j] = mfma_i8(f[i], fa[j], acc[i][j]);
                 fa[j] = *reinterpret_cast<const v4i *>(ar + j * 16 * kA2pitch + 64);
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[0][j] = mfma_i8(h0, fa[j], acc[0][j]);
-                acc[1][j] = mfma_i8(h1, fa[j], acc[1][j]);
-            }
+            for (int j = 0; j < MJ; ++j)
+#pragma unroll
+                for (int i = 0; i < NI; ++i) acc[i][j] = mfma_i8(h[i], fa[j], acc[i][j]);
         }
         if (kt + 1 < nk) store_stage(buf ^ 1);
         __syncthreads();   // after the last stage: every wave is done reading sA / sW
     }
+    // output (n, m) of acc[i][j][r]: n = nb + i*16 + 4*lq + r, m = mb + j*16 + l16
+    const int nb = wn * NI * 16, mb = wm * MJ * 16;
 
     if constexpr (LDSOUT) {
         int8_t *sO = &sA[0][0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < MJ; ++j)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < NI; ++i) {
                 uint32_t pk = 0;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -228,7 +249,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                     const int v = KIND == MI_OUT_INT8 ? clamp32(q, -127, 127) : clamp32(q, -20, 20);
                     pk |= (uint32_t)(v & 255) << (8 * r);
                 }
-                *reinterpret_cast<uint32_t *>(&sO[(j * 16 + l16) * kOpitch + wn * 32 + i * 16 + 4 * lq]) = pk;
+                *reinterpret_cast<uint32_t *>(&sO[(mb + j * 16 + l16) * kOpitch + nb + i * 16 + 4 * lq]) = pk;
             }
         __syncthreads();
 #pragma unroll
@@ -253,25 +274,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         // before any update (rows past M and groups past N read clamped in-bounds
         // addresses; their results are not stored)
         int32_t *ob = (int32_t *)g.out;
+        // token groups of 4 m-tiles (or all of them) x every n-tile of the wave
+        constexpr int JG = MJ < 4 ? MJ : 4;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            v4i old[4][2];
+        for (int h = 0; h < MJ / JG; ++h) {
+            v4i old[JG][NI];
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
+            for (int jj = 0; jj < JG; ++jj)
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int m = min(m0 + (4 * h + jj) * 16 + l16, g.M - 1);
-                    const int n = n0 + wn * 32 + i * 16 + 4 * lq;
+                for (int i = 0; i < NI; ++i) {
+                    const int m = min(m0 + mb + (JG * h + jj) * 16 + l16, g.M - 1);
+                    const int n = n0 + nb + i * 16 + 4 * lq;
                     old[jj][i] = *reinterpret_cast<const v4i *>(ob + (int64_t)m * g.ldo + (n < g.N ? n : 0));
                 }
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int j = 4 * h + jj;
-                const int m = m0 + j * 16 + l16;
+            for (int jj = 0; jj < JG; ++jj) {
+                const int j = JG * h + jj;
+                const int m = m0 + mb + j * 16 + l16;
                 RowStat st{0, 0};
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int n = n0 + wn * 32 + i * 16 + 4 * lq;
+                for (int i = 0; i < NI; ++i) {
+                    const int n = n0 + nb + i * 16 + 4 * lq;
                     if (m < g.M && n < g.N) {
                         v4i nv;
 #pragma unroll
@@ -299,10 +322,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int m = m0 + j * 16 + l16;
+        for (int j = 0; j < MJ; ++j) {
+            const int m = m0 + mb + j * 16 + l16;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) store4<KIND>(g, m, n0 + wn * 32 + i * 16 + 4 * lq, acc[i][j]);
+            for (int i = 0; i < NI; ++i) store4<KIND>(g, m, n0 + nb + i * 16 + 4 * lq, acc[i][j]);
         }
     }
 }
@@ -742,9 +765,9 @@ hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
     }
     constexpr bool kInt8Out = KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD;
     if (kInt8Out && g.ldo % 16 == 0 && aligned(g.out, 16))
-        hipLaunchKernelGGL((gemm_kernel<KIND, kInt8Out>), grid, dim3(256), 0, st, g);
+        hipLaunchKernelGGL((gemm_kernel<KIND, kInt8Out, kGemmNI>), grid, dim3(256), 0, st, g);
     else
-        hipLaunchKernelGGL((gemm_kernel<KIND, false>), grid, dim3(256), 0, st, g);
+        hipLaunchKernelGGL((gemm_kernel<KIND, false, kGemmNI>), grid, dim3(256), 0, st, g);
     return hipGetLastError();
 }
 
