@@ -97,6 +97,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     __shared__ __align__(16) int32_t s_o32[STAGE_Y ? kTC : 1][STAGE_Y ? CH : 4];
     __shared__ int32_t s_dt[MODEL ? 41 : 1];
     __shared__ int32_t s_gate[MODEL ? 256 : 1];
+    // blocks of <= 32 channels (G >= 8) reduce the y partials of four steps
+    // together and park the exact (yhi, ylo) pairs here; the chunk epilogue
+    // recombines and saturates once per (step, channel)
+    constexpr bool DEFER = CH <= 32;
+    __shared__ __align__(16) int2 s_y[DEFER ? kTC : 1][DEFER ? CH : 1];
 
     const int tid = threadIdx.x;
     const int ch = tid / G;
@@ -188,6 +193,46 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         __syncthreads();
         if (cidx + 1 < nchunks) prefetch(t0 + kTC);
 
+        // one step of this lane's S states: the exact int32 partials of y
+        auto update = [&](int t, int xv, int dmv, int &yhi, int &ylo) {
+            int32_t nt[S];
+            if constexpr (MODEL) {
+                xv = (xv * s_dt[dmv + 20] + 512) >> 10;           // rshr(xs * dt, 10)
+                for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + dmv, 0, 32000);
+            } else {
+                for (int s = 0; s < S; ++s) nt[s] = ndec[s];
+            }
+            uint32_t bw[(S + 3) / 4], cw[(S + 3) / 4];
+            if constexpr (S >= 4) {
+                for (int q = 0; q < S / 4; ++q) {
+                    bw[q] = *reinterpret_cast<const uint32_t *>(&s_b[t][g * S + 4 * q]);
+                    cw[q] = *reinterpret_cast<const uint32_t *>(&s_c[t][g * S + 4 * q]);
+                }
+            } else {
+                uint32_t bb = 0, cc = 0;
+                for (int s = 0; s < S; ++s) {
+                    bb |= (uint32_t)(uint8_t)s_b[t][g * S + s] << (8 * s);
+                    cc |= (uint32_t)(uint8_t)s_c[t][g * S + s] << (8 * s);
+                }
+                bw[0] = bb;
+                cw[0] = cc;
+            }
+            yhi = 0;
+            ylo = 0;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int bv = sbyte(bw[s >> 2], s & 3);
+                const int cv = sbyte(cw[s >> 2], s & 3);
+                const int u = __mul24(bv, xv);
+                const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt[s]) >> k);
+                const int d = __mul24(hh[s], nt[s]) + c;
+                const int hn = __builtin_elementwise_add_sat(d, u);
+                hh[s] = hn >> k;
+                hl[s] = hn & kmask;
+                yhi += __mul24(cv, hh[s]);
+                ylo += __mul24(cv, hl[s]);
+            }
+        };
         for (int t4 = 0; t4 < tn; t4 += 4) {
             const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_xa[0][ch][t4]);
             uint32_t dmw = 0, zw = 0;
@@ -196,6 +241,34 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                 zw = *reinterpret_cast<const uint32_t *>(&s_xa[2][ch][t4]);
             }
             const int tend = min(4, tn - t4);
+            if constexpr (DEFER) {
+                if (tend == 4) {
+                    // the eight partials of the group reduced stage by stage
+                    // across all eight (no DPP wait states)
+                    int y[8];
+#pragma unroll
+                    for (int tt = 0; tt < 4; ++tt)
+                        update(t4 + tt, sbyte(xw, tt), MODEL ? clamp32(sbyte(dmw, tt), -20, 20) : 0, y[2 * tt],
+                               y[2 * tt + 1]);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) if constexpr (G >= 2) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0xB1, 0xF, 0xF, false);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) if constexpr (G >= 4) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0x4E, 0xF, 0xF, false);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) if constexpr (G >= 8) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0x141, 0xF, 0xF, false);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) if constexpr (G >= 16) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0x140, 0xF, 0xF, false);
+#pragma unroll
+                    for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][ch] = make_int2(y[2 * tt], y[2 * tt + 1]);
+                } else {
+                    for (int tt = 0; tt < tend; ++tt) {
+                        int yhi, ylo;
+                        update(t4 + tt, sbyte(xw, tt), MODEL ? clamp32(sbyte(dmw, tt), -20, 20) : 0, yhi, ylo);
+                        s_y[t4 + tt][ch] = make_int2(group_sum<G>(yhi), group_sum<G>(ylo));
+                    }
+                }
+                continue;
+            }
             for (int tt = 0; tt < tend; ++tt) {
                 const int t = t4 + tt;
                 int xv = sbyte(xw, tt);
@@ -253,6 +326,25 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             }
         }
         __syncthreads();
+        if constexpr (DEFER) {
+            // chunk epilogue: y = sat32(yhi * 2^k + ylo), then the gate and requant
+            // (model mode) or the int32 output
+            for (int i = tid; i < kTC * CH; i += kThreads) {
+                const int tt = i / CH, cc = i % CH;
+                if (tt < tn) {
+                    const int2 yv = s_y[tt][cc];
+                    const int32_t y32 = sat32_64(((int64_t)yv.x << k) + yv.y);
+                    if constexpr (MODEL) {
+                        const int zv = s_xa[2][cc][tt];
+                        const int64_t yg = ((int64_t)y32 * s_gate[zv + 128]) >> 15;
+                        s_o8[tt][cc] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
+                    } else {
+                        s_o32[tt][cc] = y32;
+                    }
+                }
+            }
+            __syncthreads();
+        }
         // ---- write the staged outputs of this chunk
         if constexpr (MODEL) {
             for (int i = tid; i < kTC * X16; i += kThreads) {
