@@ -12,7 +12,7 @@ bytes; the prefill block scan (timed with HIP events around each launch inside
 the timed steps) against HBM and the int32 VALU rate; and the CPU oracle (C,
 OpenMP on every host core) on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--kernels]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-kernels]
     python bench.py --pmc-probe     # only the dominant kernel + a copy of known size, for rocprofv3 --pmc
     python bench.py --gemm-probe    # only the config-2 prefill GEMM (20 launches), for rocprofv3 counters
     python bench.py --scan-probe    # only the scan kernels at their benchmark shapes, for rocprofv3 counters
@@ -36,6 +36,9 @@ VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 393
 # shape, measured with rocprofv3 --pmc SQ_INSTS_VALU (wave64 instructions x 64
 # / updates; profiles/scan_kernels_valu_pmc.md)
 SCAN_LANE_OPS_PER_UPDATE = 17.71
+# the same for the config-4 chunked multi-head scan (B4 L8192, 24 heads x 64, N128)
+C4_LANE_OPS_PER_UPDATE = 11.81
+MFMA_I8_PEAK_TOPS = 5000.0
 
 
 def scan_bytes(B, L, D, N):
@@ -326,7 +329,10 @@ def kernel_table():
     ms = _time_kernel(lambda: ops.dyadic_scan(x, b, c, n, 15))
     byt = 696320
     out["config1_scan"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
-                           "G_updates_s": 256 * 512 * 16 / ms / 1e6}
+                           "G_updates_s": 256 * 512 * 16 / ms / 1e6,
+                           "roofline": {"bound": "latency (0.7 MB, 2.1 M updates per launch)", "achieved":
+                                        byt / ms / 1e6, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                        "frac": byt / ms / 1e6 / HBM_PEAK_GBS}}
     # config 2: GEMM M4096 K768 N3072 -> int8, and GEMV M1
     M, K, N = 4096, 768, 3072
     a = t8(M, K)
@@ -334,8 +340,10 @@ def kernel_table():
     o8 = torch.empty((M, N), dtype=torch.int8, device=dev)
     ms = _time_kernel(lambda: ops.bitlinear(a, wp, ops.OUT_INT8, N, shift=5, out=o8, path="gemm"))
     tops = 2 * M * N * K / ms / 1e9
-    out["config2_gemm"] = {"ms": ms, "TOPS": tops, "mfma_frac": tops / 5000.0,
-                           "GB_s": 16318464 / ms / 1e6}
+    out["config2_gemm"] = {"ms": ms, "TOPS": tops, "mfma_frac": tops / MFMA_I8_PEAK_TOPS,
+                           "GB_s": 16318464 / ms / 1e6,
+                           "roofline": {"bound": "mfma", "achieved": tops, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
+                                        "frac": tops / MFMA_I8_PEAK_TOPS}}
     copies = 512
     wrot = wp.repeat(copies, 1).view(copies, N, K // 4)
     a1 = a[:1].contiguous()
@@ -348,7 +356,9 @@ def kernel_table():
     ms = _time_kernel(gemv, iters=copies)
     byt = 593664
     out["config2_gemv_m1"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
-                              "note": "weights rotated over 512 copies (302 MB > MALL)"}
+                              "note": "weights rotated over 512 copies (302 MB > MALL)",
+                              "roofline": {"bound": "hbm", "achieved": byt / ms / 1e6, "peak": HBM_PEAK_GBS,
+                                           "unit": "GB/s", "frac": byt / ms / 1e6 / HBM_PEAK_GBS}}
     # config-3 decode GEMVs at batch 8
     for name, (NN, KK) in {"in_proj": (3072, 768), "out_proj": (768, 1536), "lm_head": (32000, 768)}.items():
         w = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(NN, KK), dtype=np.int8))).to(dev)
@@ -385,6 +395,8 @@ def kernel_table():
         "decode_ms_per_step": ms_dec, "decode_tok_s": 64 / (ms_dec * 1e-3),
         "decode_bytes_per_step": sb, "decode_GB_s": sb / (ms_dec * 1e-3) / 1e9,
         "decode_hbm_frac": sb / (ms_dec * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "roofline": {"bound": "hbm", "kernel": "whole decode step", "achieved": sb / (ms_dec * 1e-3) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": sb / (ms_dec * 1e-3) / 1e9 / HBM_PEAK_GBS},
         "note": "device-generated random weights; decode steps include the host-side graph launch"}
     del run5, st5, lg5
     torch.cuda.empty_cache()
@@ -436,7 +448,11 @@ def kernel_table():
     byt = 452984928
     upd = B * L * H * P * NS
     out["config4_ssd"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
-                          "G_updates_s": upd / ms / 1e6}
+                          "G_updates_s": upd / ms / 1e6,
+                          "roofline": {"bound": "valu", "lane_ops_per_update": C4_LANE_OPS_PER_UPDATE,
+                                       "achieved": C4_LANE_OPS_PER_UPDATE * upd / ms / 1e6, "peak": VALU_PEAK_GOPS,
+                                       "unit": "G lane-ops/s",
+                                       "frac": C4_LANE_OPS_PER_UPDATE * upd / ms / 1e6 / VALU_PEAK_GOPS}}
     return out
 
 
@@ -447,7 +463,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=256)
-    ap.add_argument("--kernels", action="store_true", help="also time each config's kernel")
+    ap.add_argument("--kernels", action="store_true", help="(default) time each config's kernels")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
     ap.add_argument("--pmc-probe", action="store_true", help="only the dominant kernel and a copy (for counters)")
     ap.add_argument("--gemm-probe", action="store_true", help="only the config-2 prefill GEMM (for counters)")
     ap.add_argument("--scan-probe", action="store_true", help="only the scan kernels at their benchmark shapes "
@@ -592,7 +609,8 @@ def main():
             "valu_frac": SCAN_LANE_OPS_PER_UPDATE * updates / (scan_avg_ms * 1e-3) / (VALU_PEAK_GOPS * 1e9),
         },
     }
-    if args.kernels:
+    if not args.no_kernels:
+        # configs 1, 2, 4, 5 and the shipped configuration, each against its roof
         line["kernels"] = kernel_table()
     if not args.no_cpu:
         threads = len(os.sched_getaffinity(0))
