@@ -213,6 +213,24 @@ mi_status mi_conv_squareplus(const int8_t *xz, int xz_stride, const int8_t *conv
                              const int32_t *conv_b, const int8_t *state_in, int8_t *state_out,
                              int8_t *xs, int batch, int len, int d_inner, void *stream);
 
+/* Prefill in_proj with the conv + squareplus of its x half fused into the
+ * GEMM epilogue: in_proj, chunk, conv1d, clamp and squareplus of
+ * MambaIntegerBlock.forward (mamba_integer_model.py:400-411), the steps the
+ * reference fuses as fused_squareplus_clamp (fused_activations.py:89-119,
+ * 229-262).  a int8 [batch*len, lda] (the normalized rows), w_in packed
+ * [2*d_inner, d_model/16 words] (16-byte aligned), shift = in_proj requant
+ * shift.  Writes xs int8 [batch*len, d_inner] = squareplus(conv(x)), the z
+ * half into xz columns [d_inner, 2*d_inner) (row stride ldxz, 16-byte
+ * aligned; the x half is not written) and state_out [batch,3,d_inner] = the
+ * last three x rows of each sequence; state_in [batch,3,d_inner] nullable
+ * (zeros), and must not overlap state_out.  Identical to mi_bitlinear
+ * (MI_OUT_INT8) followed by mi_conv_squareplus.  d_inner % 128 == 0,
+ * d_model % 64 == 0. */
+mi_status mi_in_proj_conv(const int8_t *a, int lda, const uint8_t *w_in, int shift,
+                          const int8_t *conv_w, const int32_t *conv_b, const int8_t *state_in,
+                          int8_t *state_out, int8_t *xs, int8_t *xz, int ldxz, int batch, int len,
+                          int d_model, int d_inner, void *stream);
+
 /* Fused model scan (spec rules 4.7-4.11; MambaIntegerBlock.forward,
  * mamba_integer_model.py:413-444): decay from base + dm, dt from dm, input
  * xs*dt (x) B, scan, y = C.h, gate by z, requant.

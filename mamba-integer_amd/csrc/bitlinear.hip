@@ -132,8 +132,24 @@ struct GemmStage {
     int wmask;   // 0 for the weight words of a K tail beyond k
 };
 
-template <int KIND, bool LDSOUT, int NI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs g) {
+// The in_proj GEMM of a prefill with the depthwise conv + squareplus of the x
+// half in its epilogue (gemm_conv_kernel).  Blocks [0, x_blocks) own x-half
+// tiles whose 128 staged token rows start 3 rows before the 125 rows they
+// store, so the conv window of every stored row lies in the block's own tile;
+// the other blocks own plain 128-row z-half tiles.
+constexpr int kConvRows = kBM - 3;
+struct ConvArgs {
+    const int8_t *w;        // [D][4] taps, w[c][j] multiplies x[t - 3 + j]
+    const int32_t *b;       // [D]
+    const int8_t *st_in;    // [batch][3][D] x[-3..-1] per sequence, or null (zeros)
+    int8_t *st_out;         // [batch][3][D] the last three x rows of each sequence
+    int8_t *xs;             // [M][D] squareplus(conv(x))
+    int D, L;               // d_inner, tokens per sequence (M = batch * L)
+    int x_blocks;           // ceil(M / kConvRows) * D / kBN
+};
+
+template <int KIND, bool LDSOUT, int NI, bool CONV>
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, const ConvArgs &cv) {
     // each wave computes NI x MJ tiles of 16 x 16 outputs: NI along n (weight
     // rows), MJ along m (tokens); the four waves tile the 128 x 128 block as
     // WN x WM
@@ -152,9 +168,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int l16 = lane & 15, lq = lane >> 4;
 
     // blockIdx.x walks m-tiles fastest so the blocks that share a weight tile run together
-    const int mtiles = (g.M + kBM - 1) / kBM;
-    const int m0 = (blockIdx.x % mtiles) * kBM;
-    const int n0 = (blockIdx.x / mtiles) * kBN;
+    int m0, n0;
+    bool xblk = false;   // block-uniform: a conv x-half tile
+    if constexpr (CONV) {
+        const int bid = blockIdx.x;
+        if (bid < cv.x_blocks) {
+            const int xmt = (g.M + kConvRows - 1) / kConvRows;
+            xblk = true;
+            m0 = (bid % xmt) * kConvRows - 3;
+            n0 = (bid / xmt) * kBN;
+        } else {
+            const int zb = bid - cv.x_blocks, mtiles = (g.M + kBM - 1) / kBM;
+            m0 = (zb % mtiles) * kBM;
+            n0 = cv.D + (zb / mtiles) * kBN;
+        }
+    } else {
+        const int mtiles = (g.M + kBM - 1) / kBM;
+        m0 = (blockIdx.x % mtiles) * kBM;
+        n0 = (blockIdx.x / mtiles) * kBN;
+    }
     const int nk = (g.K + kBK - 1) / kBK;
 
     const int arow = tid >> 3, ac16 = tid & 7;   // activation rows arow + 32j, 16 bytes at k = 16 * ac16
@@ -162,7 +194,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int8_t *pa[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int m = min(m0 + arow + 32 * j, g.M - 1);
+        // rows before the first (the halo of the first x-half tile) read row 0;
+        // rows past the last read row M - 1: neither reaches a stored output
+        int m = min(m0 + arow + 32 * j, g.M - 1);
+        if constexpr (CONV) m = max(m, 0);
         pa[j] = g.a + (int64_t)m * g.lda + ac16 * 16;
     }
     const uint32_t *pw = g.w + (int64_t)min(n0 + wrow, g.N - 1) * g.kw + wh * 4;
@@ -238,6 +273,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     if constexpr (LDSOUT) {
         int8_t *sO = &sA[0][0];
+        // conv operands of this thread's 4 channels, loaded before the tile is requantised
+        const int cg = tid & 31, ch = n0 + 4 * cg;
+        uint32_t tw[4] = {0, 0, 0, 0};
+        int32_t tb[4] = {0, 0, 0, 0};
+        if constexpr (CONV) {
+            if (xblk) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    tw[r] = *reinterpret_cast<const uint32_t *>(cv.w + (int64_t)(ch + r) * 4);
+                    tb[r] = cv.b[ch + r];
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < MJ; ++j)
 #pragma unroll
@@ -252,6 +300,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                 *reinterpret_cast<uint32_t *>(&sO[(mb + j * 16 + l16) * kOpitch + nb + i * 16 + 4 * lq]) = pk;
             }
         __syncthreads();
+        if constexpr (CONV) {
+            if (xblk) {
+                // depthwise conv + squareplus (spec rules 4.3-4.4) down the tile:
+                // thread (cg, run) takes channels ch..ch+3 of staged rows
+                // 3 + 16 run .. (16 rows; the last run 13), walking token
+                // positions t of sequence sb; the window rows before a
+                // sequence start come from the conv state
+                const int run = tid >> 5;
+                const int i0 = 3 + 16 * run, i1 = min(i0 + 16, kBM);
+                int gm = m0 + i0;   // >= 0: m0 >= -3
+                if (gm < g.M) {
+                    int sb = gm / cv.L, t = gm - sb * cv.L;
+                    auto row = [&](int i) { return *reinterpret_cast<const uint32_t *>(&sO[i * kOpitch + 4 * cg]); };
+                    auto state = [&](int k) -> uint32_t {  // x[k] of sequence sb, k in [-3, -1]
+                        return cv.st_in ? *reinterpret_cast<const uint32_t *>(cv.st_in + ((int64_t)sb * 3 + 3 + k) * cv.D + ch)
+                                        : 0u;
+                    };
+                    // per-channel windows: byte j of win[r] is x[t - 3 + j] of channel
+                    // ch + r once row t is shifted in (v_perm_b32 drops byte 0 and
+                    // appends the new row's byte r), so the conv is one v_dot4
+                    uint32_t win[4] = {0, 0, 0, 0};
+                    auto push = [&](uint32_t v) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            win[r] = __builtin_amdgcn_perm(v, win[r], 0x00030201u | ((uint32_t)(4 + r) << 24));
+                    };
+                    // the window of the run's first row: rows of its own sequence, the
+                    // conv state before the sequence start
+                    for (int j = 3; j >= 1; --j) push(t - j >= 0 ? row(i0 - j) : state(t - j));
+                    for (int i = i0; i < i1 && gm < g.M; ++i, ++gm) {
+                        if (t == 0) {
+                            if (i > i0)
+                                for (int j = 3; j >= 1; --j) push(state(-j));
+                            // a sequence shorter than the window keeps part of the old state
+                            for (int j = 0; j < 3 - cv.L; ++j)
+                                *reinterpret_cast<uint32_t *>(cv.st_out + ((int64_t)sb * 3 + j) * cv.D + ch) =
+                                    state(cv.L + j - 3);
+                        }
+                        const uint32_t cur = row(i);
+                        push(cur);
+                        uint32_t o = 0;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int32_t c = __builtin_amdgcn_sdot4((int)win[r], (int)tw[r], tb[r], false);
+                            o |= (uint32_t)(sqp_q(c) & 255) << (8 * r);
+                        }
+                        *reinterpret_cast<uint32_t *>(cv.xs + (int64_t)gm * cv.D + ch) = o;
+                        if (t >= cv.L - 3)
+                            *reinterpret_cast<uint32_t *>(cv.st_out + ((int64_t)sb * 3 + t - (cv.L - 3)) * cv.D + ch) = cur;
+                        if (++t == cv.L) {
+                            t = 0;
+                            ++sb;
+                        }
+                    }
+                }
+                return;
+            }
+        }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int row = arow + 32 * p;
@@ -328,6 +434,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             for (int i = 0; i < NI; ++i) store4<KIND>(g, m, n0 + nb + i * 16 + 4 * lq, acc[i][j]);
         }
     }
+}
+
+template <int KIND, bool LDSOUT, int NI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(GemmArgs g) {
+    gemm_tile<KIND, LDSOUT, NI, false>(g, ConvArgs{});
+}
+
+// in_proj (int8 out, shifted) with the conv + squareplus of the x half fused
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_conv_kernel(GemmArgs g,
+                                                                                              ConvArgs cv) {
+    gemm_tile<MI_OUT_INT8, true, kGemmNI, true>(g, cv);
 }
 
 // gemm_any_kernel: any k % 16 == 0 and 4-byte aligned weights (e.g. dt_proj
@@ -892,6 +1009,47 @@ extern "C" mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const
     g.stats_parts = stats_parts;
     hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16)), dim3(512), 0,
                        as_stream(stream), g);
+    return check_launch(fn);
+}
+
+extern "C" mi_status mi_in_proj_conv(const int8_t *a, int lda, const uint8_t *w_in, int shift, const int8_t *conv_w,
+                                     const int32_t *conv_b, const int8_t *state_in, int8_t *state_out, int8_t *xs,
+                                     int8_t *xz, int ldxz, int batch, int len, int d_model, int d_inner,
+                                     void *stream) {
+    const char *fn = "mi_in_proj_conv";
+    clear_error();
+    MI_REQUIRE(batch >= 0 && len >= 0 && d_inner >= 0, MI_ERR_BAD_DIM, "%s: negative size", fn);
+    // tile counts are computed as (m + kBM - 1) / kBM in int
+    MI_REQUIRE((int64_t)batch * len <= INT32_MAX - kBM && (int64_t)d_inner * 2 <= INT32_MAX, MI_ERR_BAD_DIM,
+               "%s: size exceeds int32", fn);
+    const int m = batch * len;
+    mi_status st = validate(fn, a, lda, w_in, xz, ldxz, MI_OUT_INT8, m, 2 * d_inner, d_model, shift, 0, nullptr);
+    if (st != MI_OK || (int64_t)m * d_inner == 0) return st;
+    MI_REQUIRE(d_inner % kBN == 0, MI_ERR_BAD_DIM, "%s: d_inner=%d must be a multiple of %d", fn, d_inner, kBN);
+    MI_REQUIRE(d_model % 64 == 0, MI_ERR_BAD_DIM, "%s: d_model=%d must be a multiple of 64", fn, d_model);
+    MI_REQUIRE(conv_w && conv_b && state_out && xs, MI_ERR_NULL_POINTER,
+               "%s: conv_w, conv_b, state_out and xs are required", fn);
+    MI_REQUIRE(aligned(w_in, 16) && aligned(xz, 16) && ldxz % 16 == 0, MI_ERR_BAD_ALIGNMENT,
+               "%s: w_in and xz must be 16-byte aligned and ldxz a multiple of 16", fn);
+    MI_REQUIRE(aligned(conv_w, 4) && aligned(conv_b, 4) && aligned(xs, 4) && aligned(state_out, 4) &&
+                   aligned(state_in, 4),
+               MI_ERR_BAD_ALIGNMENT, "%s: conv_w, conv_b, xs and the states must be 4-byte aligned", fn);
+    const uintptr_t sbytes = (uintptr_t)batch * 3 * (uintptr_t)d_inner;
+    if (state_in) {
+        const uintptr_t i0 = reinterpret_cast<uintptr_t>(state_in), o0 = reinterpret_cast<uintptr_t>(state_out);
+        // blocks read the old state of a sequence's first rows while others
+        // write the new state of its last rows: the buffers must be distinct
+        MI_REQUIRE(i0 + sbytes <= o0 || o0 + sbytes <= i0, MI_ERR_BAD_ARG, "%s: state_in and state_out overlap", fn);
+    }
+    const int64_t nt = d_inner / kBN;
+    const int64_t xb = (int64_t)((m + kConvRows - 1) / kConvRows) * nt;
+    const int64_t zb = (int64_t)((m + kBM - 1) / kBM) * nt;
+    MI_REQUIRE(xb + zb <= INT32_MAX, MI_ERR_BAD_DIM, "%s: grid too large", fn);
+    GemmArgs g = make_args(a, lda, w_in, xz, ldxz, m, 2 * d_inner, d_model, shift, 0, 0, nullptr, 0.0f, nullptr);
+    ConvArgs cv{};
+    cv.w = conv_w; cv.b = conv_b; cv.st_in = state_in; cv.st_out = state_out; cv.xs = xs;
+    cv.D = d_inner; cv.L = len; cv.x_blocks = (int)xb;
+    hipLaunchKernelGGL(gemm_conv_kernel, dim3((unsigned)(xb + zb)), dim3(256), 0, as_stream(stream), g, cv);
     return check_launch(fn);
 }
 

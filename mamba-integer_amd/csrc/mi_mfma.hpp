@@ -36,7 +36,7 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 __device__ __forceinline__ int sqp_q(int32_t c) {
     const int32_t v = clamp32(c, -51200, 51200);
     const uint32_t av = (uint32_t)(v < 0 ? -v : v);
-    const uint32_t Y = av * av + (1u << 22);  // < 2^32
+    const uint32_t Y = __umul24(av, av) + (1u << 22);  // av <= 51200: the 24-bit product is exact, < 2^32
     uint32_t s = (uint32_t)__builtin_amdgcn_sqrtf((float)Y);
     s -= __umul24(s, s) > Y ? 1u : 0u;
     s += __umul24(s + 1, s + 1) <= Y ? 1u : 0u;

@@ -38,6 +38,7 @@ SIGNATURES = {
     "mi_bitshift_norm": [P, P, P, I, I, P, P],
     "mi_embed": [P, P, P, I, I, I, P, I, P],
     "mi_conv_squareplus": [P, I, P, P, P, P, P, I, I, I, P],
+    "mi_in_proj_conv": [P, I, P, I, P, P, P, P, P, P, I, I, I, I, I, P],
     "mi_block_scan": [P, P, P, I, I, P, I, I, P, I, I, P, P, P, I, I, I, I, P],
     "mi_bitshift_norm_v2": [P, P, P, I, I, P, P],
     "mi_ssd_block_scan": [P, P, I, P, I, I, P, I, I, P, P, P, I, I, I, I, P],

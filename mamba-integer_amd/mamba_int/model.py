@@ -176,8 +176,12 @@ class IntegerMambaRunner:
             self._layer_ssd(ly, ws, B, L, conv_state, h_state, fresh, stats_in, stats_out)
             return
         ops.bitshift_norm(ws.r, ly.gamma, out=ws.a, row_stats=stats_in)
-        ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
         step = L == 1 and not fresh
+        conv_done = not step and self._in_proj_conv_ok()
+        if conv_done:
+            self._in_proj_conv(ly, ws, B, conv_state, fresh)
+        else:
+            ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
         if step and self._conv_xproj_ok():
             # one recurrent step per sequence: conv step + x_proj (four blocks per token
             # leaving int32 partials where d_inner allows, else one block per token),
@@ -199,8 +203,9 @@ class IntegerMambaRunner:
                 ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
                               res_shift=ly.res_shift, row_stats=stats_out)
             return
-        ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
-                            state_out=conv_state, out=ws.xs, batch=B)
+        if not conv_done:
+            ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
+                                state_out=conv_state, out=ws.xs, batch=B)
         ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
         if step:
             # one recurrent step per sequence (any batch): dt_proj + scan step + gate
@@ -227,9 +232,12 @@ class IntegerMambaRunner:
         dims = self.dims
         D, d = dims.d_inner, dims.d_model
         ops.bitshift_norm(ws.r, ly.gamma, out=ws.a, row_stats=stats_in, v2=True)
-        ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
-        ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
-                            state_out=conv_state, out=ws.xs, batch=B)
+        if not (L == 1 and not fresh) and self._in_proj_conv_ok():
+            self._in_proj_conv(ly, ws, B, conv_state, fresh)
+        else:
+            ops.bitlinear(ws.a, ly.w_in, ops.OUT_INT8, 2 * D, shift=ly.s_in, out=ws.xz)
+            ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
+                                state_out=conv_state, out=ws.xs, batch=B)
         ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
         if self.scan_timer is not None:
             self.scan_timer[0]()
@@ -239,6 +247,20 @@ class IntegerMambaRunner:
             self.scan_timer[1]()
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
                       res_shift=ly.res_shift, row_stats=stats_out)
+
+    def _in_proj_conv_ok(self) -> bool:
+        """mi_in_proj_conv's limits: d_inner a multiple of 128, d_model of 64."""
+        return self.dims.d_inner % 128 == 0 and self.dims.d_model % 64 == 0
+
+    def _in_proj_conv(self, ly: DeviceLayer, ws: _Workspace, B: int, conv_state: torch.Tensor,
+                      fresh: bool) -> None:
+        """Prefill in_proj with the conv + squareplus of the x half in its epilogue:
+        writes ws.xs, the z half of ws.xz and the new conv state.  The old state
+        is read from a copy (blocks read a sequence's old state while others
+        write its new one)."""
+        prev = None if fresh else conv_state.clone()
+        ops.in_proj_conv(ws.a, ly.w_in, ly.s_in, self.dims.d_inner, ly.conv_w, ly.conv_b, B, conv_state,
+                         state_in=prev, xs=ws.xs, xz=ws.xz)
 
     def _step_parts(self, ws: _Workspace) -> bool:
         """The batched one-token step (conv step + x_proj kernel) hands the row

@@ -208,6 +208,27 @@ def conv_squareplus(xz: torch.Tensor, d_inner: int, conv_w, conv_b, state_in=Non
     return xs
 
 
+def in_proj_conv(a: torch.Tensor, w_in: torch.Tensor, shift: int, d_inner: int, conv_w, conv_b, batch: int,
+                 state_out: torch.Tensor, state_in=None, xs=None, xz=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Prefill in_proj + conv + squareplus: a int8 [batch*L, d_model] -> (xs int8 [batch*L, d_inner],
+    xz int8 [batch*L, 2*d_inner] with only the z half written); state_out int8 [batch, 3, d_inner]
+    receives the last three x rows of each sequence (state_in: the previous ones, or None for zeros)."""
+    _req(a, torch.int8, "a"); _req(conv_w, torch.int8, "conv_w"); _req(conv_b, torch.int32, "conv_b")
+    _req(state_out, torch.int8, "state_out")
+    T, d = a.shape
+    L = T // batch if batch else 0
+    if batch and L * batch != T:
+        raise ValueError("in_proj_conv: rows must be batch * len")
+    if xs is None:
+        xs = torch.empty((T, d_inner), dtype=torch.int8, device=a.device)
+    if xz is None:
+        xz = torch.empty((T, 2 * d_inner), dtype=torch.int8, device=a.device)
+    _lib.call("mi_in_proj_conv", _ptr(a), a.stride(0), _ptr(w_in), shift, _ptr(conv_w), _ptr(conv_b),
+              _ptr(_opt(state_in, torch.int8, "state_in")), _ptr(state_out), _ptr(xs), _ptr(xz), xz.stride(0),
+              batch, L, d, d_inner, _stream())
+    return xs, xz
+
+
 def block_scan(xs, dm, xp, b_off: int, z, z_off: int, base, decay_shift: int, s_y: int,
                h_in=None, h_out=None, out=None, batch: Optional[int] = None) -> torch.Tensor:
     """Fused model scan; xs/dm int8 [B,L,D] (or [B*L,D] with ``batch``)."""

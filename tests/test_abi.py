@@ -82,6 +82,16 @@ def _fake(n=64):
     (("mi_xpart_dt_scan_step", None, 96, 5, 48, None, 2, None, None, 3072, 1536, None, 15, 12, None, None, 70000,
       1536, 16, None), 2, "65535"),
     (("mi_conv_step_xpart", "A16", 1024, "W4", "A16", "A16", "A16", "A16", 80, "A16", 4, 1024, None), 3, "aligned"),
+    (("mi_in_proj_conv", "A16", 64, "A16", 5, "A16", "A16", None, "A16", "A16", "O16", 208, 1, 4, 64, 100, None), 2,
+     "multiple of 128"),
+    (("mi_in_proj_conv", "A16", 32, "A16", 5, "A16", "A16", None, "A16", "A16", "O16", 256, 1, 4, 32, 128, None), 2,
+     "multiple of 64"),
+    (("mi_in_proj_conv", "A16", 64, "A16", 5, "A16", "A16", None, "A16", None, "O16", 256, 1, 4, 64, 128, None), 1,
+     "required"),
+    (("mi_in_proj_conv", "A16", 64, "A16", 5, "A16", "A16", "A16", "A16", "A16", "O16", 256, 1, 4, 64, 128, None), 4,
+     "overlap"),
+    (("mi_in_proj_conv", "A16", 64, "W4", 5, "A16", "A16", None, "A16", "A16", "O16", 256, 1, 4, 64, 128, None), 3,
+     "16-byte"),
 ])
 def test_argument_validation(call, status, needle):
     from mamba_int import _lib
