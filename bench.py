@@ -30,7 +30,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the decode in_proj stage kernel at batch 8, measured
 # with rocprofv3 FETCH_SIZE and WRITE_SIZE (one run each) and scaled by the
 # same counters on a 256 MiB device copy (FETCH x 2.000, WRITE x 1.000)
-IN_PROJ_STAGE_TRAFFIC_B8 = 2059174
+IN_PROJ_STAGE_TRAFFIC_B8 = 1456128   # 561.0 KiB x 2 + 300.0 KiB
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 39321.6 G/s
 # VALU lane-ops the prefill block scan issues per state update at the bench
 # shape, measured with rocprofv3 --pmc SQ_INSTS_VALU (wave64 instructions x 64
