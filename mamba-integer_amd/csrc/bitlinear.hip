@@ -636,15 +636,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
 // 16-byte load and the 64 activation bytes of the same k of each token tile;
 // all loads are unconditional from clamped addresses (a clamped row or token
 // only feeds results that are not stored; a chunk past the end is re-read and
-// its products skipped).  The waves' partial sums meet in LDS through integer
-// atomics (exact, order-free), then waves 0-3 finish one token tile each.
+// its products skipped).  The waves' partial sums meet in LDS: up to 8 waves
+// store them as 16-byte vectors (WAVES x FT x 4 x 1 KB) and waves 0-3 add
+// them up for one token tile each; 16 waves add into one copy with integer
+// atomics (exact, order-free; 2 of 3 LDS cycles were bank conflicts at
+// 4 waves, where the stores measured faster).
 // Requires kw % 16 == 0, 16-byte aligned w, a and lda.
 template <int KIND, int FT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
     constexpr int U = WAVES >= 16 ? 1 : 2;  // chunks in flight (16 waves: 128 VGPRs a lane)
-    __shared__ int32_t red[FT][4][64][4];
+    constexpr bool kStore = WAVES <= 8;
+    __shared__ int32_t red[kStore ? 1 : FT][4][64][4];
+    __shared__ v4i part[kStore ? WAVES : 1][kStore ? FT : 1][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
-    for (int i = tid; i < FT * 4 * 64 * 4; i += 64 * WAVES) (&red[0][0][0][0])[i] = 0;
+    if constexpr (!kStore)
+        for (int i = tid; i < FT * 4 * 64 * 4; i += 64 * WAVES) (&red[0][0][0][0])[i] = 0;
     const int n0 = blockIdx.x * 16 * FT;
     const int nchunk = g.kw / 16;
     const uint32_t *wrow[FT];
@@ -687,13 +693,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
             }
         }
     }
-    __syncthreads();  // red zeroed
+    if constexpr (kStore) {
 #pragma unroll
-    for (int f = 0; f < FT; ++f)
+        for (int f = 0; f < FT; ++f)
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+            for (int t = 0; t < 4; ++t) part[wave][f][t][lane] = acc[f][t];
+    } else {
+        __syncthreads();  // red zeroed
 #pragma unroll
-            for (int r = 0; r < 4; ++r) atomicAdd(&red[f][t][lane][r], acc[f][t][r]);
+        for (int f = 0; f < FT; ++f)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) atomicAdd(&red[f][t][lane][r], acc[f][t][r]);
+    }
     __syncthreads();
     if (wave >= 4) return;
     // wave w finishes token tile w: lane (token 16w + l16, group lq) holds
@@ -701,7 +714,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
     const int m = 16 * wave + l16;
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
-        const v4i v = v4i{red[f][wave][lane][0], red[f][wave][lane][1], red[f][wave][lane][2], red[f][wave][lane][3]};
+        v4i v;
+        if constexpr (kStore) {
+            v = part[0][f][wave][lane];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) v += part[w][f][wave][lane];
+        } else {
+            v = v4i{red[f][wave][lane][0], red[f][wave][lane][1], red[f][wave][lane][2], red[f][wave][lane][3]};
+        }
         const RowStat st = store4<KIND>(g, m, n0 + 16 * f + 4 * lq, v);
         if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
     }

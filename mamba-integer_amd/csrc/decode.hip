@@ -797,7 +797,14 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
 // channel owns states 4q..4q+3, as in dt_scan_step_kernel<0, 4>.
 // XP: the x_proj rows arrive as nblk <= kTokMaxParts int32 partial sums per
 // token (mi_xpart_dt_scan_step), summed and requantised while staging.
-template <int TPB, bool XP>
+// S24 (decay_shift 15): the state update in 24-bit multiplies.  With
+// h = hh * 2^15 + hl (0 <= hl < 2^15) and 0 <= nt <= 32000,
+// floor(h * nt / 2^15) = hh * nt + floor(hl * nt / 2^15), where |hh * nt| <
+// 2^31 and hl * nt < 2^32; B * xd fits 32 bits (|xd| <= 813), so the sum
+// saturates with one clamped add; y = C . h accumulates C * (h >> 15) and
+// C * (h & 0x7fff) in two int32 sums (each < 2^28 over a channel's 16
+// states).  Without S24 the same rules run in 64-bit arithmetic.
+template <int TPB, bool XP, bool S24>
 __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_dt[TPB][kMaxR];
     __shared__ __align__(16) int8_t s_bc[TPB][32];
@@ -897,23 +904,45 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
         acc += __shfl_xor(acc, 1);
         acc += __shfl_xor(acc, 2);
         const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
-        const int64_t xd = rshr64((int64_t)xsv[t] * s_dtq[dm + 20], 10);
         const int hv[4] = {h4[t][0], h4[t][1], h4[t][2], h4[t][3]};
         const int bv[4] = {b4.x, b4.y, b4.z, b4.w};
         int32_t hn[4];
         int64_t y = 0;
+        if constexpr (S24) {
+            // |x * dt| <= 127 * 6554: the rounded shift is exact in 32 bits
+            const int xd = (xsv[t] * s_dtq[dm + 20] + 512) >> 10;
+            const int bw = *reinterpret_cast<const int *>(&s_bc[t][4 * q]);
+            const int cw = *reinterpret_cast<const int *>(&s_bc[t][16 + 4 * q]);
+            int yh = 0, yl = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int n = 4 * q + i;
-            const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
-            hn[i] = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[t][n] * xd);
-            y += (int64_t)s_bc[t][16 + n] * hn[i];
+            for (int i = 0; i < 4; ++i) {
+                const int nt = min(max(__builtin_elementwise_add_sat(bv[i], dm), 0), 32000);
+                const int a = __mul24(hv[i] >> 15, nt) + (int)(__umul24((uint32_t)hv[i] & 0x7fffu, (uint32_t)nt) >> 15);
+                const int bn = (bw << (24 - 8 * i)) >> 24, cn = (cw << (24 - 8 * i)) >> 24;
+                hn[i] = __builtin_elementwise_add_sat(a, __mul24(bn, xd));
+                yh += __mul24(cn, hn[i] >> 15);
+                yl += __mul24(cn, hn[i] & 0x7fff);
+            }
+            yh += __shfl_xor(yh, 1);
+            yl += __shfl_xor(yl, 1);
+            yh += __shfl_xor(yh, 2);
+            yl += __shfl_xor(yl, 2);
+            y = (int64_t)yh * 32768 + yl;
+        } else {
+            const int64_t xd = rshr64((int64_t)xsv[t] * s_dtq[dm + 20], 10);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int n = 4 * q + i;
+                const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
+                hn[i] = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[t][n] * xd);
+                y += (int64_t)s_bc[t][16 + n] * hn[i];
+            }
+            y += __shfl_xor(y, 1);
+            y += __shfl_xor(y, 2);
         }
         if (active && m < g.M)
             __builtin_nontemporal_store(v4i{hn[0], hn[1], hn[2], hn[3]},
                                         reinterpret_cast<v4i *>(g.h + ((int64_t)m * g.D + d) * 16 + 4 * q));
-        y += __shfl_xor(y, 1);
-        y += __shfl_xor(y, 2);
         if (active && q == 0 && m < g.M) {
             const int64_t yg = ((int64_t)sat32_64(y) * s_gate[zv[t] + 128]) >> 15;
             g.yo[(int64_t)m * g.D + d] = (int8_t)clamp64(rshr64(yg, g.s_y), -127, 127);
@@ -1106,10 +1135,13 @@ extern "C" mi_status mi_dt_scan_step(const int8_t *xp, int xp_stride, int dt_ran
     const bool vec = nstate == 16 && aligned(h_state, 16) && aligned(base, 16);
     // two tokens per block measured fastest at batch 64 (2.40 ms per d2048x48 step
     // against 2.44 with four, 2.54 with eight and 2.46 with one)
-    if (vec && m >= 2)
-        hipLaunchKernelGGL((dt_scan_tok_kernel<2, false>), dim3((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2)),
-                           dim3(256), 0, as_stream(stream), g);
-    else if (vec) hipLaunchKernelGGL((dt_scan_step_kernel<0, 4>), grid, dim3(256), 0, as_stream(stream), g);
+    if (vec && m >= 2) {
+        const dim3 tgrid((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2));
+        if (decay_shift == 15)
+            hipLaunchKernelGGL((dt_scan_tok_kernel<2, false, true>), tgrid, dim3(256), 0, as_stream(stream), g);
+        else
+            hipLaunchKernelGGL((dt_scan_tok_kernel<2, false, false>), tgrid, dim3(256), 0, as_stream(stream), g);
+    } else if (vec) hipLaunchKernelGGL((dt_scan_step_kernel<0, 4>), grid, dim3(256), 0, as_stream(stream), g);
     else hipLaunchKernelGGL((dt_scan_step_kernel<0, 0>), grid, dim3(256), 0, as_stream(stream), g);
     return check_launch("mi_dt_scan_step");
 }
@@ -1145,11 +1177,14 @@ extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
     const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
     const bool vec = nstate == 16 && aligned(h_state, 16) && aligned(base, 16);
-    if (vec && nblk <= kTokMaxParts && m >= 2 && aligned(xpart, 16))
+    if (vec && nblk <= kTokMaxParts && m >= 2 && aligned(xpart, 16)) {
         // few partials (mi_conv_step_xpart's channel quarters): two tokens per block
-        hipLaunchKernelGGL((dt_scan_tok_kernel<2, true>), dim3((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2)),
-                           dim3(256), 0, as_stream(stream), g);
-    else if (vec)
+        const dim3 tgrid((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2));
+        if (decay_shift == 15)
+            hipLaunchKernelGGL((dt_scan_tok_kernel<2, true, true>), tgrid, dim3(256), 0, as_stream(stream), g);
+        else
+            hipLaunchKernelGGL((dt_scan_tok_kernel<2, true, false>), tgrid, dim3(256), 0, as_stream(stream), g);
+    } else if (vec)
         hipLaunchKernelGGL((dt_scan_step_kernel<-1, 4>), grid, dim3(256), 0, as_stream(stream), g);
     else
         hipLaunchKernelGGL((dt_scan_step_kernel<-1, 0>), grid, dim3(256), 0, as_stream(stream), g);

@@ -81,6 +81,51 @@ def test_dt_scan_step(cuda, m, D, N, R):
     assert np.array_equal(H(hg), h_ref)
 
 
+@pytest.mark.parametrize("m,k", [(2, 15), (64, 15), (5, 15), (8, 12), (3, 17)])
+def test_batched_scan_step_full_range(cuda, m, k):
+    """The batched scan step (two tokens per block: 24-bit multiplies at decay
+    shift 15, 64-bit arithmetic at other shifts), from int8 x_proj rows and
+    from int32 x_proj partials, over the whole int32 state range: states at
+    INT32_MIN / INT32_MAX and uniform over int32, decay numerators below 0 and
+    above 32000 before the clamp (base values up to the int32 limits), x, B and
+    C over the whole int8 range.  Decay numerators are clamped to 32000, so at
+    shifts 15 and 17 every decay is below one and no state can saturate; at
+    shift 12 the states grow and both saturation directions occur."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(100 * m + k)
+    D, N, R = 1024, 16, 48
+    W = R + 2 * N
+    xs = i8(rng, m, D)
+    z = i8(rng, m, 2 * D, lo=-128)
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int64)
+    base[::7, 3] = -50
+    base[::11, 5] = 40000
+    base[0, :4] = [2**31 - 1, 2**31 - 10, -2**31, -2**31 + 5]
+    base = base.astype(np.int32)
+    h0 = rng.integers(-2**31, 2**31, size=(m, D, N), dtype=np.int64).astype(np.int32)
+    h0[:, ::5, 0] = 2**31 - 1
+    h0[:, ::9, 1] = -2**31
+    # x_proj as four int32 partials per token; the int8 rows are their requantised sum
+    xq = rng.integers(-3000, 3000, size=(m, 4, W), dtype=np.int32)
+    xp = np.clip((xq.sum(1) + 16) >> 5, -127, 127).astype(np.int8)
+    dm = O.bitlinear(np.ascontiguousarray(xp[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs.reshape(m, 1, D), dm.reshape(m, 1, D), xp.reshape(m, 1, W), R,
+                                 z.reshape(m, 1, 2 * D), D, base, k, 13, h_state=h0)
+    if k < 15:
+        assert (h_ref == 2**31 - 1).any() and (h_ref == -2**31).any()
+    for form in ("rows", "partials"):
+        hg = T(h0)
+        yo = T(np.zeros((m, D), np.int8))
+        if form == "rows":
+            ops.dt_scan_step(T(xp), R, T(wdt), 2, T(xs), T(z), D, T(base), k, 13, hg, yo)
+        else:
+            ops.xpart_dt_scan_step(T(xq), 5, R, T(wdt), 2, T(xs), T(z), D, T(base), k, 13, hg, yo)
+        assert np.array_equal(H(yo), yo_ref[:, 0]), form
+        assert np.array_equal(H(hg), h_ref), form
+
+
 def test_row_stats_paths(cuda):
     """Embed row statistics, the RESIDUAL epilogue's atomics (GEMV and GEMM) and
     the stats-driven norms equal the reducing norm."""
