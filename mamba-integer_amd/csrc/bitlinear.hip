@@ -727,6 +727,97 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
     }
 }
 
+// gemv64_kernel<KIND, FT, 4> with the activations staged through LDS: every
+// block reads all M x K activation bytes, and read straight into MFMA operands
+// (16 rows x 4 scattered 16-byte pieces per load) they cost more than the
+// weights.  Here each wave copies the 64 x 256-byte activation slab of each of
+// its chunks into its own LDS region with global_load_lds_dwordx4 (one load
+// moves 4 whole rows x 256 bytes, no VGPRs involved), then reads the MFMA B
+// operands from LDS.  Lane i of a load lands at byte 16i of its 1 KB block, so
+// the lane choosing row 4r + i/16 fetches segment (i % 16) ^ (row % 16) of it:
+// the XOR swizzle makes the 16 rows of an operand read fall in 16 different
+// bank groups.  Same chunk ownership and results as gemv64_kernel.
+constexpr int kG64Waves = 4, kG64U = 2;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+template <int KIND, int FT>
+__global__ __launch_bounds__(64 * kG64Waves) void gemv64s_kernel(GemmArgs g) {
+    constexpr int WAVES = kG64Waves, U = kG64U;
+    __shared__ __align__(16) int8_t stage[WAVES][U][64 * 256];
+    static_assert(FT * 4 * 64 * 16 <= U * 64 * 256, "partial sums reuse the wave's staging region");
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
+    const int n0 = blockIdx.x * 16 * FT;
+    const int nchunk = g.kw / 16;
+    const uint32_t *wrow[FT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f) wrow[f] = g.w + (int64_t)min(n0 + 16 * f + l16, g.N - 1) * g.kw;
+    v4i acc[FT][4];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[f][t] = v4i{0, 0, 0, 0};
+    // this lane's row and segment in each 4-row load (rows past M read row M - 1)
+    const int srow = lane >> 4;
+    for (int c0 = wave; c0 < nchunk; c0 += U * WAVES) {
+        v4i wv[U][FT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + WAVES * u < nchunk ? c0 + WAVES * u : c0;
+#pragma unroll
+            for (int f = 0; f < FT; ++f) wv[u][f] = *reinterpret_cast<const v4i *>(wrow[f] + 16 * c + 4 * lq);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 4 * r + srow;
+                const int seg = (lane & 15) ^ (row & 15);
+                const int8_t *src = g.a + (int64_t)min(row, g.M - 1) * g.lda + 256 * c + 16 * seg;
+                __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)&stage[wave][u][r * 1024], 16, 0,
+                                                 0);
+            }
+        }
+        // the slabs are this wave's own: once its loads have landed it reads them
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + WAVES * u < nchunk) {  // same for the whole wave
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v4i xv[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        xv[t] = *reinterpret_cast<const v4i *>(
+                            &stage[wave][u][(16 * t + l16) * 256 + 16 * ((4 * lq + j) ^ l16)]);
+#pragma unroll
+                    for (int f = 0; f < FT; ++f) {
+                        const v4i fw = unpack16((uint32_t)wv[u][f][j]);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) acc[f][t] = mfma_i8(fw, xv[t], acc[f][t]);
+                    }
+                }
+            }
+        }
+        // the next chunks' loads overwrite the slabs: every lane is done reading them
+        __builtin_amdgcn_wave_barrier();
+    }
+    // partial sums into the wave's own region, then waves 0-3 add them up for one token tile each
+    v4i *part = reinterpret_cast<v4i *>(&stage[wave][0][0]);   // [FT][4][64]
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) part[(f * 4 + t) * 64 + lane] = acc[f][t];
+    __syncthreads();
+    const int m = 16 * wave + l16;
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+        v4i v = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w)
+            v += reinterpret_cast<const v4i *>(&stage[w][0][0])[(f * 4 + wave) * 64 + lane];
+        const RowStat st = store4<KIND>(g, m, n0 + 16 * f + 4 * lq, v);
+        if (KIND == MI_OUT_RESIDUAL && g.row_stats) flush_row_stat(g, st, m, lq);
+    }
+}
+
 // ------------------------------------------- decode RESIDUAL GEMV, m <= 16
 // The out_proj of one decode step (a few tokens): 16 features per block, 8
 // waves taking 16-word chunks of K (c, c+8, ...).  In a chunk, lane (row
@@ -741,6 +832,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
 // Requires kw % 4 == 0, 16-byte aligned w, a and lda.  Blocks along y take
 // 16-token row groups (m <= 64 in one launch; the weight tile of a block is
 // then shared by the row groups through L2).
+// STAGE (the row groups of a batched step, m > 16): the 16 activation rows of
+// each chunk go through LDS as in gemv64s_kernel (4 x global_load_lds per
+// chunk, XOR-swizzled segments); segments past k are fetched from a clamped
+// in-bounds offset and meet zeroed weight words.
+template <bool STAGE>
 __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
     GemmArgs g = g0;
     if (gridDim.y > 1) {
@@ -753,6 +849,7 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
     }
     __shared__ int32_t red[8][64][4];
     __shared__ int32_t s_new[16][17];
+    __shared__ __align__(16) int8_t stage[STAGE ? 8 : 1][STAGE ? 2 : 1][STAGE ? 16 * 256 : 16];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), l16 = lane & 15, lq = lane >> 4;
     const int n0 = blockIdx.x * 16;
     const int nchunk = (g.kw + 15) / 16;
@@ -774,8 +871,28 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
             const int wl = min(w, g.kw - 4);  // kw % 4 == 0: all four words in or all past the row
             live[u] = w < g.kw;
             wv[u] = *reinterpret_cast<const v4i *>(wrow + wl);
+            if constexpr (STAGE) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xv[u][j] = *reinterpret_cast<const v4i *>(arow + 16 * (wl + j));
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 4 * r + (lane >> 4);
+                    const int seg = (lane & 15) ^ row;
+                    const int8_t *src = g.a + (int64_t)min(row, g.M - 1) * g.lda + min(256 * c + 16 * seg, g.K - 16);
+                    __builtin_amdgcn_global_load_lds((global_void_t *)src, (lds_void_t *)&stage[wave][u][r * 1024],
+                                                     16, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xv[u][j] = *reinterpret_cast<const v4i *>(arow + 16 * (wl + j));
+            }
+        }
+        if constexpr (STAGE) {
+            // the wave's own slabs: once its loads have landed it reads them
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    xv[u][j] = *reinterpret_cast<const v4i *>(&stage[wave][u][l16 * 256 + 16 * ((4 * lq + j) ^ l16)]);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -783,6 +900,7 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc = mfma_i8(unpack16(live[u] ? (uint32_t)wv[u][j] : 0u), xv[u][j], acc);
+        if constexpr (STAGE) __builtin_amdgcn_wave_barrier();
     }
     *reinterpret_cast<v4i *>(&red[wave][lane][0]) = acc;
     __syncthreads();
@@ -934,8 +1052,11 @@ hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
     if (KIND == MI_OUT_RESIDUAL && g.M <= 64 && g.kw % 4 == 0 && aligned(g.w, 16) && aligned(g.a, 16) &&
         g.lda % 16 == 0) {
         // 16-token row groups along y (weight tiles shared through L2)
-        hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((g.N + 15) / 16), (unsigned)((g.M + 15) / 16)),
-                           dim3(512), 0, st, g);
+        if (g.M > 16)
+            hipLaunchKernelGGL(resid_gemv16_kernel<true>, dim3((unsigned)((g.N + 15) / 16), (unsigned)((g.M + 15) / 16)),
+                               dim3(512), 0, st, g);
+        else
+            hipLaunchKernelGGL(resid_gemv16_kernel<false>, dim3((unsigned)((g.N + 15) / 16), 1u), dim3(512), 0, st, g);
         return hipGetLastError();
     }
     if (g.M > 16 && g.M <= 64 && g.kw % 16 == 0 && aligned(g.w, 16) && aligned(g.a, 16) && g.lda % 16 == 0) {
@@ -943,7 +1064,7 @@ hipError_t launch_gemv_kind(const GemmArgs &g, hipStream_t st) {
         // (many 16-word chunks per block) spreads over 8 or 16 waves
         const int nchunk = g.kw / 16;
         if ((g.N + 31) / 32 >= 128 && nchunk <= 8)
-            hipLaunchKernelGGL((gemv64_kernel<KIND, 2, 4>), dim3((unsigned)((g.N + 31) / 32)), dim3(256), 0, st, g);
+            hipLaunchKernelGGL((gemv64s_kernel<KIND, 2>), dim3((unsigned)((g.N + 31) / 32)), dim3(256), 0, st, g);
         else if (nchunk <= 8)
             hipLaunchKernelGGL((gemv64_kernel<KIND, 1, 4>), dim3((unsigned)((g.N + 15) / 16)), dim3(256), 0, st, g);
         else if (nchunk <= 16)
@@ -1027,8 +1148,12 @@ extern "C" mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const
                "%s: w_packed and stats_parts must be 16-byte aligned", fn);
     GemmArgs g = make_args(a, lda, w_packed, r, ldr, m, n, k, 0, res_mult, res_shift, nullptr, 0.0f, nullptr);
     g.stats_parts = stats_parts;
-    hipLaunchKernelGGL(resid_gemv16_kernel, dim3((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16)), dim3(512), 0,
-                       as_stream(stream), g);
+    if (m > 16)
+        hipLaunchKernelGGL(resid_gemv16_kernel<true>, dim3((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16)),
+                           dim3(512), 0, as_stream(stream), g);
+    else
+        hipLaunchKernelGGL(resid_gemv16_kernel<false>, dim3((unsigned)((n + 15) / 16), 1u), dim3(512), 0,
+                           as_stream(stream), g);
     return check_launch(fn);
 }
 

@@ -226,7 +226,8 @@ def test_embed_and_argmax(cuda, rng):
     assert torch.equal(ops.argmax(T(lg)).cpu(), torch.argmax(torch.from_numpy(lg), dim=1))
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 8192, 512), (40, 4096, 256), (17, 100, 256), (64, 300, 4096), (33, 4100, 256)])
+@pytest.mark.parametrize("M,N,K", [(64, 8192, 512), (40, 4096, 256), (17, 100, 256), (64, 300, 4096), (33, 4100, 256),
+                                   (64, 8192, 2048), (50, 4096, 2048), (20, 4096, 1536)])
 def test_batched_decode_gemv_kinds(cuda, M, N, K):
     """The batched decode GEMV (16 < m <= 64, K a multiple of 256; 16 or 32
     features per block): every epilogue kind, and the residual's row
