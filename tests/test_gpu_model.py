@@ -224,3 +224,31 @@ def test_native_decode_step_matches_oracle(cuda):
         got.append(H(cur))
         run.forward_logits(T(ids[:, :4]))  # unrelated eager work between replays
     assert np.array_equal(np.stack(got, 1), eager)
+
+
+@pytest.mark.parametrize("block", ["dyadic", "ssd"])
+def test_chunked_prefill_equals_one_prefill(cuda, block):
+    """Prefill continued from a carried state (the fused in_proj + conv reads
+    the previous conv state; chunks of 5, 2, 1 and 16 tokens, the short ones
+    shorter than the conv window) gives the logits and the conv and scan
+    states of one prefill over the whole prompt, and of the oracle."""
+    from mamba_int.model import IntegerMambaRunner
+    if block == "ssd":
+        from test_gpu_ssd import _ssd_params
+        p = _ssd_params()
+        V = 400
+    else:
+        p = _small()
+        V = 500
+    ids = np.random.default_rng(9).integers(0, V, size=(3, 24))
+    run = IntegerMambaRunner(p)
+    lg_all, st_all = run.prefill(T(ids))
+    st = None
+    t = 0
+    for n in (5, 2, 1, 16):
+        lg, st = run.prefill(T(ids[:, t:t + n]), st)
+        t += n
+    assert np.array_equal(H(lg), H(lg_all))
+    for a, b in zip(st.conv + st.h, st_all.conv + st_all.h):
+        assert np.array_equal(H(a), H(b))
+    assert np.array_equal(H(lg_all), O.OracleModel(p).prefill(ids)[0])
