@@ -90,7 +90,8 @@ def test_bitlinear_kinds(cuda, M, N, K):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 200, 192), (130, 36, 64), (257, 129, 320)])
+@pytest.mark.parametrize("M,N,K", [(200, 200, 192), (130, 36, 64), (257, 129, 320), (200, 200, 768), (130, 36, 704),
+                                   (257, 129, 1536), (70, 300, 1472)])
 @pytest.mark.parametrize("pad", [0, 4, 16])
 def test_gemm_tile_edges(cuda, M, N, K, pad):
     """Prefill GEMM edge tiles: a K tail of 64 past the last 128-deep stage, ragged
