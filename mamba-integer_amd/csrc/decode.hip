@@ -797,13 +797,12 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
 // channel owns states 4q..4q+3, as in dt_scan_step_kernel<0, 4>.
 // XP: the x_proj rows arrive as nblk <= kTokMaxParts int32 partial sums per
 // token (mi_xpart_dt_scan_step), summed and requantised while staging.
-// S24 (decay_shift 15): the state update in 24-bit multiplies.  With
-// h = hh * 2^15 + hl (0 <= hl < 2^15) and 0 <= nt <= 32000,
-// floor(h * nt / 2^15) = hh * nt + floor(hl * nt / 2^15), where |hh * nt| <
-// 2^31 and hl * nt < 2^32; B * xd fits 32 bits (|xd| <= 813), so the sum
-// saturates with one clamped add; y = C . h accumulates C * (h >> 15) and
-// C * (h & 0x7fff) in two int32 sums (each < 2^28 over a channel's 16
-// states).  Without S24 the same rules run in 64-bit arithmetic.
+// S24 (decay_shift 15): the state update in 24-bit multiplies (update16:
+// h read as H = h >> 16 and L = h & 0xffff, n2 = 2 * nt <= 64000, so
+// floor(h * nt / 2^15) = H * n2 + floor(L * n2 / 2^16) exactly); B * xd fits
+// 32 bits (|xd| <= 813), so the sum saturates with one clamped add; y = C . h
+// accumulates C * H and C * L in two int32 sums (each < 2^29 over a channel's
+// 16 states).  Without S24 the same rules run in 64-bit arithmetic.
 template <int TPB, bool XP, bool S24>
 __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_dt[TPB][kMaxR];
@@ -823,6 +822,10 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     for (int i = 0; i < kMaxR / 64; ++i)  // unconditional (kw >= 1): words past kw are never used
         wdt[i] = g.w_dt[(int64_t)dd * kw + min(q + 4 * i, kw - 1)];
     const int4 b4 = *reinterpret_cast<const int4 *>(g.base + (int64_t)dd * 16 + 4 * q);
+    // S24: 2 * base, the base first clamped to [-21, 32021] (with |dm| <= 20,
+    // clamp(base + dm, 0, 32000) is unchanged and the doubling cannot overflow)
+    const int b2[4] = {2 * clamp32(b4.x, -21, 32021), 2 * clamp32(b4.y, -21, 32021), 2 * clamp32(b4.z, -21, 32021),
+                       2 * clamp32(b4.w, -21, 32021)};
     v4i h4[TPB];   // streamed: the whole state is read and written once per step
     int xsv[TPB], zv[TPB];
 #pragma unroll
@@ -916,18 +919,16 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
             int yh = 0, yl = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int nt = min(max(__builtin_elementwise_add_sat(bv[i], dm), 0), 32000);
-                const int a = __mul24(hv[i] >> 15, nt) + (int)(__umul24((uint32_t)hv[i] & 0x7fffu, (uint32_t)nt) >> 15);
+                const int n2 = min(max(b2[i] + 2 * dm, 0), 64000);
                 const int bn = (bw << (24 - 8 * i)) >> 24, cn = (cw << (24 - 8 * i)) >> 24;
-                hn[i] = __builtin_elementwise_add_sat(a, __mul24(bn, xd));
-                yh += __mul24(cn, hn[i] >> 15);
-                yl += __mul24(cn, hn[i] & 0x7fff);
+                hn[i] = hv[i];
+                update16(hn[i], n2, __mul24(bn, xd), cn, yh, yl);
             }
             yh += __shfl_xor(yh, 1);
             yl += __shfl_xor(yl, 1);
             yh += __shfl_xor(yh, 2);
             yl += __shfl_xor(yl, 2);
-            y = (int64_t)yh * 32768 + yl;
+            y = (int64_t)yh * 65536 + yl;
         } else {
             const int64_t xd = rshr64((int64_t)xsv[t] * s_dtq[dm + 20], 10);
 #pragma unroll

@@ -43,6 +43,46 @@ __host__ __device__ __forceinline__ int32_t sat32_64(int64_t v) {
 __host__ __device__ __forceinline__ int32_t sat8(int32_t v) { return clamp32(v, -127, 127); }
 constexpr int32_t kResidualLimit = (1 << 23) - 1;
 
+// One step of the dyadic recurrence at decay shift 15, for one state:
+// h <- sat32(floor(h * n / 2^15) + u), and the state's two exact y partials.
+// h is read as two 16-bit fields, H = h >> 16 (signed) and L = h & 0xffff,
+// with n2 = 2n <= 2^16:  floor(h*n/2^15) = H*n2 + floor(L*n2/2^16), exactly
+// (H*n2 is an integer), with L*n2 < 2^32 and |H*n2| <= 2^31.  y = C . h is
+// kept as yhi = sum C*H and ylo = sum C*L (y = yhi * 2^16 + ylo; both stay in
+// int32 for up to 128 states of int8 C).  The fields are word halves, so the
+// 24-bit multiplies read them through SDWA operand selects: the update is
+// three multiplies, an add and the clamped add, and y two multiplies and
+// their share of the adds.
+__device__ __forceinline__ void update16(int32_t &h, int n2, int u, int cv, int &yhi, int &ylo) {
+    // The products are kept as plain multiplies (the empty asm hides them from
+    // mad formation): fused into a v_mad_i32_i24, H or L would need a shift or
+    // a mask of its own, where v_mul_*_u24/i24 read them as SDWA word selects.
+    int dh = __mul24(h >> 16, n2);
+    asm("" : "+v"(dh));
+    const uint32_t cl = __umul24((uint32_t)h & 0xffffu, (uint32_t)n2);
+    h = __builtin_elementwise_add_sat(dh + (int)(cl >> 16), u);
+    int ph = __mul24(cv, h >> 16), pl = __mul24(cv, h & 0xffff);
+    asm("" : "+v"(ph), "+v"(pl));
+    yhi += ph;
+    ylo += pl;
+}
+
+typedef short mi_short2 __attribute__((ext_vector_type(2)));
+
+// update16 for a coefficient held as cs = C * 2^16 (C in the high half, zero
+// low half): yhi accumulates H*C in one v_dot2c_i32_i16 on the state's two
+// halves (the low half meets the zero), and ylo reads C as cs's high word.
+__device__ __forceinline__ void update16_cs(int32_t &h, int n2, int u, int cs, int &yhi, int &ylo) {
+    int dh = __mul24(h >> 16, n2);
+    asm("" : "+v"(dh));
+    const uint32_t cl = __umul24((uint32_t)h & 0xffffu, (uint32_t)n2);
+    h = __builtin_elementwise_add_sat(dh + (int)(cl >> 16), u);
+    yhi = __builtin_amdgcn_sdot2(__builtin_bit_cast(mi_short2, h), __builtin_bit_cast(mi_short2, cs), yhi, false);
+    int pl = __mul24(cs >> 16, h & 0xffff);
+    asm("" : "+v"(pl));
+    ylo += pl;
+}
+
 // Exact floor(sqrt(v)) for v < 2^62 (host and device): a float estimate
 // refined by integer correction steps.
 __host__ __device__ __forceinline__ uint64_t isqrt64(uint64_t v) {

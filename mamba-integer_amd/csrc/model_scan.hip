@@ -3,8 +3,8 @@
 // recurrence, y = C.h, the gate by z and the requant of the out_proj input.
 //
 // Layout: a block of NT threads owns CH = NT/G channels of one sequence; G
-// adjacent lanes share a channel and keep S = N/G states each in VGPRs as
-// h = hh*2^15 + hl.  Per chunk of 64 steps the block stages xs, dm, z
+// adjacent lanes share a channel and keep S = N/G states each in VGPRs (read
+// as two 16-bit fields by the update, update16).  Per chunk of 64 steps the block stages xs, dm, z
 // (transposed to channel-major bytes) and B, C (widened to int32 so a state
 // reads its coefficients with one ds_read_b128 per four states) through LDS,
 // in two buffers where they fit: chunk c+1 is staged right after chunk c's
@@ -18,10 +18,10 @@
 // were written several instructions earlier, so no wait states).  The
 // epilogue (recombine, saturate, gate, requant) runs once per (step, channel)
 // at the end of the chunk, spread over all threads.
-// Per update: decay term 3 (v_mul_u32_u24, shift, v_mad_i32_i24), input 1,
-// saturating add 1, split 2, y partials 2, decay clamp 0-2 (skipped when every
-// base of the wave lies at least 20 inside [0, 32000], where base + dm cannot
-// leave the range).
+// Per update: decay 1 (2*base + 2*dm), decay term 3 (two SDWA multiplies, an
+// SDWA add), input 1, saturating add 1, y partials 2 multiplies and their
+// adds, decay clamp 0-1 (skipped when every base of the wave lies at least 20
+// inside [0, 32000], where base + dm cannot leave the range).
 #include <type_traits>
 
 #include "mi_common.hpp"
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     constexpr int NB = 2 * kStage + kMTC * CH * 9 + 297 * 4 <= 65536 ? 2 : 1;
     static_assert(NB * kStage + kMTC * CH * 9 + 297 * 4 <= 65536, "LDS budget");
 
-    __shared__ __align__(16) int8_t s_x[NB][2][CH][XP];    // dm, z (channel-major)
+    __shared__ __align__(16) int8_t s_x[NB][2][CH][XP];    // 2*dm, z (channel-major)
     __shared__ __align__(16) int16_t s_xd[NB][CH][XP];      // rshr(xs * dt(dm), 10), |xd| <= 813
     __shared__ __align__(16) int32_t s_b[NB][kMTC][N];
     __shared__ __align__(16) int32_t s_c[NB][kMTC][N];
@@ -114,16 +114,15 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     for (int i = tid; i < 41; i += NT) s_dt[i] = dt_q16(i - 20);
     for (int i = tid; i < 256; i += NT) s_gate[i] = gate_q15(i - 128);
 
-    int32_t base[S], hh[S], hl[S];
+    int32_t base2[S], h[S];  // 2 * base: the update takes n2 = 2n
     bool safe = true;
     {
         const int64_t sidx = ((int64_t)b * a.D + (active ? p : 0)) * N + g * S;
         for (int s = 0; s < S; ++s) {
-            const int32_t hv = (a.h_in && active) ? a.h_in[sidx + s] : 0;
-            hh[s] = hv >> 15;
-            hl[s] = hv & 0x7fff;
-            base[s] = active ? a.base[(int64_t)p * N + g * S + s] : 16000;
-            safe = safe && base[s] >= 20 && base[s] <= 32000 - 20;
+            h[s] = (a.h_in && active) ? a.h_in[sidx + s] : 0;
+            const int32_t bs = active ? a.base[(int64_t)p * N + g * S + s] : 16000;
+            base2[s] = 2 * bs;
+            safe = safe && bs >= 20 && bs <= 32000 - 20;
         }
     }
     // a wave-uniform choice: every lane of the wave can drop the decay clamp
@@ -168,7 +167,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int dmv = clamp32(sb(wd[e >> 2], e & 3), -20, 20);
-                s_x[bf][0][c16 * 16 + e][tt] = (int8_t)dmv;
+                s_x[bf][0][c16 * 16 + e][tt] = (int8_t)(2 * dmv);  // the decay takes 2n
                 s_x[bf][1][c16 * 16 + e][tt] = (int8_t)sb(wz[e >> 2], e & 3);
                 s_xd[bf][c16 * 16 + e][tt] = (int16_t)((sb(wx[e >> 2], e & 3) * s_dt[dmv + 20] + 512) >> 10);
             }
@@ -182,7 +181,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 s_b[bf][tt][c16 * 16 + e] = sb(wb[e >> 2], e & 3);
-                s_c[bf][tt][c16 * 16 + e] = sb(wc[e >> 2], e & 3);
+                s_c[bf][tt][c16 * 16 + e] = sb(wc[e >> 2], e & 3) * 65536;  // C * 2^16 (update16_cs)
             }
         }
     };
@@ -207,23 +206,16 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         }
     };
     // the recurrence of this lane's S states for one step: returns the exact
-    // int32 partials (sum C*hh, sum C*hl) of y over the lane's states
-    auto update = [&](int xd, int dmv, const int (&bv)[S], const int (&cv)[S], int &yhi, int &ylo,
+    // int32 partials (sum C*H, sum C*L) of y over the lane's states
+    auto update = [&](int xd, int dm2, const int (&bv)[S], const int (&cs)[S], int &yhi, int &ylo,
                       auto clamp_tag) {
         constexpr bool CLAMP = decltype(clamp_tag)::value;
         yhi = 0;
         ylo = 0;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const int nt = CLAMP ? clamp32(base[s] + dmv, 0, 32000) : base[s] + dmv;
-            const int u = __mul24(bv[s], xd);
-            const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt) >> 15);
-            const int d = __mul24(hh[s], nt) + c;
-            const int hn = __builtin_elementwise_add_sat(d, u);
-            hh[s] = hn >> 15;
-            hl[s] = hn & 0x7fff;
-            yhi += __mul24(cv[s], hh[s]);
-            ylo += __mul24(cv[s], hl[s]);
+            const int n2 = CLAMP ? clamp32(base2[s] + dm2, 0, 64000) : base2[s] + dm2;
+            update16_cs(h[s], n2, __mul24(bv[s], xd), cs[s], yhi, ylo);
         }
     };
 
@@ -273,9 +265,9 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
             for (int t = t4n; t < tn; ++t) {
                 int bv[S], cv[S];
                 load_bc(cur, t, bv, cv);
-                const int dmv = s_x[cur][0][ch][t];
+                const int dm2 = s_x[cur][0][ch][t];
                 int y[2];
-                update(s_xd[cur][ch][t], dmv, bv, cv, y[0], y[1], clamp_tag);
+                update(s_xd[cur][ch][t], dm2, bv, cv, y[0], y[1], clamp_tag);
                 msum_all<G>(y);
                 s_y[t][ch] = make_int2(y[0], y[1]);  // all G lanes hold the same sums: no branch
             }
@@ -285,12 +277,12 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         if constexpr (NB == 2)
             if (cidx + 1 < nchunks) stash(cur ^ 1);
         __syncthreads();
-        // epilogue of the chunk: y = sat32(yhi*2^15 + ylo), gate, requant
+        // epilogue of the chunk: y = sat32(yhi*2^16 + ylo), gate, requant
         for (int i = tid; i < kMTC * CH; i += NT) {
             const int tt = i / CH, cc = i % CH;
             if (tt < tn) {
                 const int2 yv = s_y[tt][cc];
-                const int32_t y32 = sat32_64(((int64_t)yv.x << 15) + yv.y);
+                const int32_t y32 = sat32_64(((int64_t)yv.x << 16) + yv.y);
                 const int zv = s_x[cur][1][cc][tt];
                 const int32_t gt = s_gate[zv + 128];
                 // floor(y32 * gt / 2^15) with 32-bit pieces: y32 = yh*2^15 + yl, 0 <= yl < 2^15
@@ -316,7 +308,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     }
     if (a.h_out && active) {
         const int64_t sidx = ((int64_t)b * a.D + p) * N + g * S;
-        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = (hh[s] << 15) + hl[s];
+        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = h[s];
     }
 }
 
@@ -347,7 +339,7 @@ hipError_t launch_model_n(int G, int NT, const MScanArgs &a, hipStream_t st) {
 // 536-586): per (sequence, head) a P x N state with one decay per step and
 // head, h = floor(h * n_t / 2^15) + Bq[n] * x[p], y = sum_n Cq[n] h, clamp,
 // gate, requant.  Same lane layout as model_scan_kernel (G lanes per channel,
-// S = N/G states each, split h = hh*2^15 + hl); a block's CH channels lie in
+// S = N/G states each, the update16 step); a block's CH channels lie in
 // one head.  Per chunk the block stages x and z (channel-major), the step
 // decays (table lookup of the head's dt column) and B, C: each 16-byte piece
 // of a token's B (or C) row sums its squares, the token's N/16 pieces (lanes
@@ -386,7 +378,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
 
     __shared__ __align__(16) int8_t s_x[2][CH][XP];        // xs, z (channel-major)
     __shared__ __align__(16) int32_t s_b[kMTC][N];
-    __shared__ __align__(16) int32_t s_c[kMTC][N];
+    __shared__ __align__(16) int32_t s_c[kMTC][N];          // C * 2^16 (update16_cs)
     __shared__ __align__(16) int2 s_y[kMTC][CH];
     __shared__ __align__(16) int8_t s_o[kMTC][CH];
     __shared__ __align__(16) int32_t s_n[kMTC];
@@ -401,17 +393,14 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
     const int b = blockIdx.y;
     const int p = p0 + ch;
 
-    for (int i = tid; i < 255; i += kMThreads) s_tab[i] = a.tab[(int64_t)head * 255 + i];
+    // doubled: the update takes n2 = 2n (table entries lie in [0, 2^15])
+    for (int i = tid; i < 255; i += kMThreads) s_tab[i] = 2 * a.tab[(int64_t)head * 255 + i];
     for (int i = tid; i < 256; i += kMThreads) s_gate[i] = gate_q15(i - 128);
 
-    int32_t hh[S], hl[S];
+    int32_t h[S];
     {
         const int64_t sidx = ((int64_t)b * a.D + p) * N + g * S;
-        for (int s = 0; s < S; ++s) {
-            const int32_t hv = a.h_in ? a.h_in[sidx + s] : 0;
-            hh[s] = hv >> 15;
-            hl[s] = hv & 0x7fff;
-        }
+        for (int s = 0; s < S; ++s) h[s] = a.h_in ? a.h_in[sidx + s] : 0;
     }
 
     // ext_vector_type registers (a union-typed uint4 array touched through
@@ -488,14 +477,14 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     s_b[tt][c16 * 16 + e] = clamp32(rshr32(sb(wb[e >> 2], e & 3) * ib, 15), -127, 127);
-                    s_c[tt][c16 * 16 + e] = clamp32(rshr32(sb(wc[e >> 2], e & 3) * ic, 15), -127, 127);
+                    s_c[tt][c16 * 16 + e] = clamp32(rshr32(sb(wc[e >> 2], e & 3) * ic, 15), -127, 127) * 65536;
                 }
             }
         }
         if (tid < kMTC) s_n[tid] = s_tab[clamp32(dtv, -127, 127) + 127];
     };
 
-    auto step = [&](int t, int xv, int nt) {
+    auto step = [&](int t, int xv, int n2) {
         int bv[S], cv[S];
         if constexpr (S >= 4) {
             for (int q = 0; q < S / 4; ++q) {
@@ -511,16 +500,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
             }
         }
         int yhi = 0, ylo = 0;
-        for (int s = 0; s < S; ++s) {
-            const int u = __mul24(bv[s], xv);
-            const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt) >> 15);
-            const int d = __mul24(hh[s], nt) + c;
-            const int hn = __builtin_elementwise_add_sat(d, u);
-            hh[s] = hn >> 15;
-            hl[s] = hn & 0x7fff;
-            yhi += __mul24(cv[s], hh[s]);
-            ylo += __mul24(cv[s], hl[s]);
-        }
+        for (int s = 0; s < S; ++s) update16_cs(h[s], n2, __mul24(bv[s], xv), cv[s], yhi, ylo);
         yhi = msum<G>(yhi);
         ylo = msum<G>(ylo);
         s_y[t][ch] = make_int2(yhi, ylo);
@@ -552,7 +532,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
             const int tt = i / CH, cc = i % CH;
             if (tt < tn) {
                 const int2 yv = s_y[tt][cc];
-                const int32_t y32 = clamp32(sat32_64(((int64_t)yv.x << 15) + yv.y), -ylim, ylim);
+                const int32_t y32 = clamp32(sat32_64(((int64_t)yv.x << 16) + yv.y), -ylim, ylim);
                 const int32_t gt = s_gate[s_x[1][cc][tt] + 128];
                 const int32_t yh = y32 >> 15, yl = y32 & 0x7fff;
                 const int32_t yg = yh * gt + (int32_t)(((uint32_t)yl * (uint32_t)gt) >> 15);
@@ -569,7 +549,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
     }
     if (a.h_out) {
         const int64_t sidx = ((int64_t)b * a.D + p) * N + g * S;
-        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = (hh[s] << 15) + hl[s];
+        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = h[s];
     }
 }
 
@@ -628,18 +608,13 @@ __global__ __launch_bounds__(kMThreads) void ssd_step_kernel(SScanArgs a) {
         }
     }
     __syncthreads();
-    const int nt = s_nt;
+    const int n2 = 2 * s_nt;  // table entries lie in [0, 2^15]
     int yhi = 0, ylo = 0;
     int32_t hn[S];
 #pragma unroll
     for (int q = 0; q < S; ++q) {
-        const int hh = hv[q] >> 15, hl = hv[q] & 0x7fff;
-        const int u = __mul24(s_b[g * S + q], xv);
-        const int c = (int)(__umul24((uint32_t)hl, (uint32_t)nt) >> 15);
-        const int d = __mul24(hh, nt) + c;
-        hn[q] = __builtin_elementwise_add_sat(d, u);
-        yhi += __mul24(s_c[g * S + q], hn[q] >> 15);
-        ylo += __mul24(s_c[g * S + q], hn[q] & 0x7fff);
+        hn[q] = hv[q];
+        update16(hn[q], n2, __mul24(s_b[g * S + q], xv), s_c[g * S + q], yhi, ylo);
     }
     if (a.h_out) {
         if constexpr (S % 4 == 0) {
@@ -656,7 +631,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_step_kernel(SScanArgs a) {
     ylo = msum<G>(ylo);
     if (g == 0) {
         const int32_t ylim = 100 << 18;
-        const int32_t y32 = clamp32(sat32_64(((int64_t)yhi << 15) + ylo), -ylim, ylim);
+        const int32_t y32 = clamp32(sat32_64(((int64_t)yhi << 16) + ylo), -ylim, ylim);
         const int32_t gt = gate_q15(zv);
         const int32_t yh = y32 >> 15, yl = y32 & 0x7fff;
         const int32_t yg = yh * gt + (int32_t)(((uint32_t)yl * (uint32_t)gt) >> 15);

@@ -6,18 +6,19 @@
 // sequential inside every lane.  The scan is integer-VALU bound, so the
 // kernels are built around a short per-update instruction sequence:
 //
-//   state kept split as h = hh * 2^k + hl with hl in [0, 2^k):
-//     c   = (hl * n) >> k          v_mul_u32_u24 + v_lshrrev      (hl*n < 2^32)
-//     h'  = hh * n + c             v_mad_i32_i24                  (fits int32)
-//     h'' = sat32(h' + u)          v_add_i32 clamp
-//     hh, hl = split(h'')          v_ashrrev + v_and
-//     yhi += C*hh; ylo += C*hl     2 x v_mad_i32_i24               (exact int32 partials)
+//   the state h is read as two 16-bit fields, H = h >> 16 (signed) and
+//   L = h & 0xffff, with n2 = 2n = n * 2^(16-k) <= 2^16:
+//     d   = H * n2 + ((L * n2) >> 16)    v_mul_i32_i24, v_mul_u32_u24, v_add_u32
+//     h'  = sat32(d + u)                 v_add_i32 clamp
+//     yhi += C*H'; ylo += C*L'           2 x v_mul_i32_i24 + adds  (exact int32 partials)
 //
-// floor(h*n/2^k) = hh*n + floor(hl*n/2^k) exactly because hh*n is an integer,
-// and y = 2^k * sum(C*hh) + sum(C*hl) is recombined in int64 once per step.
-// This holds for 0 <= n <= 2^k with k = 15 and N <= 128 (|hh| <= 2^16, so
-// |sum C*hh| <= 128*128*2^16 = 2^30; hl*n < 2^31); other shifts and shapes
-// take the plain int64 kernels at the end.
+// floor(h*n/2^15) = H*n2 + floor(L*n2/2^16) exactly because H*n2 is an
+// integer (h*n/2^15 = h*n2/2^16), and y = 2^16 * sum(C*H) + sum(C*L) is
+// recombined in int64 once per step.  The fields are word halves, so every
+// read of H and L is an SDWA operand select: no shift or mask per state.
+// This holds for 0 <= n <= 2^k with k = 15 and N <= 128 (L*n2 < 2^32,
+// |H*n2| <= 2^31, |sum C*H| <= 128*128*2^15 = 2^29, |sum C*L| < 2^31); other
+// shifts and shapes take the plain int64 kernels at the end.
 //
 // Layout: a block owns CH = 256/G channels of one (batch, head); G adjacent
 // lanes share a channel and hold S = N/G states each; their partial y sums
@@ -111,8 +112,6 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     const int b = blockIdx.z;
     const int p = p0 + ch;
     const bool active = p < a.P;
-    const int k = a.k;
-    const int32_t kmask = (1 << k) - 1;
 
     if constexpr (MODEL) {
         for (int i = tid; i < 41; i += kThreads) s_dt[i] = dt_q16(i - 20);
@@ -120,18 +119,16 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     }
 
     // ---- per-thread constants and state
-    int32_t ndec[S];
-    int32_t hh[S], hl[S];
+    int32_t ndec[S];  // 2n (the model mode's base before its per-step clamp)
+    int32_t h[S];
     {
         const int64_t sidx = ((((int64_t)b * a.H + hd) * a.P + (active ? p : 0)) * N) + g * S;
         for (int s = 0; s < S; ++s) {
-            int32_t hv = (a.h_in && active) ? a.h_in[sidx + s] : 0;
-            hh[s] = hv >> k;
-            hl[s] = hv & kmask;
+            h[s] = (a.h_in && active) ? a.h_in[sidx + s] : 0;
             if constexpr (MODE == kModeChannel || MODE == kModeModel)
-                ndec[s] = active ? a.decay[(int64_t)p * N + g * S + s] : 0;
+                ndec[s] = 2 * (active ? a.decay[(int64_t)p * N + g * S + s] : 0);
             else
-                ndec[s] = a.decay[hd];
+                ndec[s] = 2 * a.decay[hd];
         }
     }
 
@@ -198,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             int32_t nt[S];
             if constexpr (MODEL) {
                 xv = (xv * s_dt[dmv + 20] + 512) >> 10;           // rshr(xs * dt, 10)
-                for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + dmv, 0, 32000);
+                for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + 2 * dmv, 0, 64000);
             } else {
                 for (int s = 0; s < S; ++s) nt[s] = ndec[s];
             }
@@ -220,18 +217,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             yhi = 0;
             ylo = 0;
 #pragma unroll
-            for (int s = 0; s < S; ++s) {
-                const int bv = sbyte(bw[s >> 2], s & 3);
-                const int cv = sbyte(cw[s >> 2], s & 3);
-                const int u = __mul24(bv, xv);
-                const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt[s]) >> k);
-                const int d = __mul24(hh[s], nt[s]) + c;
-                const int hn = __builtin_elementwise_add_sat(d, u);
-                hh[s] = hn >> k;
-                hl[s] = hn & kmask;
-                yhi += __mul24(cv, hh[s]);
-                ylo += __mul24(cv, hl[s]);
-            }
+            for (int s = 0; s < S; ++s)
+                update16(h[s], nt[s], __mul24(sbyte(bw[s >> 2], s & 3), xv), sbyte(cw[s >> 2], s & 3), yhi, ylo);
         };
         for (int t4 = 0; t4 < tn; t4 += 4) {
             const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_xa[0][ch][t4]);
@@ -276,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                 if constexpr (MODEL) {
                     const int dmv = clamp32(sbyte(dmw, tt), -20, 20);
                     xv = (xv * s_dt[dmv + 20] + 512) >> 10;           // rshr(xs * dt, 10)
-                    for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + dmv, 0, 32000);
+                    for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + 2 * dmv, 0, 64000);
                 } else {
                     for (int s = 0; s < S; ++s) nt[s] = ndec[s];
                 }
@@ -296,21 +283,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                     cw[0] = cc;
                 }
                 int yhi = 0, ylo = 0;
-                for (int s = 0; s < S; ++s) {
-                    const int bv = sbyte(bw[s >> 2], s & 3);
-                    const int cv = sbyte(cw[s >> 2], s & 3);
-                    const int u = __mul24(bv, xv);
-                    const int c = (int)(__umul24((uint32_t)hl[s], (uint32_t)nt[s]) >> k);
-                    const int d = __mul24(hh[s], nt[s]) + c;
-                    const int hn = __builtin_elementwise_add_sat(d, u);
-                    hh[s] = hn >> k;
-                    hl[s] = hn & kmask;
-                    yhi += __mul24(cv, hh[s]);
-                    ylo += __mul24(cv, hl[s]);
-                }
+                for (int s = 0; s < S; ++s)
+                    update16(h[s], nt[s], __mul24(sbyte(bw[s >> 2], s & 3), xv), sbyte(cw[s >> 2], s & 3), yhi, ylo);
                 yhi = group_sum<G>(yhi);
                 ylo = group_sum<G>(ylo);
-                const int64_t y64 = ((int64_t)yhi << k) + ylo;
+                const int64_t y64 = ((int64_t)yhi << 16) + ylo;
                 const int32_t y32 = sat32_64(y64);
                 if (g == 0) {
                     if constexpr (MODEL) {
@@ -333,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                 const int tt = i / CH, cc = i % CH;
                 if (tt < tn) {
                     const int2 yv = s_y[tt][cc];
-                    const int32_t y32 = sat32_64(((int64_t)yv.x << k) + yv.y);
+                    const int32_t y32 = sat32_64(((int64_t)yv.x << 16) + yv.y);
                     if constexpr (MODEL) {
                         const int zv = s_xa[2][cc][tt];
                         const int64_t yg = ((int64_t)y32 * s_gate[zv + 128]) >> 15;
@@ -369,13 +346,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                 const int cc = (tdone - 1) / a.cs;
                 int32_t *dst = a.chunk_states +
                                ((((int64_t)b * a.nchunks_out + cc) * a.H + hd) * a.P + p) * N + g * S;
-                for (int s = 0; s < S; ++s) dst[s] = (hh[s] << k) + hl[s];
+                for (int s = 0; s < S; ++s) dst[s] = h[s];
             }
         }
     }
     if (a.h_out && active) {
         const int64_t sidx = ((((int64_t)b * a.H + hd) * a.P + p) * N) + g * S;
-        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = (hh[s] << k) + hl[s];
+        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = h[s];
     }
 }
 
@@ -489,9 +466,7 @@ hipError_t launch_scan(const ScanArgs &a, int N, bool fast, hipStream_t st) {
 bool fast_shape(int N, int P, int k, int mode) {
     if (N != 16 && N != 32 && N != 64 && !(N == 128 && mode != kModeModel)) return false;
     if (P % 16 != 0) return false;
-    // k = 15 only: hl*n < 2^15 * (2^15 + 1) < 2^31, so the product's sign bit is
-    // clear (the compiler lowers the unsigned shift of the 24-bit product to an
-    // arithmetic shift, which is exact only then), and sum C*hh stays in int32.
+    // k = 15 only: n2 = 2n <= 2^16 keeps L*n2 below 2^32 and H*n2 in int32.
     return k == 15;
 }
 
