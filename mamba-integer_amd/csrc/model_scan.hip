@@ -328,6 +328,7 @@ template <int N>
 hipError_t launch_model_n(int G, int NT, const MScanArgs &a, hipStream_t st) {
 #define MI_MCASE(GG, TT) \
     if (G == GG && NT == TT) return launch_model_ngt<N, GG, TT>(a, st);
+    MI_MCASE(4, 256)
     MI_MCASE(8, 256)
     MI_MCASE(16, 256)
 #undef MI_MCASE
@@ -693,9 +694,13 @@ hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z
     a.B = B; a.L = L; a.D = D; a.s_y = s_y;
     // lanes per channel and block size, measured at d_inner 1536 x batch 8 x
     // L2048, N16 (ms per launch): G8/256 threads 0.333, G8/128 0.337, G4/64
-    // 0.373, G4/256 0.369, G16/256 0.356, G4/128 0.531
+    // 0.373, G4/256 0.369, G16/256 0.356, G4/128 0.531.  G4 (4 states a lane,
+    // two DPP stages instead of three) wins once it still gives every SIMD
+    // three waves, B * d_inner / 16 >= 3072 (L256, ms, G8 vs G4): B32 x 1536
+    // 0.118 vs 0.113, B64 x 1536 0.219 vs 0.197, B32 x 4096 0.287 vs 0.262;
+    // B16 x 1536 0.068 vs 0.074
     switch (N) {
-        case 16: return launch_model_n<16>(8, 256, a, st);
+        case 16: return launch_model_n<16>((int64_t)B * D >= 3072 * 16 ? 4 : 8, 256, a, st);
         case 32: return launch_model_n<32>(8, 256, a, st);
         case 64: return launch_model_n<64>(16, 256, a, st);
     }

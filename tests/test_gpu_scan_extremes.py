@@ -92,14 +92,16 @@ def test_ssd_chunked_scan_state_extremes(cuda):
     assert np.array_equal(H(hout), h_ref)
 
 
-@pytest.mark.parametrize("N", [16, 32])
-def test_block_scan_state_extremes(cuda, N):
+@pytest.mark.parametrize("N,B,L,D", [(16, 2, 140, 256), (32, 2, 140, 256), (16, 32, 70, 1536)])
+def test_block_scan_state_extremes(cuda, N, B, L, D):
     """mi_block_scan (the fused prefill scan) from full-range states, bases at
     the clamp edges 0 and 32000 (and within 20 of them, so some waves take the
-    clamped decay and some the unclamped one), dm over its whole range."""
+    clamped decay and some the unclamped one), dm over its whole range.  The
+    32 x 1536 case takes the 4-lanes-per-channel layout (batch x d_inner >=
+    49152), the others 8 lanes."""
     from mamba_int import ops
-    rng = np.random.default_rng(200 + N)
-    B, L, D, R = 2, 140, 256, 16
+    rng = np.random.default_rng(200 + N + B)
+    R = 16
     W = (R + 2 * N + 15) // 16 * 16
     xs = i8(rng, B, L, D, lo=-128)
     dm = i8(rng, B, L, D, lo=-128)
