@@ -69,14 +69,25 @@ __device__ __forceinline__ void update16(int32_t &h, int n2, int u, int cv, int 
 
 typedef short mi_short2 __attribute__((ext_vector_type(2)));
 
+// sat32(b * x + d) for b, x in 24-bit signed range: v_mad_i32_i24 with the
+// clamp bit saturates the full-precision sum (checked on the hardware against
+// a 64-bit saturating reference, both directions)
+__device__ __forceinline__ int mad24_sat(int b, int x, int d) {
+    int r;
+    asm("v_mad_i32_i24 %0, %1, %2, %3 clamp" : "=v"(r) : "v"(b), "v"(x), "v"(d));
+    return r;
+}
+
 // update16 for a coefficient held as cs = C * 2^16 (C in the high half, zero
-// low half): yhi accumulates H*C in one v_dot2c_i32_i16 on the state's two
-// halves (the low half meets the zero), and ylo reads C as cs's high word.
-__device__ __forceinline__ void update16_cs(int32_t &h, int n2, int u, int cs, int &yhi, int &ylo) {
+// low half) and the input term as the pair (b, x), u = b * x: the input and
+// the saturating add are one clamped v_mad_i32_i24; yhi accumulates H*C in one
+// v_dot2c_i32_i16 on the state's two halves (the low half meets the zero), and
+// ylo reads C as cs's high word.
+__device__ __forceinline__ void update16_cs(int32_t &h, int n2, int b, int x, int cs, int &yhi, int &ylo) {
     int dh = __mul24(h >> 16, n2);
     asm("" : "+v"(dh));
     const uint32_t cl = __umul24((uint32_t)h & 0xffffu, (uint32_t)n2);
-    h = __builtin_elementwise_add_sat(dh + (int)(cl >> 16), u);
+    h = mad24_sat(b, x, dh + (int)(cl >> 16));
     yhi = __builtin_amdgcn_sdot2(__builtin_bit_cast(mi_short2, h), __builtin_bit_cast(mi_short2, cs), yhi, false);
     int pl = __mul24(cs >> 16, h & 0xffff);
     asm("" : "+v"(pl));

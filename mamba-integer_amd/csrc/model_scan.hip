@@ -19,9 +19,10 @@
 // epilogue (recombine, saturate, gate, requant) runs once per (step, channel)
 // at the end of the chunk, spread over all threads.
 // Per update: decay 1 (2*base + 2*dm), decay term 3 (two SDWA multiplies, an
-// SDWA add), input 1, saturating add 1, y partials 2 multiplies and their
-// adds, decay clamp 0-1 (skipped when every base of the wave lies at least 20
-// inside [0, 32000], where base + dm cannot leave the range).
+// SDWA add), input and saturating add 1 (a clamped v_mad_i32_i24), y partials
+// 2 (a v_dot2c and a multiply) and their adds, decay clamp 0-1 (skipped when
+// every base of the wave lies at least 20 inside [0, 32000], where base + dm
+// cannot leave the range).
 #include <type_traits>
 
 #include "mi_common.hpp"
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int n2 = CLAMP ? clamp32(base2[s] + dm2, 0, 64000) : base2[s] + dm2;
-            update16_cs(h[s], n2, __mul24(bv[s], xd), cs[s], yhi, ylo);
+            update16_cs(h[s], n2, bv[s], xd, cs[s], yhi, ylo);
         }
     };
 
@@ -501,7 +502,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
             }
         }
         int yhi = 0, ylo = 0;
-        for (int s = 0; s < S; ++s) update16_cs(h[s], n2, __mul24(bv[s], xv), cv[s], yhi, ylo);
+        for (int s = 0; s < S; ++s) update16_cs(h[s], n2, bv[s], xv, cv[s], yhi, ylo);
         yhi = msum<G>(yhi);
         ylo = msum<G>(ylo);
         s_y[t][ch] = make_int2(yhi, ylo);
