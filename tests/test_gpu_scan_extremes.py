@@ -120,8 +120,9 @@ def test_block_scan_state_extremes(cuda, N, B, L, D):
 @pytest.mark.parametrize("L", [1, 90])
 def test_ssd_block_scan_state_extremes(cuda, L):
     """mi_ssd_block_scan from full-range states with decay-table entries 0 and
-    2^15 among random ones: the chunked kernel (L 90) and the one-step kernel
-    (L 1)."""
+    2^15 among random ones, and one head driven into both saturation directions
+    (the clamped multiply-add of the input term): the chunked kernel (L 90) and
+    the one-step kernel (L 1)."""
     from mamba_int import ops
     rng = np.random.default_rng(300 + L)
     B, Hh, P, N = 2, 3, 32, 64
@@ -134,7 +135,14 @@ def test_ssd_block_scan_state_extremes(cuda, L):
     tab[:, ::4] = 32768
     tab[:, 1::4] = 0
     h0 = _full_range_states(rng, (B, D, N))
+    # head 0 keeps its state (decay 2^15 at every dt) and takes a positive unit
+    # B: channel 0 (x = 127) saturates up, channel 1 (x = -128) down
+    tab[0] = 32768
+    xp[:, :, :N] = 127
+    xs[:, :, 0], xs[:, :, 1] = 127, -128
+    h0[:, 0], h0[:, 1] = I32_MAX - 5, I32_MIN + 5
     ref_y, ref_h = O.ssd_v2_scan(xs, xp, xz, D, tab, 14, Hh, N, h_state=h0)
+    assert (ref_h[:, 0] == I32_MAX).all() and (ref_h[:, 1] == I32_MIN).all()
     h = T(h0)
     y = ops.ssd_block_scan(T(xs), T(xp), T(xz), D, T(tab), Hh, N, 14, h_in=h, h_out=h)
     assert np.array_equal(H(y), ref_y)
