@@ -78,6 +78,20 @@ __device__ __forceinline__ int mad24_sat(int b, int x, int d) {
     return r;
 }
 
+// update16 with the input term as the pair (b, x), u = b * x: the input and
+// the saturating add are one clamped v_mad_i32_i24
+__device__ __forceinline__ void update16_b(int32_t &h, int n2, int b, int x, int cv, int &yhi, int &ylo) {
+    int dh = __mul24(h >> 16, n2);
+    asm("" : "+v"(dh));
+    const uint32_t cl = __umul24((uint32_t)h & 0xffffu, (uint32_t)n2);
+    h = mad24_sat(b, x, dh + (int)(cl >> 16));
+    // (no barrier on the y products here: behind the clamped multiply-add the
+    // compiler keeps them as SDWA multiplies by itself, and an asm statement
+    // costs an s_nop after it)
+    yhi += __mul24(cv, h >> 16);
+    ylo += __mul24(cv, h & 0xffff);
+}
+
 // update16 for a coefficient held as cs = C * 2^16 (C in the high half, zero
 // low half) and the input term as the pair (b, x), u = b * x: the input and
 // the saturating add are one clamped v_mad_i32_i24; yhi accumulates H*C in one

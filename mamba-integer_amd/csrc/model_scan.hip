@@ -616,7 +616,7 @@ __global__ __launch_bounds__(kMThreads) void ssd_step_kernel(SScanArgs a) {
 #pragma unroll
     for (int q = 0; q < S; ++q) {
         hn[q] = hv[q];
-        update16(hn[q], n2, __mul24(s_b[g * S + q], xv), s_c[g * S + q], yhi, ylo);
+        update16_b(hn[q], n2, s_b[g * S + q], xv, s_c[g * S + q], yhi, ylo);
     }
     if (a.h_out) {
         if constexpr (S % 4 == 0) {

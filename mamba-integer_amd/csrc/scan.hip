@@ -9,7 +9,8 @@
 //   the state h is read as two 16-bit fields, H = h >> 16 (signed) and
 //   L = h & 0xffff, with n2 = 2n = n * 2^(16-k) <= 2^16:
 //     d   = H * n2 + ((L * n2) >> 16)    v_mul_i32_i24, v_mul_u32_u24, v_add_u32
-//     h'  = sat32(d + u)                 v_add_i32 clamp
+//     h'  = sat32(d + B * x)             v_mad_i32_i24 clamp (S >= 4; else
+//                                        an SDWA multiply and v_add_i32 clamp)
 //     yhi += C*H'; ylo += C*L'           2 x v_mul_i32_i24 + adds  (exact int32 partials)
 //
 // floor(h*n/2^15) = H*n2 + floor(L*n2/2^16) exactly because H*n2 is an
@@ -23,9 +24,12 @@
 // Layout: a block owns CH = 256/G channels of one (batch, head); G adjacent
 // lanes share a channel and hold S = N/G states each; their partial y sums
 // are combined with DPP adds.  Inputs of TC time steps are staged through LDS
-// (prefetched into registers one chunk ahead), x-like bytes transposed to
-// channel-major so one ds_read_b32 serves 4 steps; outputs are staged in LDS
-// and written with 16-byte stores.
+// (prefetched into registers one chunk ahead), x bytes transposed to
+// channel-major so one ds_read_b32 serves 4 steps, B widened to int32 for the
+// clamped multiply-add where a lane holds four or more states; outputs are
+// staged in LDS and written with 16-byte stores.
+#include <type_traits>
+
 #include "mi_common.hpp"
 
 namespace mi {
@@ -78,26 +82,27 @@ __device__ __forceinline__ uint4 load16(const int8_t *p, bool ok) {
 
 template <int N, int G, int MODE>
 __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
+    static_assert(MODE != kModeModel, "the fused model scan has its own kernel (model_scan.hip)");
     constexpr int S = N / G;
     constexpr int CH = kThreads / G;
-    constexpr int XP = kTC + 4;                 // padded row of the transposed x tiles
+    constexpr int XP = kTC + 4;                 // padded row of the transposed x tile
     constexpr int X16 = CH / 16;                // 16-byte pieces per time row of x
     constexpr int XPIECES = kTC * X16;          // per chunk
     constexpr int XPER = (XPIECES + kThreads - 1) / kThreads;
     constexpr int BC16 = N / 16;
     constexpr int BCPIECES = kTC * BC16;
     constexpr int BCPER = (BCPIECES + kThreads - 1) / kThreads;
-    constexpr bool MODEL = MODE == kModeModel;
-    constexpr int NXA = MODEL ? 3 : 1;          // staged x-like arrays: x | xs, dm, z
 
-    __shared__ __align__(16) int8_t s_xa[NXA][CH][XP];
-    __shared__ __align__(16) int8_t s_b[kTC][N];
+    __shared__ __align__(16) int8_t s_x[CH][XP];
+    // WIDEB: B widened to int32, so the input term B * x and the saturating
+    // add are one clamped v_mad_i32_i24 (which takes no SDWA byte select).
+    // Lanes of one or two states keep B as bytes: their latency-bound chain
+    // measured slower with the wider staging (config 1: 22.0 -> 25.1 us)
+    constexpr bool WIDEB = S >= 4;
+    __shared__ __align__(16) std::conditional_t<WIDEB, int32_t, int8_t> s_b[kTC][N];
     __shared__ __align__(16) int8_t s_c[kTC][N];
-    __shared__ __align__(16) int8_t s_o8[MODEL ? kTC : 1][MODEL ? CH : 16];
-    constexpr bool STAGE_Y = !MODEL && CH <= 64;  // int32 y staged in LDS (16 KB at most)
+    constexpr bool STAGE_Y = CH <= 64;  // int32 y staged in LDS (16 KB at most)
     __shared__ __align__(16) int32_t s_o32[STAGE_Y ? kTC : 1][STAGE_Y ? CH : 4];
-    __shared__ int32_t s_dt[MODEL ? 41 : 1];
-    __shared__ int32_t s_gate[MODEL ? 256 : 1];
     // blocks of <= 32 channels (G >= 8) reduce the y partials of four steps
     // together and park the exact (yhi, ylo) pairs here; the chunk epilogue
     // recombines and saturates once per (step, channel)
@@ -113,27 +118,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     const int p = p0 + ch;
     const bool active = p < a.P;
 
-    if constexpr (MODEL) {
-        for (int i = tid; i < 41; i += kThreads) s_dt[i] = dt_q16(i - 20);
-        for (int i = tid; i < 256; i += kThreads) s_gate[i] = gate_q15(i - 128);
-    }
-
     // ---- per-thread constants and state
-    int32_t ndec[S];  // 2n (the model mode's base before its per-step clamp)
+    int32_t n2[S];  // 2n: the update16 form takes the doubled decay
     int32_t h[S];
     {
         const int64_t sidx = ((((int64_t)b * a.H + hd) * a.P + (active ? p : 0)) * N) + g * S;
         for (int s = 0; s < S; ++s) {
             h[s] = (a.h_in && active) ? a.h_in[sidx + s] : 0;
-            if constexpr (MODE == kModeChannel || MODE == kModeModel)
-                ndec[s] = 2 * (active ? a.decay[(int64_t)p * N + g * S + s] : 0);
+            if constexpr (MODE == kModeChannel)
+                n2[s] = 2 * (active ? a.decay[(int64_t)p * N + g * S + s] : 0);
             else
-                ndec[s] = 2 * a.decay[hd];
+                n2[s] = 2 * a.decay[hd];
         }
     }
 
     // ---- staging registers
-    uint4 rx[NXA][XPER];
+    uint4 rx[XPER];
     uint4 rb[BCPER], rc[BCPER];
     const int64_t row0 = (int64_t)b * a.L;  // first (b, t=0) row index
 
@@ -142,15 +142,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             const int i = tid + j * kThreads;
             const int tt = i / X16, c16 = i % X16;
             const bool ok = i < XPIECES && t0 + tt < a.L && p0 + c16 * 16 < a.P;
-            const int64_t rr = row0 + t0 + tt;
-            if constexpr (MODEL) {
-                const int64_t off = rr * a.x_row + p0 + c16 * 16;
-                rx[0][j] = load16(a.x + off, ok);
-                rx[1][j] = load16(a.dm + off, ok);
-                rx[2][j] = load16(a.z + rr * a.z_row + p0 + c16 * 16, ok);
-            } else {
-                rx[0][j] = load16(a.x + rr * a.x_row + (int64_t)hd * a.P + p0 + c16 * 16, ok);
-            }
+            rx[j] = load16(a.x + (row0 + t0 + tt) * a.x_row + (int64_t)hd * a.P + p0 + c16 * 16, ok);
         }
         for (int j = 0; j < BCPER; ++j) {
             const int i = tid + j * kThreads;
@@ -166,17 +158,50 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             const int i = tid + j * kThreads;
             if (i >= XPIECES) break;
             const int tt = i / X16, c16 = i % X16;
-            for (int q = 0; q < NXA; ++q) {
-                const uint32_t w[4] = {rx[q][j].x, rx[q][j].y, rx[q][j].z, rx[q][j].w};
-                for (int e = 0; e < 16; ++e) s_xa[q][c16 * 16 + e][tt] = (int8_t)(w[e >> 2] >> (8 * (e & 3)));
-            }
+            const uint32_t w[4] = {rx[j].x, rx[j].y, rx[j].z, rx[j].w};
+            for (int e = 0; e < 16; ++e) s_x[c16 * 16 + e][tt] = (int8_t)(w[e >> 2] >> (8 * (e & 3)));
         }
         for (int j = 0; j < BCPER; ++j) {
             const int i = tid + j * kThreads;
             if (i >= BCPIECES) break;
             const int tt = i / BC16, c16 = i % BC16;
-            *reinterpret_cast<uint4 *>(&s_b[tt][c16 * 16]) = rb[j];
+            if constexpr (WIDEB) {
+                const uint32_t w[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<int4 *>(&s_b[tt][c16 * 16 + 4 * q]) =
+                        make_int4(sbyte(w[q], 0), sbyte(w[q], 1), sbyte(w[q], 2), sbyte(w[q], 3));
+            } else {
+                *reinterpret_cast<uint4 *>(&s_b[tt][c16 * 16]) = rb[j];
+            }
             *reinterpret_cast<uint4 *>(&s_c[tt][c16 * 16]) = rc[j];
+        }
+    };
+
+    // one step of this lane's S states: the exact int32 partials of y
+    auto step = [&](int t, int xv, int &yhi, int &ylo) {
+        yhi = 0;
+        ylo = 0;
+        if constexpr (WIDEB) {
+            // every coefficient read first, then the S updates
+            int bv[S];
+            uint32_t cw[S / 4];
+#pragma unroll
+            for (int q = 0; q < S / 4; ++q) {
+                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[t][g * S + 4 * q]);
+                bv[4 * q] = b4.x; bv[4 * q + 1] = b4.y; bv[4 * q + 2] = b4.z; bv[4 * q + 3] = b4.w;
+                cw[q] = *reinterpret_cast<const uint32_t *>(&s_c[t][g * S + 4 * q]);
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) update16_b(h[s], n2[s], bv[s], xv, sbyte(cw[s >> 2], s & 3), yhi, ylo);
+        } else {
+            uint32_t bw = 0, cw = 0;
+            for (int s = 0; s < S; ++s) {
+                bw |= (uint32_t)(uint8_t)s_b[t][g * S + s] << (8 * s);
+                cw |= (uint32_t)(uint8_t)s_c[t][g * S + s] << (8 * s);
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) update16(h[s], n2[s], __mul24(sbyte(bw, s), xv), sbyte(cw, s), yhi, ylo);
         }
     };
 
@@ -190,43 +215,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         __syncthreads();
         if (cidx + 1 < nchunks) prefetch(t0 + kTC);
 
-        // one step of this lane's S states: the exact int32 partials of y
-        auto update = [&](int t, int xv, int dmv, int &yhi, int &ylo) {
-            int32_t nt[S];
-            if constexpr (MODEL) {
-                xv = (xv * s_dt[dmv + 20] + 512) >> 10;           // rshr(xs * dt, 10)
-                for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + 2 * dmv, 0, 64000);
-            } else {
-                for (int s = 0; s < S; ++s) nt[s] = ndec[s];
-            }
-            uint32_t bw[(S + 3) / 4], cw[(S + 3) / 4];
-            if constexpr (S >= 4) {
-                for (int q = 0; q < S / 4; ++q) {
-                    bw[q] = *reinterpret_cast<const uint32_t *>(&s_b[t][g * S + 4 * q]);
-                    cw[q] = *reinterpret_cast<const uint32_t *>(&s_c[t][g * S + 4 * q]);
-                }
-            } else {
-                uint32_t bb = 0, cc = 0;
-                for (int s = 0; s < S; ++s) {
-                    bb |= (uint32_t)(uint8_t)s_b[t][g * S + s] << (8 * s);
-                    cc |= (uint32_t)(uint8_t)s_c[t][g * S + s] << (8 * s);
-                }
-                bw[0] = bb;
-                cw[0] = cc;
-            }
-            yhi = 0;
-            ylo = 0;
-#pragma unroll
-            for (int s = 0; s < S; ++s)
-                update16(h[s], nt[s], __mul24(sbyte(bw[s >> 2], s & 3), xv), sbyte(cw[s >> 2], s & 3), yhi, ylo);
-        };
         for (int t4 = 0; t4 < tn; t4 += 4) {
-            const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_xa[0][ch][t4]);
-            uint32_t dmw = 0, zw = 0;
-            if constexpr (MODEL) {
-                dmw = *reinterpret_cast<const uint32_t *>(&s_xa[1][ch][t4]);
-                zw = *reinterpret_cast<const uint32_t *>(&s_xa[2][ch][t4]);
-            }
+            const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_x[ch][t4]);
             const int tend = min(4, tn - t4);
             if constexpr (DEFER) {
                 if (tend == 4) {
@@ -234,9 +224,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                     // across all eight (no DPP wait states)
                     int y[8];
 #pragma unroll
-                    for (int tt = 0; tt < 4; ++tt)
-                        update(t4 + tt, sbyte(xw, tt), MODEL ? clamp32(sbyte(dmw, tt), -20, 20) : 0, y[2 * tt],
-                               y[2 * tt + 1]);
+                    for (int tt = 0; tt < 4; ++tt) step(t4 + tt, sbyte(xw, tt), y[2 * tt], y[2 * tt + 1]);
 #pragma unroll
                     for (int q = 0; q < 8; ++q) if constexpr (G >= 2) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0xB1, 0xF, 0xF, false);
 #pragma unroll
@@ -250,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
                 } else {
                     for (int tt = 0; tt < tend; ++tt) {
                         int yhi, ylo;
-                        update(t4 + tt, sbyte(xw, tt), MODEL ? clamp32(sbyte(dmw, tt), -20, 20) : 0, yhi, ylo);
+                        step(t4 + tt, sbyte(xw, tt), yhi, ylo);
                         s_y[t4 + tt][ch] = make_int2(group_sum<G>(yhi), group_sum<G>(ylo));
                     }
                 }
@@ -258,79 +246,31 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             }
             for (int tt = 0; tt < tend; ++tt) {
                 const int t = t4 + tt;
-                int xv = sbyte(xw, tt);
-                int32_t nt[S];
-                if constexpr (MODEL) {
-                    const int dmv = clamp32(sbyte(dmw, tt), -20, 20);
-                    xv = (xv * s_dt[dmv + 20] + 512) >> 10;           // rshr(xs * dt, 10)
-                    for (int s = 0; s < S; ++s) nt[s] = clamp32(ndec[s] + 2 * dmv, 0, 64000);
-                } else {
-                    for (int s = 0; s < S; ++s) nt[s] = ndec[s];
-                }
-                uint32_t bw[(S + 3) / 4], cw[(S + 3) / 4];
-                if constexpr (S >= 4) {
-                    for (int q = 0; q < S / 4; ++q) {
-                        bw[q] = *reinterpret_cast<const uint32_t *>(&s_b[t][g * S + 4 * q]);
-                        cw[q] = *reinterpret_cast<const uint32_t *>(&s_c[t][g * S + 4 * q]);
-                    }
-                } else {
-                    uint32_t bb = 0, cc = 0;
-                    for (int s = 0; s < S; ++s) {
-                        bb |= (uint32_t)(uint8_t)s_b[t][g * S + s] << (8 * s);
-                        cc |= (uint32_t)(uint8_t)s_c[t][g * S + s] << (8 * s);
-                    }
-                    bw[0] = bb;
-                    cw[0] = cc;
-                }
-                int yhi = 0, ylo = 0;
-                for (int s = 0; s < S; ++s)
-                    update16(h[s], nt[s], __mul24(sbyte(bw[s >> 2], s & 3), xv), sbyte(cw[s >> 2], s & 3), yhi, ylo);
+                int yhi, ylo;
+                step(t, sbyte(xw, tt), yhi, ylo);
                 yhi = group_sum<G>(yhi);
                 ylo = group_sum<G>(ylo);
-                const int64_t y64 = ((int64_t)yhi << 16) + ylo;
-                const int32_t y32 = sat32_64(y64);
+                const int32_t y32 = sat32_64(((int64_t)yhi << 16) + ylo);
                 if (g == 0) {
-                    if constexpr (MODEL) {
-                        const int zv = sbyte(zw, tt);
-                        const int64_t yg = ((int64_t)y32 * s_gate[zv + 128]) >> 15;
-                        s_o8[t][ch] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
-                    } else if constexpr (STAGE_Y) {
-                        s_o32[t][ch] = y32;
-                    } else if (active) {
-                        a.y[(row0 + t0 + t) * a.x_row + (int64_t)hd * a.P + p] = y32;
-                    }
+                    if constexpr (STAGE_Y) s_o32[t][ch] = y32;
+                    else if (active) a.y[(row0 + t0 + t) * a.x_row + (int64_t)hd * a.P + p] = y32;
                 }
             }
         }
         __syncthreads();
         if constexpr (DEFER) {
-            // chunk epilogue: y = sat32(yhi * 2^k + ylo), then the gate and requant
-            // (model mode) or the int32 output
+            // chunk epilogue: y = sat32(yhi * 2^16 + ylo)
             for (int i = tid; i < kTC * CH; i += kThreads) {
                 const int tt = i / CH, cc = i % CH;
                 if (tt < tn) {
                     const int2 yv = s_y[tt][cc];
-                    const int32_t y32 = sat32_64(((int64_t)yv.x << 16) + yv.y);
-                    if constexpr (MODEL) {
-                        const int zv = s_xa[2][cc][tt];
-                        const int64_t yg = ((int64_t)y32 * s_gate[zv + 128]) >> 15;
-                        s_o8[tt][cc] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
-                    } else {
-                        s_o32[tt][cc] = y32;
-                    }
+                    s_o32[tt][cc] = sat32_64(((int64_t)yv.x << 16) + yv.y);
                 }
             }
             __syncthreads();
         }
         // ---- write the staged outputs of this chunk
-        if constexpr (MODEL) {
-            for (int i = tid; i < kTC * X16; i += kThreads) {
-                const int tt = i / X16, c16 = i % X16;
-                if (tt < tn && p0 + c16 * 16 < a.P)
-                    *reinterpret_cast<uint4 *>(a.yo + (row0 + t0 + tt) * a.x_row + p0 + c16 * 16) =
-                        *reinterpret_cast<const uint4 *>(&s_o8[tt][c16 * 16]);
-            }
-        } else if constexpr (STAGE_Y) {
+        if constexpr (STAGE_Y) {
             constexpr int Y4 = CH / 4;
             for (int i = tid; i < kTC * Y4; i += kThreads) {
                 const int tt = i / Y4, c4 = i % Y4;
@@ -447,15 +387,17 @@ hipError_t launch_fast_n(int G, const ScanArgs &a, hipStream_t st) {
 
 template <int MODE>
 hipError_t launch_scan(const ScanArgs &a, int N, bool fast, hipStream_t st) {
-    if (fast) {
-        const int G = pick_g(N, (int64_t)a.B * a.H * a.P);
-        switch (N) {
-            case 16: return launch_fast_n<16, MODE>(G, a, st);
-            case 32: return launch_fast_n<32, MODE>(G, a, st);
-            case 64: return launch_fast_n<64, MODE>(G, a, st);
-            case 128:
-                if constexpr (MODE != kModeModel) return launch_fast_n<128, MODE>(G, a, st);
-                break;
+    // (the model mode's fast shapes run model_scan_kernel; here it takes the
+    // generic kernel only)
+    if constexpr (MODE != kModeModel) {
+        if (fast) {
+            const int G = pick_g(N, (int64_t)a.B * a.H * a.P);
+            switch (N) {
+                case 16: return launch_fast_n<16, MODE>(G, a, st);
+                case 32: return launch_fast_n<32, MODE>(G, a, st);
+                case 64: return launch_fast_n<64, MODE>(G, a, st);
+                case 128: return launch_fast_n<128, MODE>(G, a, st);
+            }
         }
     }
     const int64_t lanes = (int64_t)a.B * a.H * a.P;
