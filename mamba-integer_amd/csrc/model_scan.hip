@@ -486,7 +486,9 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
         if (tid < kMTC) s_n[tid] = s_tab[clamp32(dtv, -127, 127) + 127];
     };
 
-    auto step = [&](int t, int xv, int n2) {
+    // one step of this lane's S states: the exact int32 partials of y (the
+    // channel's G lanes are summed per group of four steps below)
+    auto step = [&](int t, int xv, int n2, int &yhi, int &ylo) {
         int bv[S], cv[S];
         if constexpr (S >= 4) {
             for (int q = 0; q < S / 4; ++q) {
@@ -501,11 +503,9 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
                 cv[s] = s_c[t][g * S + s];
             }
         }
-        int yhi = 0, ylo = 0;
+        yhi = 0;
+        ylo = 0;
         for (int s = 0; s < S; ++s) update16_cs(h[s], n2, bv[s], xv, cv[s], yhi, ylo);
-        yhi = msum<G>(yhi);
-        ylo = msum<G>(ylo);
-        s_y[t][ch] = make_int2(yhi, ylo);
     };
 
     const int32_t ylim = 100 << 18;
@@ -523,10 +523,22 @@ __global__ __launch_bounds__(kMThreads) void ssd_scan_kernel(SScanArgs a) {
             const int4 n4 = *reinterpret_cast<const int4 *>(&s_n[t4]);
             const int nv[4] = {n4.x, n4.y, n4.z, n4.w};
             if (t4 + 4 <= tn) {
+                // the eight partials of the group reduced stage by stage across
+                // all eight: each DPP add reads a register written several
+                // instructions earlier, so it needs no wait states
+                int y[8];
 #pragma unroll
-                for (int tt = 0; tt < 4; ++tt) step(t4 + tt, sb(xw, tt), nv[tt]);
+                for (int tt = 0; tt < 4; ++tt) step(t4 + tt, sb(xw, tt), nv[tt], y[2 * tt], y[2 * tt + 1]);
+                msum_all<G>(y);
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][ch] = make_int2(y[2 * tt], y[2 * tt + 1]);
             } else {
-                for (int tt = 0; tt < tn - t4; ++tt) step(t4 + tt, sb(xw, tt), s_n[t4 + tt]);
+                for (int tt = 0; tt < tn - t4; ++tt) {
+                    int y[2];
+                    step(t4 + tt, sb(xw, tt), s_n[t4 + tt], y[0], y[1]);
+                    msum_all<G>(y);
+                    s_y[t4 + tt][ch] = make_int2(y[0], y[1]);
+                }
             }
         }
         __syncthreads();
