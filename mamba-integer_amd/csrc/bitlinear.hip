@@ -449,7 +449,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
 // gemm_any_kernel: any k % 16 == 0 and 4-byte aligned weights (e.g. dt_proj
 // with k = dt_rank): 4 waves of 64x64, weights fetched one word per thread.
-template <int KIND>
+// 64-deep halves of a stage that lie wholly past K are skipped (k = 48 has
+// one).  LDSOUT: int8 tiles leave through LDS as whole 16-byte row pieces
+// (requires ldo % 16 == 0 and a 16-byte aligned output), as in gemm_tile.
+template <int KIND, bool LDSOUT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemm_any_kernel(GemmArgs g) {
     __shared__ __align__(16) int8_t sA[2][kBM * kApitch];
     __shared__ __align__(16) uint32_t sW[2][kBN * kWpitch];
@@ -508,6 +511,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
         const int buf = kt & 1;
         if (kt + 1 < nk) load_stage((kt + 1) * kBK);
         for (int ks = 0; ks < kBK / 64; ++ks) {
+            if (kt * kBK + ks * 64 >= g.K) break;  // block-uniform: the rest of the stage is zero padding
             v4i fw[4], fa[4];
             for (int i = 0; i < 4; ++i) {
                 const int row = wn * 64 + i * 16 + l16;
@@ -524,6 +528,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void g
         __syncthreads();
     }
 
+    if constexpr (LDSOUT) {
+        // the requantised tile as dwords into LDS (the loop's last barrier
+        // freed the staging buffers), then 16-byte pieces of whole rows out
+        static_assert(KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD, "int8 tiles only");
+        int8_t *sO = &sA[0][0];
+        static_assert(kBM * kOpitch <= 2 * kBM * kApitch, "output tile must fit the staging buffers");
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int q = rshr32(acc[i][j][r], g.shift);
+                    const int v = KIND == MI_OUT_INT8 ? clamp32(q, -127, 127) : clamp32(q, -20, 20);
+                    pk |= (uint32_t)(v & 255) << (8 * r);
+                }
+                *reinterpret_cast<uint32_t *>(&sO[(wm * 64 + j * 16 + l16) * kOpitch + wn * 64 + i * 16 + 4 * lq]) = pk;
+            }
+        __syncthreads();
+        const int arow = tid >> 3, ac16 = tid & 7;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int row = arow + 32 * p;
+            const int gm = m0 + row, gn = n0 + ac16 * 16;
+            if (gm < g.M && gn < g.N) {
+                const v4i v = *reinterpret_cast<const v4i *>(&sO[row * kOpitch + ac16 * 16]);
+                int8_t *o = (int8_t *)g.out + (int64_t)gm * g.ldo + gn;
+                if (gn + 16 <= g.N) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(o));
+                } else {
+                    for (int e = 0; e < 16 && gn + e < g.N; ++e) o[e] = (int8_t)(v[e >> 2] >> (8 * (e & 3)));
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int m = m0 + wm * 64 + j * 16 + l16;
@@ -1013,12 +1054,15 @@ GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ld
 template <int KIND>
 hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
     const dim3 grid((unsigned)(((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN)));
+    constexpr bool kInt8Out = KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD;
     // gemm_kernel reads each weight row as 16-byte runs of 4 words
     if (g.kw % 4 != 0 || !aligned(g.w, 16)) {
-        hipLaunchKernelGGL(gemm_any_kernel<KIND>, grid, dim3(256), 0, st, g);
+        if (kInt8Out && g.ldo % 16 == 0 && aligned(g.out, 16))
+            hipLaunchKernelGGL((gemm_any_kernel<KIND, kInt8Out>), grid, dim3(256), 0, st, g);
+        else
+            hipLaunchKernelGGL((gemm_any_kernel<KIND, false>), grid, dim3(256), 0, st, g);
         return hipGetLastError();
     }
-    constexpr bool kInt8Out = KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD;
     if (kInt8Out && g.ldo % 16 == 0 && aligned(g.out, 16))
         hipLaunchKernelGGL((gemm_kernel<KIND, kInt8Out, kGemmNI>), grid, dim3(256), 0, st, g);
     else

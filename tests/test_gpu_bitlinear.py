@@ -91,13 +91,16 @@ def test_bitlinear_kinds(cuda, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(200, 200, 192), (130, 36, 64), (257, 129, 320), (200, 200, 768), (130, 36, 704),
-                                   (257, 129, 1536), (70, 300, 1472)])
+                                   (257, 129, 1536), (70, 300, 1472), (130, 36, 48), (257, 129, 80),
+                                   (200, 300, 112), (300, 1536, 48)])
 @pytest.mark.parametrize("pad", [0, 4, 16])
 def test_gemm_tile_edges(cuda, M, N, K, pad):
     """Prefill GEMM edge tiles: a K tail of 64 past the last 128-deep stage, ragged
     M and N (the int8 tile store's 16-byte runs cut short), output row pitches that
     select the staged 16-byte store (pitch % 16 == 0) or the per-lane dword
-    store, and the RESIDUAL row statistics."""
+    store, and the RESIDUAL row statistics.  K = 48, 80, 112 (weight rows of 3, 5,
+    7 words) take the generic kernel, with its skipped zero halves (48: the
+    dt_proj depth of the d768 model)."""
     import torch
     from mamba_int import ops, pack_ternary
     rng = np.random.default_rng(M * 3 + N + K + pad)
