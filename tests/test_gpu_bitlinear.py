@@ -92,7 +92,8 @@ def test_bitlinear_kinds(cuda, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(200, 200, 192), (130, 36, 64), (257, 129, 320), (200, 200, 768), (130, 36, 704),
                                    (257, 129, 1536), (70, 300, 1472), (130, 36, 48), (257, 129, 80),
-                                   (200, 300, 112), (300, 1536, 48)])
+                                   (200, 300, 112), (300, 1536, 48), (200, 80, 1536), (130, 36, 256),
+                                   (300, 160, 2048), (65, 17, 512), (1000, 150, 4096)])
 @pytest.mark.parametrize("pad", [0, 4, 16])
 def test_gemm_tile_edges(cuda, M, N, K, pad):
     """Prefill GEMM edge tiles: a K tail of 64 past the last 128-deep stage, ragged
@@ -100,7 +101,8 @@ def test_gemm_tile_edges(cuda, M, N, K, pad):
     select the staged 16-byte store (pitch % 16 == 0) or the per-lane dword
     store, and the RESIDUAL row statistics.  K = 48, 80, 112 (weight rows of 3, 5,
     7 words) take the generic kernel, with its skipped zero halves (48: the
-    dt_proj depth of the d768 model)."""
+    dt_proj depth of the d768 model).  N <= 160 with K % 256 == 0 (x_proj) takes
+    the staged GEMV kernel in 64-row groups, for int8 and int32 outputs."""
     import torch
     from mamba_int import ops, pack_ternary
     rng = np.random.default_rng(M * 3 + N + K + pad)
