@@ -344,6 +344,17 @@ def kernel_table():
                            "GB_s": 16318464 / ms / 1e6,
                            "roofline": {"bound": "mfma", "achieved": tops, "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
                                         "frac": tops / MFMA_I8_PEAK_TOPS}}
+    # the same kernel at the config-5 prefill in_proj shape (64 x 512 tokens,
+    # d2048 -> 2 x 4096), where per-launch fixed costs matter least
+    M5, K5, N5 = 32768, 2048, 8192
+    a5 = t8(M5, K5)
+    wp5 = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(N5, K5), dtype=np.int8))).to(dev)
+    o5 = torch.empty((M5, N5), dtype=torch.int8, device=dev)
+    ms5 = _time_kernel(lambda: ops.bitlinear(a5, wp5, ops.OUT_INT8, N5, shift=6, out=o5, path="gemm"), iters=5)
+    tops5 = 2 * M5 * N5 * K5 / ms5 / 1e9
+    out["config5_in_proj_gemm"] = {"ms": ms5, "TOPS": tops5, "mfma_frac": tops5 / MFMA_I8_PEAK_TOPS,
+                                   "shape": "M32768 K2048 N8192 -> int8"}
+    del a5, wp5, o5
     copies = 512
     wrot = wp.repeat(copies, 1).view(copies, N, K // 4)
     a1 = a[:1].contiguous()
