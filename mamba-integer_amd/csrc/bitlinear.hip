@@ -828,9 +828,12 @@ template <int KIND, int FT>
 __global__ __launch_bounds__(64 * kG64Waves) void gemv64s_kernel(GemmArgs g) {
     constexpr int WAVES = kG64Waves, U = kG64U;
     if (gridDim.y > 1) {
+        constexpr int kOutBytes = KIND == MI_OUT_INT8 || KIND == MI_OUT_DECAY_MOD ? 1 : 4;
         const int64_t m0 = 64 * (int64_t)blockIdx.y;
         g.a += m0 * g.lda;
-        g.out = (char *)g.out + m0 * g.ldo * (KIND == MI_OUT_INT32 ? 4 : 1);
+        g.out = (char *)g.out + m0 * g.ldo * kOutBytes;
+        if (g.x_scale) g.x_scale += m0;
+        if (g.row_stats) g.row_stats += 2 * m0;
         g.M = min(64, g.M - (int)m0);
     }
     __shared__ __align__(16) int8_t stage[WAVES][U][64 * 256];
