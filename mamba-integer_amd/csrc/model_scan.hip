@@ -4,7 +4,11 @@
 //
 // Layout: a block of NT threads owns CH = NT/G channels of one sequence; G
 // adjacent lanes share a channel and keep S = N/G states each in VGPRs (read
-// as two 16-bit fields by the update, update16).  Per chunk of 64 steps the block stages xs, dm, z
+// as two 16-bit fields by the update, update16).  The mixed block puts half
+// its threads in layout G and half in a layout G2 > G (at N = 16: 32 channels
+// of 8 lanes, then 16 of 16 lanes): where batch x d_inner gives 1 to 1.5
+// waves of 8-lane channels per SIMD, one such block per CU loads every SIMD
+// with the same work instead of leaving half of them with twice the rest.  Per chunk of 64 steps the block stages xs, dm, z
 // (transposed to channel-major bytes) and B, C (widened to int32 so a state
 // reads its coefficients with one ds_read_b128 per four states) through LDS,
 // in two buffers where they fit: chunk c+1 is staged right after chunk c's
@@ -77,10 +81,18 @@ __device__ __forceinline__ void msum_all(int (&v)[K]) {
         if constexpr (G >= 16) v[k] += __builtin_amdgcn_update_dpp(0, v[k], 0x140, 0xF, 0xF, true);
 }
 
-template <int N, int G, int NT>
+// G2 = 0: every lane of the block in layout G.  G2 > G: threads [0, NT/2)
+// in layout G and [NT/2, NT) in layout G2 (fewer states a lane), the block's
+// first CHA channels in the first; with one block per CU and waves dealt to
+// the four SIMDs in turn, every SIMD then holds one wave of each.
+template <int N, int G, int NT, int G2 = 0>
 __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
-    constexpr int S = N / G;
-    constexpr int CH = NT / G;
+    constexpr bool MIX = G2 > 0;
+    constexpr int NTA = MIX ? NT / 2 : NT;           // threads of layout G
+    constexpr int CHA = NTA / G;
+    constexpr int CH = CHA + (MIX ? (NT - NTA) / G2 : 0);
+    constexpr int S = N / G;                          // the most states a lane holds
+    static_assert(!MIX || (G2 > G && NTA % 64 == 0 && N % G2 == 0), "mixed layout");
     constexpr int XP = kMTC + 4;
     constexpr int X16 = CH / 16;
     constexpr int XPIECES = kMTC * X16;
@@ -89,11 +101,13 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     constexpr int BCPIECES = kMTC * BC16;
     constexpr int BCPER = (BCPIECES + NT - 1) / NT;
     static_assert(N % 16 == 0 && CH % 16 == 0 && (S == 1 || S == 2 || S % 4 == 0), "state split");
+    static_assert(!MIX || N / G2 == 1 || N / G2 == 2 || (N / G2) % 4 == 0, "state split");
     // staging buffers: two (chunk c + 1 is staged while chunk c's epilogue runs)
     // where they fit in 64 KB of LDS, else one
     constexpr int kStage = 2 * CH * XP + CH * XP * 2 + 2 * kMTC * N * 4;
-    constexpr int NB = 2 * kStage + kMTC * CH * 9 + 297 * 4 <= 65536 ? 2 : 1;
-    static_assert(NB * kStage + kMTC * CH * 9 + 297 * 4 <= 65536, "LDS budget");
+    constexpr int kLds = MIX ? 163840 : 65536;   // a mixed block has its CU to itself
+    constexpr int NB = 2 * kStage + kMTC * CH * 9 + 297 * 4 <= kLds ? 2 : 1;
+    static_assert(NB * kStage + kMTC * CH * 9 + 297 * 4 <= kLds, "LDS budget");
 
     __shared__ __align__(16) int8_t s_x[NB][2][CH][XP];    // 2*dm, z (channel-major)
     __shared__ __align__(16) int16_t s_xd[NB][CH][XP];      // rshr(xs * dt(dm), 10), |xd| <= 813
@@ -105,8 +119,11 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     __shared__ int32_t s_gate[256];
 
     const int tid = threadIdx.x;
-    const int ch = tid / G;
-    const int g = tid % G;
+    const bool second = MIX && tid >= NTA;                     // wave-uniform
+    constexpr int GB = MIX ? G2 : G;
+    const int SL = second ? N / GB : S;                        // this lane's states
+    const int ch = second ? CHA + (tid - NTA) / GB : tid / G;
+    const int g = second ? (tid - NTA) % GB : tid % G;
     const int p0 = blockIdx.x * CH;
     const int b = blockIdx.y;
     const int p = p0 + ch;
@@ -118,10 +135,12 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     int32_t base2[S], h[S];  // 2 * base: the update takes n2 = 2n
     bool safe = true;
     {
-        const int64_t sidx = ((int64_t)b * a.D + (active ? p : 0)) * N + g * S;
+        const int64_t sidx = ((int64_t)b * a.D + (active ? p : 0)) * N + g * SL;
+#pragma unroll
         for (int s = 0; s < S; ++s) {
-            h[s] = (a.h_in && active) ? a.h_in[sidx + s] : 0;
-            const int32_t bs = active ? a.base[(int64_t)p * N + g * S + s] : 16000;
+            const bool own = s < SL;
+            h[s] = (a.h_in && active && own) ? a.h_in[sidx + s] : 0;
+            const int32_t bs = active && own ? a.base[(int64_t)p * N + g * SL + s] : 16000;
             base2[s] = 2 * bs;
             safe = safe && bs >= 20 && bs <= 32000 - 20;
         }
@@ -187,34 +206,35 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         }
     };
 
-    // this lane's S coefficients of B and C for step t (LDS row t < kMTC)
-    auto load_bc = [&](int bf, int t, int (&bv)[S], int (&cv)[S]) {
-        if constexpr (S >= 4) {
+    // this lane's SS coefficients of B and C for step t (LDS row t < kMTC)
+    auto load_bc = [&](int bf, int t, auto &bv, auto &cv) {
+        constexpr int SS = sizeof(bv) / sizeof(int);
+        if constexpr (SS >= 4) {
 #pragma unroll
-            for (int q = 0; q < S / 4; ++q) {
-                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[bf][t][g * S + 4 * q]);
-                const int4 c4 = *reinterpret_cast<const int4 *>(&s_c[bf][t][g * S + 4 * q]);
+            for (int q = 0; q < SS / 4; ++q) {
+                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[bf][t][g * SS + 4 * q]);
+                const int4 c4 = *reinterpret_cast<const int4 *>(&s_c[bf][t][g * SS + 4 * q]);
                 bv[4 * q] = b4.x; bv[4 * q + 1] = b4.y; bv[4 * q + 2] = b4.z; bv[4 * q + 3] = b4.w;
                 cv[4 * q] = c4.x; cv[4 * q + 1] = c4.y; cv[4 * q + 2] = c4.z; cv[4 * q + 3] = c4.w;
             }
-        } else if constexpr (S == 2) {
-            const int2 b2 = *reinterpret_cast<const int2 *>(&s_b[bf][t][g * S]);
-            const int2 c2 = *reinterpret_cast<const int2 *>(&s_c[bf][t][g * S]);
+        } else if constexpr (SS == 2) {
+            const int2 b2 = *reinterpret_cast<const int2 *>(&s_b[bf][t][g * SS]);
+            const int2 c2 = *reinterpret_cast<const int2 *>(&s_c[bf][t][g * SS]);
             bv[0] = b2.x; bv[1] = b2.y; cv[0] = c2.x; cv[1] = c2.y;
         } else {
             bv[0] = s_b[bf][t][g];
             cv[0] = s_c[bf][t][g];
         }
     };
-    // the recurrence of this lane's S states for one step: returns the exact
+    // the recurrence of this lane's SS states for one step: returns the exact
     // int32 partials (sum C*H, sum C*L) of y over the lane's states
-    auto update = [&](int xd, int dm2, const int (&bv)[S], const int (&cs)[S], int &yhi, int &ylo,
-                      auto clamp_tag) {
+    auto update = [&](int xd, int dm2, const auto &bv, const auto &cs, int &yhi, int &ylo, auto clamp_tag) {
         constexpr bool CLAMP = decltype(clamp_tag)::value;
+        constexpr int SS = sizeof(bv) / sizeof(int);
         yhi = 0;
         ylo = 0;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
+        for (int s = 0; s < SS; ++s) {
             const int n2 = CLAMP ? clamp32(base2[s] + dm2, 0, 64000) : base2[s] + dm2;
             update16_cs(h[s], n2, bv[s], xd, cs[s], yhi, ylo);
         }
@@ -235,14 +255,15 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         const int tn = min(kMTC, a.L - t0);
         const int cur = NB == 2 ? (cidx & 1) : 0;
 
-        auto run_chunk = [&](auto clamp_tag) {
+        auto run_chunk = [&](auto clamp_tag, auto g_tag) {
+            constexpr int GG = decltype(g_tag)::value, SS = N / GG;
             const int t4n = tn & ~3;  // steps in whole groups of four
             // groups of four steps: the next group's coefficients are read from
             // LDS while this group's recurrence runs, and the y partials of the
             // four steps are reduced together afterwards; two register sets of
             // coefficients alternate between the groups of a pair
-            auto group = [&](int t4, const int (&bq)[4][S], const int (&cq)[4][S], int (&bn)[4][S],
-                             int (&cn)[4][S]) {
+            auto group = [&](int t4, const int (&bq)[4][SS], const int (&cq)[4][SS], int (&bn)[4][SS],
+                             int (&cn)[4][SS]) {
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) load_bc(cur, min(t4 + 4 + tt, kMTC - 1), bn[tt], cn[tt]);
                 const uint32_t dw = *reinterpret_cast<const uint32_t *>(&s_x[cur][0][ch][t4]);
@@ -252,11 +273,11 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt)
                     update(xdv[tt], sb(dw, tt), bq[tt], cq[tt], y[2 * tt], y[2 * tt + 1], clamp_tag);
-                msum_all<G>(y);
+                msum_all<GG>(y);
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][ch] = make_int2(y[2 * tt], y[2 * tt + 1]);
             };
-            int b0[4][S], c0[4][S], b1[4][S], c1[4][S];
+            int b0[4][SS], c0[4][SS], b1[4][SS], c1[4][SS];
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) load_bc(cur, tt, b0[tt], c0[tt]);
             for (int t4 = 0; t4 < t4n; t4 += 8) {
@@ -264,17 +285,26 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
                 if (t4 + 4 < t4n) group(t4 + 4, b1, c1, b0, c0);
             }
             for (int t = t4n; t < tn; ++t) {
-                int bv[S], cv[S];
+                int bv[SS], cv[SS];
                 load_bc(cur, t, bv, cv);
                 const int dm2 = s_x[cur][0][ch][t];
                 int y[2];
                 update(s_xd[cur][ch][t], dm2, bv, cv, y[0], y[1], clamp_tag);
-                msum_all<G>(y);
+                msum_all<GG>(y);
                 s_y[t][ch] = make_int2(y[0], y[1]);  // all G lanes hold the same sums: no branch
             }
         };
-        if (wave_safe) run_chunk(std::false_type{});
-        else run_chunk(std::true_type{});
+        using GA = std::integral_constant<int, G>;
+        using GBT = std::integral_constant<int, GB>;
+        if (second) {
+            if constexpr (MIX) {
+                if (wave_safe) run_chunk(std::false_type{}, GBT{});
+                else run_chunk(std::true_type{}, GBT{});
+            }
+        } else {
+            if (wave_safe) run_chunk(std::false_type{}, GA{});
+            else run_chunk(std::true_type{}, GA{});
+        }
         if constexpr (NB == 2)
             if (cidx + 1 < nchunks) stash(cur ^ 1);
         __syncthreads();
@@ -308,8 +338,10 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         }
     }
     if (a.h_out && active) {
-        const int64_t sidx = ((int64_t)b * a.D + p) * N + g * S;
-        for (int s = 0; s < S; ++s) a.h_out[sidx + s] = h[s];
+        const int64_t sidx = ((int64_t)b * a.D + p) * N + g * SL;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            if (s < SL) a.h_out[sidx + s] = h[s];
     }
 }
 
@@ -323,6 +355,15 @@ hipError_t launch_model_ngt(const MScanArgs &a, hipStream_t st) {
         return hipGetLastError();
     }
     return hipErrorInvalidValue;
+}
+
+// The mixed block: NT/2 threads in layout G, NT/2 in layout G2.
+template <int N, int G, int G2, int NT>
+hipError_t launch_model_mix(const MScanArgs &a, hipStream_t st) {
+    constexpr int CH = NT / 2 / G + NT / 2 / G2;
+    hipLaunchKernelGGL((model_scan_kernel<N, G, NT, G2>), dim3((unsigned)((a.D + CH - 1) / CH), (unsigned)a.B),
+                       dim3(NT), 0, st, a);
+    return hipGetLastError();
 }
 
 template <int N>
@@ -713,7 +754,15 @@ hipError_t launch_model_scan(const int8_t *xs, const int8_t *dm, const int8_t *z
     // 0.118 vs 0.113, B64 x 1536 0.219 vs 0.197, B32 x 4096 0.287 vs 0.262;
     // B16 x 1536 0.068 vs 0.074
     switch (N) {
-        case 16: return launch_model_n<16>((int64_t)B * D >= 3072 * 16 ? 4 : 8, 256, a, st);
+        case 16:
+            // 1024 < G8 waves <= 1536 (1.5 a SIMD at most): the mixed block of
+            // 48 channels gives every SIMD one 2-state and one 1-state wave
+            // when one block per CU (256 CUs) covers the batch.  d_inner 1536
+            // x batch 8 x L2048: 0.317-0.325 ms (G8) -> 0.274-0.288 ms; the
+            // staging pieces moved onto the 1-state waves: 0.310 ms
+            if ((int64_t)B * D > 8192 && (int64_t)B * ((D + 47) / 48) <= 256)
+                return launch_model_mix<16, 8, 16, 512>(a, st);
+            return launch_model_n<16>((int64_t)B * D >= 3072 * 16 ? 4 : 8, 256, a, st);
         case 32: return launch_model_n<32>(8, 256, a, st);
         case 64: return launch_model_n<64>(16, 256, a, st);
     }

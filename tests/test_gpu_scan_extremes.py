@@ -92,13 +92,16 @@ def test_ssd_chunked_scan_state_extremes(cuda):
     assert np.array_equal(H(hout), h_ref)
 
 
-@pytest.mark.parametrize("N,B,L,D", [(16, 2, 140, 256), (32, 2, 140, 256), (16, 32, 70, 1536)])
+@pytest.mark.parametrize("N,B,L,D", [(16, 2, 140, 256), (32, 2, 140, 256), (16, 32, 70, 1536), (16, 8, 70, 1536),
+                                     (16, 6, 50, 1504)])
 def test_block_scan_state_extremes(cuda, N, B, L, D):
     """mi_block_scan (the fused prefill scan) from full-range states, bases at
     the clamp edges 0 and 32000 (and within 20 of them, so some waves take the
     clamped decay and some the unclamped one), dm over its whole range.  The
     32 x 1536 case takes the 4-lanes-per-channel layout (batch x d_inner >=
-    49152), the others 8 lanes."""
+    49152); 8 x 1536 and 6 x 1504 the mixed 48-channel block (8 lanes a
+    channel in one half, 16 in the other; 1504 ends in a block with 16 of its
+    48 channels); the others 8 lanes."""
     from mamba_int import ops
     rng = np.random.default_rng(200 + N + B)
     R = 16
