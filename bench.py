@@ -32,10 +32,10 @@ HBM_PEAK_GBS = 8000.0
 # same counters on a 256 MiB device copy (FETCH x 2.000, WRITE x 1.000)
 IN_PROJ_STAGE_TRAFFIC_B8 = 1456128   # 561.0 KiB x 2 + 300.0 KiB
 VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 39321.6 G/s
-# VALU lane-ops the prefill block scan issues per state update at the bench
-# shape, measured with rocprofv3 --pmc SQ_INSTS_VALU (wave64 instructions x 64
-# / updates; profiles/scan_kernels_valu_pmc.md)
-SCAN_LANE_OPS_PER_UPDATE = 16.07
+# VALU lane-ops the prefill block scan (the mixed 48-channel block) issues per
+# state update at the bench shape, measured with rocprofv3 --pmc SQ_INSTS_VALU
+# (wave64 instructions x 64 / updates; profiles/scan_kernels_valu_pmc.md)
+SCAN_LANE_OPS_PER_UPDATE = 18.58
 # the same for the config-4 chunked multi-head scan (B4 L8192, 24 heads x 64, N128)
 C4_LANE_OPS_PER_UPDATE = 9.03
 MFMA_I8_PEAK_TOPS = 5000.0
@@ -612,7 +612,7 @@ def main():
             "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS,
         },
         "roofline_scan": {
-            "kernel": "prefill fused block scan (model_scan_kernel<16,G>), one launch per layer",
+            "kernel": "prefill fused block scan (model_scan_kernel<16,8,512,16>, the mixed 48-channel block), one launch per layer",
             "bound": "valu", "bytes_per_launch": sbytes, "avg_launch_ms": scan_avg_ms,
             "launches_timed": len(scan_ms), "hbm_GB_s": achieved, "hbm_frac": achieved / HBM_PEAK_GBS,
             "updates_per_s": updates / (scan_avg_ms * 1e-3),
