@@ -99,14 +99,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     // Lanes of one or two states keep B as bytes: their latency-bound chain
     // measured slower with the wider staging (config 1: 22.0 -> 25.1 us)
     constexpr bool WIDEB = S >= 4;
-    __shared__ __align__(16) std::conditional_t<WIDEB, int32_t, int8_t> s_b[kTC][N];
-    __shared__ __align__(16) int8_t s_c[kTC][N];
     constexpr bool STAGE_Y = CH <= 64;  // int32 y staged in LDS (16 KB at most)
-    __shared__ __align__(16) int32_t s_o32[STAGE_Y ? kTC : 1][STAGE_Y ? CH : 4];
     // blocks of <= 32 channels (G >= 8) reduce the y partials of four steps
     // together and park the exact (yhi, ylo) pairs here; the chunk epilogue
     // recombines and saturates once per (step, channel)
     constexpr bool DEFER = CH <= 32;
+    // C32: C staged as int32 C * 2^16 as well (update16_cs: y's high partial
+    // in one v_dot2c, no byte extraction per state), where the block's LDS
+    // then stays within 80 KB (two blocks per CU).  Channel mode only: B8 x
+    // L2048 x 1536 channels, N32 0.380 -> 0.367 ms, N64 0.626 -> 0.614 ms;
+    // the head layout (B4 x L8192, 24 heads x 64, N128) measured 2.466 ->
+    // 2.512 ms with it (twice the LDS bytes per step for C)
+    constexpr int kLdsC32 = CH * (kTC + 4) + 2 * kTC * N * 4 + (STAGE_Y ? kTC * CH * 4 : 16) + (DEFER ? kTC * CH * 8 : 8);
+    constexpr bool C32 = WIDEB && MODE == kModeChannel && kLdsC32 <= 81920;
+    __shared__ __align__(16) std::conditional_t<WIDEB, int32_t, int8_t> s_b[kTC][N];
+    __shared__ __align__(16) std::conditional_t<C32, int32_t, int8_t> s_c[kTC][N];
+    __shared__ __align__(16) int32_t s_o32[STAGE_Y ? kTC : 1][STAGE_Y ? CH : 4];
     __shared__ __align__(16) int2 s_y[DEFER ? kTC : 1][DEFER ? CH : 1];
 
     const int tid = threadIdx.x;
@@ -174,7 +182,16 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
             } else {
                 *reinterpret_cast<uint4 *>(&s_b[tt][c16 * 16]) = rb[j];
             }
-            *reinterpret_cast<uint4 *>(&s_c[tt][c16 * 16]) = rc[j];
+            if constexpr (C32) {
+                const uint32_t w[4] = {rc[j].x, rc[j].y, rc[j].z, rc[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<int4 *>(&s_c[tt][c16 * 16 + 4 * q]) =
+                        make_int4(sbyte(w[q], 0) * 65536, sbyte(w[q], 1) * 65536, sbyte(w[q], 2) * 65536,
+                                  sbyte(w[q], 3) * 65536);
+            } else {
+                *reinterpret_cast<uint4 *>(&s_c[tt][c16 * 16]) = rc[j];
+            }
         }
     };
 
@@ -182,7 +199,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     auto step = [&](int t, int xv, int &yhi, int &ylo) {
         yhi = 0;
         ylo = 0;
-        if constexpr (WIDEB) {
+        if constexpr (C32) {
+            // every coefficient read first, then the S updates
+            int bv[S], cv[S];
+#pragma unroll
+            for (int q = 0; q < S / 4; ++q) {
+                const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[t][g * S + 4 * q]);
+                const int4 c4 = *reinterpret_cast<const int4 *>(&s_c[t][g * S + 4 * q]);
+                bv[4 * q] = b4.x; bv[4 * q + 1] = b4.y; bv[4 * q + 2] = b4.z; bv[4 * q + 3] = b4.w;
+                cv[4 * q] = c4.x; cv[4 * q + 1] = c4.y; cv[4 * q + 2] = c4.z; cv[4 * q + 3] = c4.w;
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) update16_cs(h[s], n2[s], bv[s], xv, cv[s], yhi, ylo);
+        } else if constexpr (WIDEB) {
             // every coefficient read first, then the S updates
             int bv[S];
             uint32_t cw[S / 4];
