@@ -8,8 +8,9 @@
 // its threads in layout G and half in a layout G2 > G (at N = 16: 32 channels
 // of 8 lanes, then 16 of 16 lanes): where batch x d_inner gives 1 to 1.5
 // waves of 8-lane channels per SIMD, one such block per CU loads every SIMD
-// with the same work instead of leaving half of them with twice the rest.  Per chunk of 64 steps the block stages xs, dm, z
-// (transposed to channel-major bytes) and B, C (widened to int32 so a state
+// with the same work instead of leaving half of them with twice the rest.
+// Per chunk of 64 steps the block stages xs, dm, z (transposed to
+// channel-major bytes) and B, C (widened to int32 so a state
 // reads its coefficients with one ds_read_b128 per four states) through LDS,
 // in two buffers where they fit: chunk c+1 is staged right after chunk c's
 // steps, and its global loads were issued a whole chunk earlier.
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     static_assert(N % 16 == 0 && CH % 16 == 0 && (S == 1 || S == 2 || S % 4 == 0), "state split");
     static_assert(!MIX || N / G2 == 1 || N / G2 == 2 || (N / G2) % 4 == 0, "state split");
     // staging buffers: two (chunk c + 1 is staged while chunk c's epilogue runs)
-    // where they fit in 64 KB of LDS, else one
+    // where they fit in 64 KB of LDS (160 KB for a mixed block), else one
     constexpr int kStage = 2 * CH * XP + CH * XP * 2 + 2 * kMTC * N * 4;
     constexpr int kLds = MIX ? 163840 : 65536;   // a mixed block has its CU to itself
     constexpr int NB = 2 * kStage + kMTC * CH * 9 + 297 * 4 <= kLds ? 2 : 1;
