@@ -150,3 +150,28 @@ def test_ssd_block_scan_state_extremes(cuda, L):
     y = ops.ssd_block_scan(T(xs), T(xp), T(xz), D, T(tab), Hh, N, 14, h_in=h, h_out=h)
     assert np.array_equal(H(y), ref_y)
     assert np.array_equal(H(h), ref_h)
+
+
+@pytest.mark.parametrize("B,L,D", [(8, 77, 1520), (8, 77, 1552), (1, 33, 8208), (3, 5, 3072)])
+def test_block_scan_mixed_route_edges(cuda, B, L, D):
+    """mi_block_scan from a zero state (no h_in) at the edges of the mixed
+    48-channel block's route (batch x d_inner > 8192 and batch x
+    ceil(d_inner / 48) <= 256): 8 x 1520 ends in a block whose 16-lane half
+    has no channel, 8 x 1552 needs 264 blocks and keeps 8 lanes a channel,
+    1 x 8208 runs 171 mixed blocks, 3 x 3072 192 of them; L not a multiple
+    of 4 or 64."""
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(B * L + D)
+    N, R = 16, 48
+    W = R + 2 * N
+    xs = i8(rng, B, L, D, lo=-128)
+    dm = i8(rng, B, L, D, lo=-128)
+    xp = i8(rng, B, L, W, lo=-128)
+    z = i8(rng, B, L, 2 * D, lo=-128)
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int32)
+    yo_ref, h_ref = O.block_scan(xs, dm, xp, R, z, D, base, 15, 14)
+    hout = torch.full((B, D, N), 7, dtype=torch.int32, device="cuda")
+    yo = ops.block_scan(T(xs), T(dm), T(xp), R, T(z), D, T(base), 15, 14, h_out=hout)
+    assert np.array_equal(H(yo), yo_ref)
+    assert np.array_equal(H(hout), h_ref)
