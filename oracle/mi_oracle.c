@@ -134,7 +134,11 @@ void mo_dyadic_scan_f32(const float *x, const int32_t *nums, const int32_t *shif
                 int64_t off = ((int64_t)b * S + t) * D + d;
                 float xs = x[off] * scale_f;
                 long long xf = (long long)xs;
+                if (g_mutation == 7) xf = llroundf(xs);          /* planted: round, not truncate */
+                if (g_mutation == 8) xf = (long long)floorf(xs); /* planted: floor, not truncate */
                 h = h * (long long)nums[off];
+                if (g_mutation == 9 && shifts[off] > 0)          /* planted: rounding shift */
+                    h += (long long)1 << (shifts[off] - 1);
                 h = h >> shifts[off];
                 h += xf;
                 hout[off] = (float)h / scale_f;

@@ -110,6 +110,38 @@ def test_scan_f32_reference_semantics(cuda):
     assert np.array_equal(H(h).view(np.uint32), h_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("sb", [0, 8, 20, 40])
+def test_scan_f32_varied_shifts_and_scale_bits(cuda, sb):
+    """Per-element shifts in {0, 1, 7, 15, 31} with nums up to 2^shift, signs and
+    magnitudes mixed, plus exact fractional inputs (-1.5, 1.75, -0.25 units: truncation
+    toward zero) and a negative impulse at decay 1/2 (arithmetic-shift floor); the
+    inputs keep |h * num| < 2^63 as the reference's int64 state requires."""
+    from mamba_int import ops
+    rng = np.random.default_rng(50 + sb)
+    B, S, D = 3, 96, 200
+    mag = rng.choice([0.5, 4.0, 16.0], size=(B, S, D)) * (2.0 ** -max(0, sb - 20))
+    x = (rng.standard_normal((B, S, D)) * mag).astype(np.float32)
+    shifts = rng.choice(np.array([0, 1, 7, 15, 31], np.int32), size=(B, S, D)).astype(np.int32)
+    hi = np.minimum(np.left_shift(np.int64(1), shifts.astype(np.int64)), 2**31 - 1)
+    nums = (rng.random((B, S, D)) * (hi + 1)).astype(np.int64).clip(0, 2**31 - 1).astype(np.int32)
+    nums[shifts == 0] = rng.integers(0, 2, size=int((shifts == 0).sum()))   # decay 0 or 1
+    u = 2.0 ** -sb
+    x[0, :, 0] = np.float32(-1.5 * u)
+    x[0, :, 1] = np.float32(1.75 * u)
+    x[0, :, 2] = np.float32(-0.25 * u)
+    nums[0, :, :3] = 0
+    x[1, :, 3] = 0
+    x[1, 0, 3] = np.float32(-3 * u)
+    nums[1, :, 3], shifts[1, :, 3] = 1, 1
+    assert (np.abs(x.astype(np.float64)) * 2.0 ** sb).sum(axis=1).max() * 2**31 < 2**63
+    h_ref = O.dyadic_scan_f32(x, nums, shifts, sb)
+    h = H(ops.dyadic_scan_f32(T(x), T(nums), T(shifts), sb))
+    assert np.array_equal(h.view(np.uint32), h_ref.view(np.uint32))
+    assert np.array_equal(h[0, :, :3].astype(np.float64) / u,
+                          np.tile([-1.0, 1.0, 0.0], (S, 1)))
+    assert np.array_equal(h[1, :5, 3].astype(np.float64) / u, [-3, -2, -1, -1, -1])
+
+
 def test_scan_elementwise(cuda):
     from mamba_int import ops
     rng = np.random.default_rng(9)

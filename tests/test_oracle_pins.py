@@ -127,6 +127,125 @@ def test_scan_f32_matches_reference_python_forward(rng):
         assert np.all(diff >= -tol) and np.all(diff <= tol)
 
 
+# Exact pins of the float-compat scan (dyadic_mamba_kernel.cu:35-63).  The kernel's
+# float steps are exact except two: x * 2^sb is a power-of-two scaling (exact in fp32),
+# the conversion to long long truncates toward zero, (float)h rounds to nearest-even,
+# and the division by 2^sb is exact again.  So the whole output is fixed by integer
+# arithmetic plus one rounding, restated here with Python integers.
+def _f32_round_int(h: int) -> int:
+    """The integer value of (float)h: round to 24 significant bits, ties to even."""
+    a = abs(h)
+    drop = a.bit_length() - 24
+    if drop <= 0:
+        return h
+    q, r = a >> drop, a & ((1 << drop) - 1)
+    half = 1 << (drop - 1)
+    if r > half or (r == half and q & 1):
+        q += 1
+    return (q << drop) * (1 if h >= 0 else -1)
+
+
+def _py_scan_f32(x, nums, shifts, sb):
+    """Brute force of launch_dyadic_scan with Python integers; output in float64
+    (every value it takes is exact there: 24-bit significand times a power of 2)."""
+    B, S, D = x.shape
+    out = np.zeros((B, S, D), np.float64)
+    for b in range(B):
+        for d in range(D):
+            h = 0
+            for t in range(S):
+                xf = math.trunc(Fraction(float(x[b, t, d])) * (1 << sb))   # toward zero
+                h = (h * int(nums[b, t, d])) >> int(shifts[b, t, d])      # Python >> floors
+                h += xf
+                out[b, t, d] = _f32_round_int(h) / 2.0**sb
+    return out
+
+
+def _f32_exact(hk, want):
+    return np.array_equal(hk.astype(np.float64), want)
+
+
+def test_f32_round_int_known_values():
+    """(float) of integers at the rounding boundaries of a 24-bit significand."""
+    assert _f32_round_int(2**24 + 1) == 2**24                 # tie, even stays
+    assert _f32_round_int(2**24 + 3) == 2**24 + 4             # tie, odd rounds up
+    assert _f32_round_int(-(2**24 + 3)) == -(2**24 + 4)
+    assert _f32_round_int(2**25 + 3) == 2**25 + 4             # above half
+    assert _f32_round_int(2**25 + 1) == 2**25
+    # against the hardware's float64 -> float32 conversion (each v is exact in float64)
+    for v in (2**24 + 1, 2**24 + 3, 2**25 + 3, 2**40 + 2**16 + 1, -(2**33 + 2**9), 2**40 + 2**16):
+        assert _f32_round_int(v) == int(np.float32(float(v))), v
+
+
+def test_scan_f32_truncates_toward_zero():
+    """num = 0 leaves h = x_fixed = trunc(x * 2^sb): -1.5 units gives -1 (floor gives -2,
+    round gives -2), +1.75 units gives 1 (round gives 2), -0.25 units gives 0."""
+    for sb in (0, 8, 20):
+        u = 2.0**-sb
+        vals = np.array([-1.5, 1.75, -0.25, 0.75, -2.5, 3.5, -1000.75, 123456.5], np.float64) * u
+        x = vals.astype(np.float32).reshape(1, -1, 1)
+        assert np.array_equal(x.astype(np.float64).ravel(), vals)        # exact inputs
+        nums = np.zeros(x.shape, np.int32)
+        shifts = np.full(x.shape, 15, np.int32)
+        hk = O.dyadic_scan_f32(x, nums, shifts, sb)
+        want = np.array([-1, 1, 0, 0, -2, 3, -1000, 123456], np.float64) * u
+        assert np.array_equal(hk.astype(np.float64).ravel(), want), sb
+
+
+def test_scan_f32_full_decay_is_prefix_sum(rng):
+    """num = 2^shift: h_t = sum of trunc(x_s * 2^sb), output (float)h_t / 2^sb."""
+    for sb, shift in ((20, 15), (8, 7), (0, 1), (12, 30)):
+        x = (rng.standard_normal((2, 60, 9)) * 3).astype(np.float32)
+        nums = np.full(x.shape, 1 << shift, np.int32)
+        shifts = np.full(x.shape, shift, np.int32)
+        xf = np.trunc(x.astype(np.float64) * 2.0**sb).astype(np.int64)
+        pref = np.cumsum(xf, axis=1)
+        want = np.vectorize(lambda v: float(_f32_round_int(int(v))))(pref) / 2.0**sb
+        assert _f32_exact(O.dyadic_scan_f32(x, nums, shifts, sb), want), (sb, shift)
+
+
+def test_scan_f32_negative_impulse_floors():
+    """Decay 1/2 on a negative state: the arithmetic shift floors, so -3 -> -2 -> -1 -> -1
+    and stays there (a truncating divide would reach 0); a positive impulse 3 -> 1 -> 0."""
+    for sb in (0, 8, 20):
+        x = np.zeros((1, 6, 2), np.float32)
+        x[0, 0, 0] = np.float32(-3 * 2.0**-sb)
+        x[0, 0, 1] = np.float32(3 * 2.0**-sb)
+        for num, shift in ((1, 1), (64, 7), (1 << 14, 15), (1 << 30, 31)):
+            nums = np.full(x.shape, num, np.int32)
+            shifts = np.full(x.shape, shift, np.int32)
+            hk = O.dyadic_scan_f32(x, nums, shifts, sb).astype(np.float64) * 2.0**sb
+            assert np.array_equal(hk[0, :, 0], [-3, -2, -1, -1, -1, -1]), (sb, num, shift)
+            assert np.array_equal(hk[0, :, 1], [3, 1, 0, 0, 0, 0]), (sb, num, shift)
+
+
+def test_scan_f32_output_rounds_to_nearest_even():
+    """(float)h on states above 2^24 (num 1, shift 0: no decay; sb 0): step 0 loads
+    2^24, 2^24, 2^25, -2^24; step 1 adds 1, 3, 3, -3.  2^24 + 1 and 2^24 + 3 are ties
+    (even significand wins), 2^25 + 3 lies above the half."""
+    x = np.array([[[2**24, 2**24, 2**25, -2**24], [1, 3, 3, -3]]], np.float32)
+    nums = np.ones(x.shape, np.int32)
+    shifts = np.zeros(x.shape, np.int32)
+    hk = O.dyadic_scan_f32(x, nums, shifts, 0).astype(np.float64)
+    assert np.array_equal(hk[0, 1], [2**24, 2**24 + 4, 2**25 + 4, -(2**24 + 4)])
+
+
+@pytest.mark.parametrize("sb", [0, 8, 20])
+def test_scan_f32_brute_force(rng, sb):
+    """Random inputs, per-element shifts in {1, 7, 15, 31} with nums up to 2^shift, mixed
+    signs and magnitudes: equal to the Python-integer brute force at every step."""
+    B, S, D = 2, 40, 6
+    x = (rng.standard_normal((B, S, D)) * rng.choice([0.5, 4.0, 16.0], size=(B, S, D)))
+    x = x.astype(np.float32)
+    # inside the reference's defined range: |h * num| < 2^63 with |h| <= sum |x_fixed|
+    assert (np.abs(x.astype(np.float64)) * 2.0**sb).sum(axis=1).max() * 2**31 < 2**63
+    shifts = rng.choice(np.array([1, 7, 15, 31], np.int32), size=(B, S, D)).astype(np.int32)
+    hi = np.minimum(np.left_shift(np.int64(1), shifts.astype(np.int64)), 2**31 - 1)
+    nums = (rng.random((B, S, D)) * (hi + 1)).astype(np.int64).clip(0, 2**31 - 1).astype(np.int32)
+    hk = O.dyadic_scan_f32(x, nums, shifts, sb)
+    assert _f32_exact(hk, _py_scan_f32(x, nums, shifts, sb))
+
+
 def test_ssd_chunked_equals_sequential_for_any_chunk(rng):
     B, L, H, P, N = 2, 97, 3, 8, 16
     x, b, c = i8(rng, B, L, H, P), i8(rng, B, L, H, N), i8(rng, B, L, H, N)
@@ -401,6 +520,9 @@ MUTANT_PINS = {
     4: test_bitlinear_equals_reference_f_linear,
     5: test_norm_table_and_rounding,
     6: test_bitlinear_equals_reference_f_linear,
+    7: test_scan_f32_truncates_toward_zero,
+    8: test_scan_f32_truncates_toward_zero,
+    9: test_scan_f32_negative_impulse_floors,
 }
 
 
