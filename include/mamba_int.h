@@ -87,7 +87,8 @@ mi_status mi_dyadic_scan_f32(const float *x, const int32_t *nums, const int32_t 
 /* Elementwise recurrence, the integer form of DyadicScanFunction.apply
  * (mamba_integer_model.py:260-316): u, nums int32 [batch,len,channels];
  * h int32 [batch,len,channels] = sat32(floor(h_prev*num / 2^shift) + u);
- * h_in / h_out int32 [batch,channels] nullable.  decay_shift in [1,30]. */
+ * h_in / h_out int32 [batch,channels] nullable.  decay_shift in [1,30].
+ * len == 0 with h_out: h_out receives h_in (zeros when h_in is NULL). */
 mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t *nums, int decay_shift,
                                      int32_t *h, const int32_t *h_in, int32_t *h_out,
                                      int batch, int len, int channels, void *stream);
@@ -106,7 +107,8 @@ mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t *nums, int 
  *                p = 2^30; p = sat32(floor(p*num / 2^shift)) per step.  With
  *                0 <= num <= 2^shift it lies within len*2^-30 below the exact
  *                product (the floor recurrence has no exact product form).
- * h_in / h_out int32 [batch,channels] nullable (state before / after). */
+ * h_in / h_out int32 [batch,channels] nullable (state before / after);
+ * len == 0 with h_out: h_out receives h_in (zeros when h_in is NULL). */
 mi_status mi_dyadic_chunked_scan(const int32_t *u, const int32_t *nums, int decay_shift, int chunk,
                                  int32_t *h, int32_t *final_h, int32_t *decay_to_end,
                                  const int32_t *h_in, int32_t *h_out, int batch, int len, int channels,
@@ -225,7 +227,8 @@ mi_status mi_conv_squareplus(const int8_t *xz, int xz_stride, const int8_t *conv
  * last three x rows of each sequence; state_in [batch,3,d_inner] nullable
  * (zeros), and must not overlap state_out.  Identical to mi_bitlinear
  * (MI_OUT_INT8) followed by mi_conv_squareplus.  d_inner % 128 == 0,
- * d_model % 64 == 0. */
+ * d_model % 64 == 0.  len == 0: only state_out is written, = state_in
+ * (zeros when state_in is NULL). */
 mi_status mi_in_proj_conv(const int8_t *a, int lda, const uint8_t *w_in, int shift,
                           const int8_t *conv_w, const int32_t *conv_b, const int8_t *state_in,
                           int8_t *state_out, int8_t *xs, int8_t *xz, int ldxz, int batch, int len,

@@ -1038,6 +1038,13 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
 }
 
 // ------------------------------------------------------------ helpers
+// A call with no rows leaves each sequence's conv state as it was: the new
+// state is the old one (zeros when there is none), word by word.
+__global__ __launch_bounds__(256) void conv_state_carry_kernel(const uint32_t *in, uint32_t *out, int64_t words) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < words) out[i] = in ? in[i] : 0u;
+}
+
 __global__ void pack_ternary_kernel(const int8_t *w, uint32_t *p, int64_t words, int kw) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= words) return;
@@ -1275,6 +1282,23 @@ extern "C" mi_status mi_in_proj_conv(const int8_t *a, int lda, const uint8_t *w_
     MI_REQUIRE((int64_t)batch * len <= INT32_MAX - kBM && (int64_t)d_inner * 2 <= INT32_MAX, MI_ERR_BAD_DIM,
                "%s: size exceeds int32", fn);
     const int m = batch * len;
+    const uintptr_t sbytes = (uintptr_t)batch * 3 * (uintptr_t)d_inner;
+    if (len == 0 && sbytes > 0) {
+        // no rows: state_out receives state_in unchanged (zeros when state_in is NULL)
+        MI_REQUIRE(state_out, MI_ERR_NULL_POINTER, "%s: state_out is required", fn);
+        MI_REQUIRE(d_inner % 4 == 0 && aligned(state_out, 4) && aligned(state_in, 4), MI_ERR_BAD_ALIGNMENT,
+                   "%s: the states must be 4-byte aligned and d_inner a multiple of 4", fn);
+        if (state_in) {
+            const uintptr_t i0 = reinterpret_cast<uintptr_t>(state_in), o0 = reinterpret_cast<uintptr_t>(state_out);
+            MI_REQUIRE(i0 + sbytes <= o0 || o0 + sbytes <= i0, MI_ERR_BAD_ARG, "%s: state_in and state_out overlap",
+                       fn);
+        }
+        const int64_t words = (int64_t)(sbytes / 4);
+        hipLaunchKernelGGL(conv_state_carry_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                           as_stream(stream), reinterpret_cast<const uint32_t *>(state_in),
+                           reinterpret_cast<uint32_t *>(state_out), words);
+        return check_launch(fn);
+    }
     mi_status st = validate(fn, a, lda, w_in, xz, ldxz, MI_OUT_INT8, m, 2 * d_inner, d_model, shift, 0, nullptr);
     if (st != MI_OK || (int64_t)m * d_inner == 0) return st;
     MI_REQUIRE(d_inner % kBN == 0, MI_ERR_BAD_DIM, "%s: d_inner=%d must be a multiple of %d", fn, d_inner, kBN);
@@ -1286,7 +1310,6 @@ extern "C" mi_status mi_in_proj_conv(const int8_t *a, int lda, const uint8_t *w_
     MI_REQUIRE(aligned(conv_w, 4) && aligned(conv_b, 4) && aligned(xs, 4) && aligned(state_out, 4) &&
                    aligned(state_in, 4),
                MI_ERR_BAD_ALIGNMENT, "%s: conv_w, conv_b, xs and the states must be 4-byte aligned", fn);
-    const uintptr_t sbytes = (uintptr_t)batch * 3 * (uintptr_t)d_inner;
     if (state_in) {
         const uintptr_t i0 = reinterpret_cast<uintptr_t>(state_in), o0 = reinterpret_cast<uintptr_t>(state_out);
         // blocks read the old state of a sequence's first rows while others

@@ -677,8 +677,10 @@ extern "C" mi_status mi_dyadic_scan_elementwise(const int32_t *u, const int32_t 
     MI_REQUIRE(batch >= 0 && len >= 0 && channels >= 0, MI_ERR_BAD_DIM, "mi_dyadic_scan_elementwise: negative size");
     MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG,
                "mi_dyadic_scan_elementwise: decay_shift=%d outside [1,30]", decay_shift);
-    if ((int64_t)batch * channels == 0 || len == 0) return MI_OK;
-    MI_REQUIRE(u && nums && h, MI_ERR_NULL_POINTER, "mi_dyadic_scan_elementwise: u, nums and h are required");
+    // len == 0 with h_out: the kernel runs no step and writes h_out = h_in (zeros when NULL)
+    if ((int64_t)batch * channels == 0 || (len == 0 && !h_out)) return MI_OK;
+    MI_REQUIRE(len == 0 || (u && nums && h), MI_ERR_NULL_POINTER,
+               "mi_dyadic_scan_elementwise: u, nums and h are required");
     const int64_t lanes = (int64_t)batch * channels;
     hipLaunchKernelGGL(scan_elem_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, as_stream(stream), u,
                        nums, decay_shift, h, h_in, h_out, batch, len, channels);
@@ -693,8 +695,9 @@ extern "C" mi_status mi_dyadic_chunked_scan(const int32_t *u, const int32_t *num
     MI_REQUIRE(decay_shift >= 1 && decay_shift <= 30, MI_ERR_BAD_ARG,
                "mi_dyadic_chunked_scan: decay_shift=%d outside [1,30]", decay_shift);
     MI_REQUIRE(chunk >= 1, MI_ERR_BAD_ARG, "mi_dyadic_chunked_scan: chunk=%d must be >= 1", chunk);
-    if ((int64_t)batch * channels == 0 || len == 0) return MI_OK;
-    MI_REQUIRE(u && nums && h, MI_ERR_NULL_POINTER, "mi_dyadic_chunked_scan: u, nums and h are required");
+    // len == 0 with h_out: the kernel runs no step and writes h_out = h_in (zeros when NULL)
+    if ((int64_t)batch * channels == 0 || (len == 0 && !h_out)) return MI_OK;
+    MI_REQUIRE(len == 0 || (u && nums && h), MI_ERR_NULL_POINTER, "mi_dyadic_chunked_scan: u, nums and h are required");
     const int64_t lanes = (int64_t)batch * channels;
     const int nc = (int)((len + (int64_t)chunk - 1) / chunk);
     hipLaunchKernelGGL(chunked_scan_kernel, dim3((unsigned)((lanes + 63) / 64)), dim3(64), 0, as_stream(stream), u,

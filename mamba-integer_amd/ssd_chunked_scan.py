@@ -10,9 +10,11 @@ the integer recurrence of spec mi-spec-1:
 
 - ``h[t] = sat32(floor(h[t-1] * nums[t] / 2^shift) + u[t])`` on int32 u;
 - ``final_h`` is the state at the last step of each chunk;
-- ``decay_to_end`` is the chunk's cumulative decay prod(nums / 2^shift) as a
-  Q30 int32, rounded down after every step (the floor recurrence applied to
-  2^30 with zero input).
+- ``decay_to_end`` is the chunk's cumulative decay prod(nums / 2^shift),
+  float32 as in the reference (``:400``): the kernel's Q30 int32 (the floor
+  recurrence applied to 2^30 with zero input, rounded down after every step)
+  divided by 2^30.  ``mamba_int.ops.dyadic_chunked_scan`` returns the Q30
+  integers themselves.
 
 The reference's float recurrence (``h = decay * h + u``, ``:366``) has no
 floor; the integer one is not associative, so chunks only bound the outputs
@@ -52,8 +54,9 @@ def ssd_chunked_scan_forward(u: torch.Tensor, nums: torch.Tensor, shifts, chunk_
         raise TypeError("the integer chunked scan takes int32 u")
     if nums.is_floating_point():
         raise TypeError("the integer chunked scan takes integer decay numerators")
-    return ops.dyadic_chunked_scan(u.contiguous(), nums.to(torch.int32).contiguous(), _shift(shifts),
-                                   int(chunk_size))
+    h, final_h, dte_q30 = ops.dyadic_chunked_scan(u.contiguous(), nums.to(torch.int32).contiguous(),
+                                                  _shift(shifts), int(chunk_size))
+    return h, final_h, dte_q30.to(torch.float32) * (1.0 / (1 << 30))
 
 
 class SSDChunkedScanFunction:

@@ -148,7 +148,33 @@ def test_gpu_chunked_scan_state_continuation_and_dropin(cuda):
     h, fh, dte = ssd_chunked_scan_forward(_T(u), _T(n).to(torch.int64), shifts, 50)
     assert np.array_equal(h.cpu().numpy(), h_ref)
     assert np.array_equal(fh.cpu().numpy(), fh_ref)
-    assert np.array_equal(dte.cpu().numpy(), dte_ref)
+    # the drop-in returns the reference's float32 decay_to_end: Q30 / 2^30
+    assert dte.dtype == torch.float32
+    assert np.array_equal(dte.cpu().numpy(), (dte_ref.astype(np.float32) / np.float32(2**30)))
     assert torch.equal(SSDChunkedScanFunction.apply(_T(u), _T(n), shifts, 50), h)
     with pytest.raises(ValueError):
         ssd_chunked_scan_forward(_T(u), _T(n), torch.tensor([12, 13], device="cuda"), 50)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("with_state", [True, False])
+def test_gpu_scans_with_no_steps_carry_state(cuda, with_state):
+    """len = 0 with h_out: no step runs and h_out receives h_in unchanged (zeros when
+    h_in is None), for the chunked and the elementwise recurrence alike."""
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(12)
+    B, C = 3, 70
+    h0 = rng.integers(-2**31, 2**31, size=(B, C), dtype=np.int64).astype(np.int32)
+    want = h0 if with_state else np.zeros_like(h0)
+    u = torch.empty((B, 0, C), dtype=torch.int32, device="cuda")
+    for run in ("chunked", "elementwise"):
+        hs = torch.full((B, C), 0x5555, dtype=torch.int32, device="cuda")
+        h_in = _T(h0) if with_state else None
+        if run == "chunked":
+            h, fh, dte = ops.dyadic_chunked_scan(u, u, 15, 8, h_in=h_in, h_out=hs)
+            assert fh.shape == (B, 0, C) and dte.shape == (B, 0, C)
+        else:
+            h = ops.dyadic_scan_elementwise(u, u, 15, h_in=h_in, h_out=hs)
+        assert h.shape == (B, 0, C)
+        assert np.array_equal(hs.cpu().numpy(), want), run

@@ -69,3 +69,22 @@ def test_in_proj_conv_rejects_overlapping_states(cuda):
     cb = torch.zeros((D,), dtype=torch.int32, device="cuda")
     with pytest.raises(_lib.MIError, match="overlap"):
         ops.in_proj_conv(a, wp, 5, D, cw, cb, B, st, state_in=st)
+
+
+@pytest.mark.parametrize("with_state", [True, False])
+def test_in_proj_conv_no_rows_carries_state(cuda, with_state):
+    """len = 0: no row is computed and state_out receives state_in unchanged (zeros
+    when state_in is None), as a sequence with no new rows keeps its conv window."""
+    import torch
+    from mamba_int import ops
+    rng = np.random.default_rng(11)
+    B, d, D = 3, 64, 256
+    wp = O.pack_ternary(rng.integers(-1, 2, size=(2 * D, d), dtype=np.int8))
+    cw, cb = i8(rng, D, 4), rng.integers(-600, 600, size=D, dtype=np.int32)
+    st = i8(rng, B, 3, D)
+    st_out = torch.full((B, 3, D), 0x55, dtype=torch.int8, device="cuda")
+    a = torch.empty((0, d), dtype=torch.int8, device="cuda")
+    xs, xz = ops.in_proj_conv(a, T(wp), 5, D, T(cw), T(cb), B, st_out,
+                              state_in=T(st) if with_state else None)
+    assert xs.shape == (0, D) and xz.shape == (0, 2 * D)
+    assert np.array_equal(H(st_out), st if with_state else np.zeros_like(st))
