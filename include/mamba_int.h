@@ -1,6 +1,6 @@
 /*
  * mamba_int.h — C ABI of libmamba_int.so, the MI355X (gfx950) integer Mamba
- * inference path (spec mi-spec-1).
+ * inference path (spec mi-spec-2).
  *
  * Conventions (every entry point):
  *   - plain device pointers and sizes; the caller owns every buffer (the
@@ -54,11 +54,11 @@ typedef enum {
     MI_OUT_INT32 = 0,      /* int32 acc */
     MI_OUT_INT8 = 1,       /* int8 sat8(rshr(acc, shift)) */
     MI_OUT_DECAY_MOD = 2,  /* int8 clamp(rshr(acc, shift), -20, 20) */
-    MI_OUT_RESIDUAL = 3,   /* int32 r = satR(r + rshr(acc*res_mult, res_shift)), in place */
+    MI_OUT_RESIDUAL = 3,   /* int32 r = satR(r + rshr(clamp(acc, +-res_clamp)*res_mult, res_shift)), in place */
     MI_OUT_FLOAT = 4       /* fp32 acc * (w_scale * x_scale[m]) */
 } mi_out_kind;
 
-/* Library and spec version, e.g. "libmamba_int 0.1 (mi-spec-1, gfx950)". */
+/* Library and spec version, e.g. "libmamba_int 0.2 (mi-spec-2, gfx950)". */
 const char *mi_version(void);
 /* Message of the calling thread's last failed call ("" if none). */
 const char *mi_last_error_string(void);
@@ -146,30 +146,34 @@ mi_status mi_act_quant_f32(const float *x, int8_t *xq, float *x_scale, int m, in
  * F.linear + rescale, rational_bitnet.py:204-208, and launch_bitlinear).
  * a int8 [m, lda] (16-byte aligned, lda % 16 == 0); w_packed [n, k/4]
  * (4-byte aligned); out [m, ldo] of the kind's element type (ldo % 4 == 0);
- * k % 16 == 0.  shift in [0,30] for INT8/DECAY_MOD; res_shift in [0,62] for
- * RESIDUAL; x_scale [m] and w_scale for FLOAT.  row_stats (RESIDUAL only,
+ * k % 16 == 0.  shift in [0,30] for INT8/DECAY_MOD; res_shift in [0,62] and
+ * res_clamp >= 0 for RESIDUAL (res_clamp > 0 bounds acc to +-res_clamp before
+ * the residual factor: MambaIntegerBlockV2's out clamp to +-100,
+ * ssd_multihead.py:589-590; 0 = no bound, MambaIntegerBlock); x_scale [m]
+ * and w_scale for FLOAT.  row_stats (RESIDUAL only,
  * nullable, int64 [m,2], 8-byte aligned): the sum and the sum of squares of
  * each updated residual row are added to it with atomics (the caller zeroes
  * it), the row statistics of the next BitShiftNorm.  Chooses the MFMA tile
  * GEMM for m > 64 and the register-unpack GEMV path for m <= 64. */
 mi_status mi_bitlinear(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
                        int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                       const float *x_scale, float w_scale, int64_t *row_stats, void *stream);
+                       int32_t res_clamp, const float *x_scale, float w_scale, int64_t *row_stats,
+                       void *stream);
 /* Same contract, forcing the MFMA tile GEMM (prefill path). */
 mi_status mi_bitlinear_gemm(const int8_t *a, int lda, const uint8_t *w_packed, void *out,
                             int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
-                            int res_shift, const float *x_scale, float w_scale, int64_t *row_stats,
-                            void *stream);
+                            int res_shift, int32_t res_clamp, const float *x_scale, float w_scale,
+                            int64_t *row_stats, void *stream);
 /* Same contract, forcing the decode GEMV (m <= 64). */
 mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, void *out,
                             int ldo, int kind, int m, int n, int k, int shift, int32_t res_mult,
-                            int res_shift, const float *x_scale, float w_scale, int64_t *row_stats,
-                            void *stream);
+                            int res_shift, int32_t res_clamp, const float *x_scale, float w_scale,
+                            int64_t *row_stats, void *stream);
 /* The decode out_proj with the next norm's row statistics as per-block
  * partials instead of atomics (the residual update of BitLinear.forward +
  * MambaIntegerBlock.forward's residual add, mamba_integer_model.py:446-447,
  * for m <= 64 tokens): r[m, n] (int32, row stride ldr) is updated as by
- * mi_bitlinear_gemv RESIDUAL, and stats_parts int64 [m, ceil(n/16), 2]
+ * mi_bitlinear_gemv RESIDUAL (res_clamp as there), and stats_parts int64 [m, ceil(n/16), 2]
  * receives, for every row i and block b of 16 features, the sum and the sum
  * of squares of the updated r[i, 16b : 16b+16] (plain stores: no zeroing,
  * no atomics).  The norm entries below sum them (their stats_parts =
@@ -177,7 +181,7 @@ mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, v
  * aligned. */
 mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const uint8_t *w_packed, int32_t *r,
                                       int ldr, int m, int n, int k, int32_t res_mult, int res_shift,
-                                      int64_t *stats_parts, void *stream);
+                                      int32_t res_clamp, int64_t *stats_parts, void *stream);
 
 /* ---------------------------------------------------------- block ops */
 
@@ -409,7 +413,7 @@ mi_status mi_embed_argmax(const int64_t *keys, int nkeys, int64_t *ids, const in
                           int tokens, int dim, int vocab, int64_t *row_stats, int stats_layers, void *stream);
 
 /* ------------------------------------------------ whole decode step */
-/* Integer parameters of one layer (device pointers; spec mi-spec-1 layouts:
+/* Integer parameters of one layer (device pointers; spec mi-spec-2 layouts:
  * packed ternary matrices [rows][cols/4] bytes, 16-byte aligned).  The
  * dyadic-scan block uses w_dt, s_dt and base; the multi-head SSD block
  * (MI_BLOCK_SSD) w_x with the planar rows of spec rule 7.3 and decay_tab. */
@@ -430,6 +434,9 @@ typedef struct mi_layer_params {
     int32_t res_mult;
     int res_shift;
     const int32_t *decay_tab; /* SSD block: [n_heads][255] decay numerators */
+    int32_t out_clamp;        /* out_proj accumulator bound, the res_clamp of
+                                 mi_bitlinear RESIDUAL (SSD block: spec rule 7.9;
+                                 0 = none, the dyadic block) */
 } mi_layer_params;
 
 enum { MI_BLOCK_DYADIC = 0, MI_BLOCK_SSD = 1 };
@@ -488,8 +495,9 @@ mi_status mi_decode_step_static(const mi_model_params *params, int m, const int6
                                 int32_t *const *h_state, void *stream);
 
 /* ------------------------------------------------ integer checkpoints */
-/* The integer parameters above in a versioned file (format 1, spec
- * mi-spec-1): a 128-byte header (magic "MIQCKPT", format, spec string, dims,
+/* The integer parameters above in a versioned file (format 2, spec
+ * mi-spec-2; format-1 files of mi-spec-1, whose SSD layers have no out_proj
+ * clamp, are read as well): a 128-byte header (magic "MIQCKPT", format, spec string, dims,
  * logit_scale, table CRC, block type and heads), a table of named
  * little-endian tensors (dtype,
  * shape, offset, bytes, CRC-32), and the tensors at 256-byte aligned offsets:
@@ -506,7 +514,7 @@ typedef struct mi_checkpoint mi_checkpoint;
 
 typedef struct mi_checkpoint_info {
     int format_version;
-    char spec[16];             /* "mi-spec-1" */
+    char spec[16];             /* "mi-spec-2" (format 2) or "mi-spec-1" (format 1) */
     int d_model, n_layer, vocab_size, d_state, dt_rank;
     float logit_scale;         /* float logits = int32 logits * logit_scale (> 0) */
     size_t device_bytes;       /* bytes mi_checkpoint_upload fills */
@@ -515,8 +523,9 @@ typedef struct mi_checkpoint_info {
 
 /* Reads a checkpoint into host memory and validates it: magic, format,
  * spec, dims, table CRC, every tensor's dtype, shape (against the dims),
- * alignment and CRC-32, the ternary codes, the shifts (decay shift 15) and
- * decays in [0, 32000].  *out is NULL on failure; close with
+ * alignment and CRC-32, the ternary codes, the shifts (decay shift 15),
+ * decays in [0, 32000] and the out_proj clamps (>= 1 in format-2 SSD layers,
+ * 0 elsewhere).  *out is NULL on failure; close with
  * mi_checkpoint_close. */
 mi_status mi_checkpoint_open(const char *path, mi_checkpoint **out);
 mi_status mi_checkpoint_get_info(const mi_checkpoint *ck, mi_checkpoint_info *info);

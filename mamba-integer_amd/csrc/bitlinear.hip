@@ -1,4 +1,4 @@
-// BitLinear b1.58 on gfx950 (spec mi-spec-1, rules 2-3).
+// BitLinear b1.58 on gfx950 (spec mi-spec-2, rules 2-3).
 //
 // acc[m,n] = sum_k a[m,k] * W[n,k], a int8, W ternary in the 2-bit word layout
 // (16 weights per 32-bit word; (word >> 2j) & 0x03030303 holds 4 codes in byte
@@ -35,6 +35,7 @@ struct GemmArgs {
     int shift;
     int32_t res_mult;
     int res_shift;
+    int32_t res_clamp;   // RESIDUAL: |acc| bound before the residual factor (INT32_MAX: none)
     float w_scale;
     int64_t *row_stats;  // RESIDUAL: per-row (sum r, sum r^2) of the new residual, atomically added
     int64_t *stats_parts;  // RESIDUAL: [M][N/16][2] per-block (sum r, sum r^2), plain stores
@@ -43,6 +44,12 @@ struct GemmArgs {
 struct RowStat {
     int64_t s1, s2;
 };
+
+// The residual increment of one accumulator: rshr(clamp(acc, +-res_clamp) * res_mult, res_shift).
+__device__ __forceinline__ int64_t residual_delta(const GemmArgs &g, int32_t acc) {
+    const int32_t c = clamp32(acc, -g.res_clamp, g.res_clamp);
+    return rshr64((int64_t)c * g.res_mult, g.res_shift);
+}
 
 // Epilogue for 4 consecutive features n..n+3 of token m (n % 4 == 0).  For
 // RESIDUAL it returns the sum and the sum of squares of the new residual
@@ -75,7 +82,7 @@ __device__ __forceinline__ RowStat store4(const GemmArgs &g, int m, int n, v4i a
     } else if constexpr (KIND == MI_OUT_RESIDUAL) {
         int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + n;
         for (int r = 0; r < 4 && n + r < g.N; ++r) {
-            const int64_t delta = rshr64((int64_t)acc[r] * g.res_mult, g.res_shift);
+            const int64_t delta = residual_delta(g, acc[r]);
             const int32_t nv = (int32_t)clamp64((int64_t)o[r] + delta, -kResidualLimit, kResidualLimit);
             o[r] = nv;
             st.s1 += nv;
@@ -444,7 +451,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const ConvArgs &cv)
                         v4i nv;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int64_t delta = rshr64((int64_t)acc[i][j][r] * g.res_mult, g.res_shift);
+                            const int64_t delta = residual_delta(g, acc[i][j][r]);
                             nv[r] = (int32_t)clamp64((int64_t)old[jj][i][r] + delta, -kResidualLimit, kResidualLimit);
                         }
                         int32_t *o = ob + (int64_t)m * g.ldo + n;
@@ -692,7 +699,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs g) {
                 if (m < g.M && nf < g.N) {
                     int32_t *o = (int32_t *)g.out + (int64_t)m * g.ldo + nf;
                     for (int r = 0; r < 4 && nf + r < g.N; ++r) {
-                        const int64_t delta = rshr64((int64_t)v[r] * g.res_mult, g.res_shift);
+                        const int64_t delta = residual_delta(g, v[r]);
                         const int32_t nv = (int32_t)clamp64((int64_t)rpre[t][r] + delta, -kResidualLimit,
                                                             kResidualLimit);
                         o[r] = nv;
@@ -1001,7 +1008,7 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
         int32_t v = 0;
 #pragma unroll
         for (int w = 0; w < 8; ++w) v += red[w][lane][r];
-        const int64_t delta = rshr64((int64_t)v * g.res_mult, g.res_shift);
+        const int64_t delta = residual_delta(g, v);
         const int32_t nv = (int32_t)clamp64((int64_t)rold + delta, -kResidualLimit, kResidualLimit);
         if (eok) *rp = nv;
         s_new[l16][4 * lq + r] = eok ? nv : 0;
@@ -1080,7 +1087,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const float *x, int8_t *
 
 // ------------------------------------------------------------ dispatch
 mi_status validate(const char *fn, const int8_t *a, int lda, const uint8_t *w, void *out, int ldo, int kind, int m,
-                   int n, int k, int shift, int res_shift, const float *x_scale) {
+                   int n, int k, int shift, int res_shift, const float *x_scale, int32_t res_clamp = 0) {
     MI_REQUIRE(m >= 0 && n >= 0 && k >= 0, MI_ERR_BAD_DIM, "%s: negative size (m=%d n=%d k=%d)", fn, m, n, k);
     MI_REQUIRE(k % 16 == 0, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 16", fn, k);
     MI_REQUIRE(kind >= MI_OUT_INT32 && kind <= MI_OUT_FLOAT, MI_ERR_BAD_ARG, "%s: unknown output kind %d", fn, kind);
@@ -1096,16 +1103,20 @@ mi_status validate(const char *fn, const int8_t *a, int lda, const uint8_t *w, v
         MI_REQUIRE(shift >= 0 && shift <= 30, MI_ERR_BAD_ARG, "%s: shift=%d outside [0,30]", fn, shift);
     if (kind == MI_OUT_RESIDUAL)
         MI_REQUIRE(res_shift >= 0 && res_shift <= 62, MI_ERR_BAD_ARG, "%s: res_shift=%d outside [0,62]", fn, res_shift);
+    if (kind == MI_OUT_RESIDUAL)
+        MI_REQUIRE(res_clamp >= 0, MI_ERR_BAD_ARG, "%s: res_clamp=%d must be >= 0 (0: no clamp)", fn, res_clamp);
     if (kind == MI_OUT_FLOAT) MI_REQUIRE(x_scale, MI_ERR_NULL_POINTER, "%s: x_scale is required for FLOAT output", fn);
     return MI_OK;
 }
 
 GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ldo, int m, int n, int k, int shift,
-                   int32_t res_mult, int res_shift, const float *x_scale, float w_scale, int64_t *row_stats) {
+                   int32_t res_mult, int res_shift, const float *x_scale, float w_scale, int64_t *row_stats,
+                   int32_t res_clamp = 0) {
     GemmArgs g{};
     g.a = a; g.w = reinterpret_cast<const uint32_t *>(w); g.out = out; g.x_scale = x_scale;
     g.lda = lda; g.ldo = ldo; g.M = m; g.N = n; g.K = k; g.kw = k / 16;
     g.shift = shift; g.res_mult = res_mult; g.res_shift = res_shift; g.w_scale = w_scale; g.row_stats = row_stats;
+    g.res_clamp = res_clamp > 0 ? res_clamp : INT32_MAX;
     return g;
 }
 
@@ -1206,16 +1217,17 @@ enum class Path { kAuto, kGemm, kGemv };
 
 mi_status bitlinear_impl(const char *fn, Path path, const int8_t *a, int lda, const uint8_t *w, void *out, int ldo,
                          int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                         const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
+                         int32_t res_clamp, const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
     clear_error();
-    mi_status st = validate(fn, a, lda, w, out, ldo, kind, m, n, k, shift, res_shift, x_scale);
+    mi_status st = validate(fn, a, lda, w, out, ldo, kind, m, n, k, shift, res_shift, x_scale, res_clamp);
     if (st != MI_OK || (int64_t)m * n == 0) return st;
     if (path == Path::kGemv) MI_REQUIRE(m <= 64, MI_ERR_BAD_DIM, "%s: the GEMV path takes m <= 64 (m=%d)", fn, m);
     if (row_stats) {
         MI_REQUIRE(kind == MI_OUT_RESIDUAL, MI_ERR_BAD_ARG, "%s: row_stats only with RESIDUAL output", fn);
         MI_REQUIRE(aligned(row_stats, 8), MI_ERR_BAD_ALIGNMENT, "%s: row_stats must be 8-byte aligned", fn);
     }
-    const GemmArgs g = make_args(a, lda, w, out, ldo, m, n, k, shift, res_mult, res_shift, x_scale, w_scale, row_stats);
+    const GemmArgs g =
+        make_args(a, lda, w, out, ldo, m, n, k, shift, res_mult, res_shift, x_scale, w_scale, row_stats, res_clamp);
     const bool gemv = path == Path::kGemv || (path == Path::kAuto && m <= 64);
     hipError_t e = gemv ? launch_gemv(kind, g, as_stream(stream)) : launch_gemm(kind, g, as_stream(stream));
     if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
@@ -1229,38 +1241,42 @@ using namespace mi;
 
 extern "C" mi_status mi_bitlinear(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo, int kind,
                                   int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                                  const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
+                                  int32_t res_clamp, const float *x_scale, float w_scale, int64_t *row_stats,
+                                  void *stream) {
     return bitlinear_impl("mi_bitlinear", Path::kAuto, a, lda, w_packed, out, ldo, kind, m, n, k, shift, res_mult,
-                          res_shift, x_scale, w_scale, row_stats, stream);
+                          res_shift, res_clamp, x_scale, w_scale, row_stats, stream);
 }
 
 extern "C" mi_status mi_bitlinear_gemm(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
                                        int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                                       const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
+                                       int32_t res_clamp, const float *x_scale, float w_scale, int64_t *row_stats,
+                                       void *stream) {
     return bitlinear_impl("mi_bitlinear_gemm", Path::kGemm, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
-                          res_mult, res_shift, x_scale, w_scale, row_stats, stream);
+                          res_mult, res_shift, res_clamp, x_scale, w_scale, row_stats, stream);
 }
 
 extern "C" mi_status mi_bitlinear_gemv(const int8_t *a, int lda, const uint8_t *w_packed, void *out, int ldo,
                                        int kind, int m, int n, int k, int shift, int32_t res_mult, int res_shift,
-                                       const float *x_scale, float w_scale, int64_t *row_stats, void *stream) {
+                                       int32_t res_clamp, const float *x_scale, float w_scale, int64_t *row_stats,
+                                       void *stream) {
     return bitlinear_impl("mi_bitlinear_gemv", Path::kGemv, a, lda, w_packed, out, ldo, kind, m, n, k, shift,
-                          res_mult, res_shift, x_scale, w_scale, row_stats, stream);
+                          res_mult, res_shift, res_clamp, x_scale, w_scale, row_stats, stream);
 }
 
 extern "C" mi_status mi_bitlinear_residual_parts(const int8_t *a, int lda, const uint8_t *w_packed, int32_t *r,
                                                  int ldr, int m, int n, int k, int32_t res_mult, int res_shift,
-                                                 int64_t *stats_parts, void *stream) {
+                                                 int32_t res_clamp, int64_t *stats_parts, void *stream) {
     const char *fn = "mi_bitlinear_residual_parts";
     clear_error();
-    mi_status st = validate(fn, a, lda, w_packed, r, ldr, MI_OUT_RESIDUAL, m, n, k, 0, res_shift, nullptr);
+    mi_status st = validate(fn, a, lda, w_packed, r, ldr, MI_OUT_RESIDUAL, m, n, k, 0, res_shift, nullptr, res_clamp);
     if (st != MI_OK || (int64_t)m * n == 0) return st;
     MI_REQUIRE(m <= 64, MI_ERR_BAD_DIM, "%s: m=%d must be <= 64", fn, m);
     MI_REQUIRE(k % 64 == 0, MI_ERR_BAD_DIM, "%s: k=%d must be a multiple of 64", fn, k);
     MI_REQUIRE(stats_parts, MI_ERR_NULL_POINTER, "%s: stats_parts is required", fn);
     MI_REQUIRE(aligned(w_packed, 16) && aligned(stats_parts, 16), MI_ERR_BAD_ALIGNMENT,
                "%s: w_packed and stats_parts must be 16-byte aligned", fn);
-    GemmArgs g = make_args(a, lda, w_packed, r, ldr, m, n, k, 0, res_mult, res_shift, nullptr, 0.0f, nullptr);
+    GemmArgs g =
+        make_args(a, lda, w_packed, r, ldr, m, n, k, 0, res_mult, res_shift, nullptr, 0.0f, nullptr, res_clamp);
     g.stats_parts = stats_parts;
     if (m > 16)
         hipLaunchKernelGGL(resid_gemv16_kernel<true>, dim3((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16)),

@@ -1,5 +1,5 @@
 // Elementwise and row stages of the integer Mamba block on gfx950 (spec
-// mi-spec-1, rules 4.1, 4.3-4.4 and the model's embedding / greedy pick).
+// mi-spec-2, rules 4.1, 4.3-4.4 and the model's embedding / greedy pick).
 #include "mi_mfma.hpp"
 
 namespace mi {

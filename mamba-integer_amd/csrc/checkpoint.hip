@@ -1,5 +1,8 @@
-// Integer checkpoint, format 1 (spec mi-spec-1): reader, validation and
-// upload into one caller-owned device buffer.
+// Integer checkpoint, formats 1 (spec mi-spec-1) and 2 (spec mi-spec-2):
+// reader, validation and upload into one caller-owned device buffer.  The
+// two formats share one layout; format 2 gives the last per-layer scalar a
+// meaning (the SSD block's out_proj accumulator bound, spec rule 7.9), which
+// format 1 holds as zero (no bound, as mi-spec-1 computes).
 //
 // The reference's inference export (scripts/export_int8.py:50-135) writes a
 // bare 0xDAD1C stream (float embedding, conv and gains, one int8 byte per
@@ -12,8 +15,8 @@
 // reports an mi_status, and the upload fills a buffer the caller allocated.
 //
 // File layout (little-endian):
-//   header, 128 bytes: magic "MIQCKPT\0", u32 format (1), u32 header bytes
-//     (128), char spec[16] ("mi-spec-1"), u32 d_model, n_layer, vocab_size,
+//   header, 128 bytes: magic "MIQCKPT\0", u32 format (1 or 2), u32 header
+//     bytes (128), char spec[16] ("mi-spec-1" / "mi-spec-2"), u32 d_model, n_layer, vocab_size,
 //     d_state, dt_rank, u32 tensor count, u64 table offset, u64 file bytes,
 //     f32 logit_scale, u32 CRC-32 of the table, u32 block (0 dyadic scan,
 //     1 multi-head SSD), u32 n_heads, u32 d_head, zeros;
@@ -47,9 +50,9 @@ namespace mi {
 namespace {
 
 constexpr char kMagic[8] = {'M', 'I', 'Q', 'C', 'K', 'P', 'T', '\0'};
-constexpr uint32_t kFormat = 1;
+constexpr uint32_t kFormatMin = 1, kFormatMax = 2;
 constexpr size_t kHeaderBytes = 128, kEntryBytes = 96, kDataAlign = 256;
-constexpr int kScalars = 8;  // s_in, s_x, s_dt, decay_shift, s_y, res_mult, res_shift, 0
+constexpr int kScalars = 8;  // s_in, s_x, s_dt, decay_shift, s_y, res_mult, res_shift, out_clamp
 enum { kI8 = 1, kU8 = 2, kI16 = 3, kI32 = 4, kF32 = 5 };
 
 uint32_t crc32_ieee(const uint8_t *p, size_t n) {
@@ -140,16 +143,17 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
     MI_REQUIRE(memcmp(b.data(), kMagic, 8) == 0, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: not an integer checkpoint "
                "(bad magic)", path);
     const uint32_t format = rd<uint32_t>(&b[8]), hbytes = rd<uint32_t>(&b[12]);
-    MI_REQUIRE(format == kFormat, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: format %u (this library reads %u)", path,
-               format, kFormat);
+    MI_REQUIRE(format >= kFormatMin && format <= kFormatMax, MI_ERR_BAD_ARG,
+               "mi_checkpoint_open: %s: format %u (this library reads %u to %u)", path, format, kFormatMin, kFormatMax);
     MI_REQUIRE(hbytes == kHeaderBytes, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: header of %u bytes", path, hbytes);
     mi_checkpoint_info &in = ck.info;
     memset(&in, 0, sizeof(in));
     in.format_version = (int)format;
     memcpy(in.spec, &b[16], 16);
     in.spec[15] = '\0';
-    MI_REQUIRE(strcmp(in.spec, "mi-spec-1") == 0, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: spec '%s' (this library "
-               "computes mi-spec-1)", path, in.spec);
+    const char *want_spec = format == 1 ? "mi-spec-1" : "mi-spec-2";
+    MI_REQUIRE(strcmp(in.spec, want_spec) == 0, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: spec '%s' in a format-%u "
+               "file (expected %s)", path, in.spec, format, want_spec);
     const uint32_t dm = rd<uint32_t>(&b[32]), nl = rd<uint32_t>(&b[36]), vs = rd<uint32_t>(&b[40]),
                    ds = rd<uint32_t>(&b[44]), dr = rd<uint32_t>(&b[48]), nt = rd<uint32_t>(&b[52]);
     const uint64_t toff = rd<uint64_t>(&b[56]), fbytes = rd<uint64_t>(&b[64]);
@@ -230,7 +234,7 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
         dev += up256((size_t)t.nbytes);
     }
     MI_REQUIRE(ck.tensors.size() == expected(in).size(), MI_ERR_BAD_ARG,
-               "mi_checkpoint_open: %s: %zu tensors, format 1 holds %zu", path, ck.tensors.size(),
+               "mi_checkpoint_open: %s: %zu tensors, the format holds %zu", path, ck.tensors.size(),
                expected(in).size());
     in.device_bytes = dev;
 
@@ -244,6 +248,14 @@ mi_status parse(mi_checkpoint &ck, const char *path) {
                    MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: layer %u: a requant shift is outside its range", path, l);
         MI_REQUIRE(s[3] == 15, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: layer %u: decay shift %d (the scan kernels "
                    "take 15)", path, l, s[3]);
+        // out_clamp: zero in format 1 and in dyadic-block layers (no bound);
+        // a format-2 SSD layer carries its bound, >= 1
+        if (format == 1 || !ssd)
+            MI_REQUIRE(s[7] == 0, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: layer %u: out_clamp %d where the format "
+                       "or block has none", path, l, s[7]);
+        else
+            MI_REQUIRE(s[7] >= 1, MI_ERR_BAD_ARG, "mi_checkpoint_open: %s: layer %u: out_clamp %d must be >= 1",
+                       path, l, s[7]);
         // decay numerators: clamp(base + dm) of the dyadic block needs base in
         // [0, 32000]; the SSD block's table entries are used as they are
         const int32_t hi = ssd ? 32768 : 32000;
@@ -359,6 +371,7 @@ extern "C" mi_status mi_checkpoint_upload(const mi_checkpoint *ck, void *device,
         ly.w_out = static_cast<const uint8_t *>(where[p + "w_out"]);
         ly.res_mult = s[5];
         ly.res_shift = s[6];
+        ly.out_clamp = s[7];
     }
     return MI_OK;
 }

@@ -26,6 +26,6 @@ mi_status check_launch(const char *what) {
 
 }  // namespace mi
 
-extern "C" const char *mi_version(void) { return "libmamba_int 0.1 (mi-spec-1, gfx950)"; }
+extern "C" const char *mi_version(void) { return "libmamba_int 0.2 (mi-spec-2, gfx950)"; }
 
 extern "C" const char *mi_last_error_string(void) { return mi::g_error; }

@@ -1,5 +1,5 @@
 // Fused decode-step stages of the integer Mamba block on gfx950 (spec
-// mi-spec-1, rules 4.1-4.12 at one token per sequence).
+// mi-spec-2, rules 4.1-4.12 at one token per sequence).
 //
 // A decode step at small batch is bound by the chain of dependent kernels,
 // not by bytes (the packed weights of the d768 x 24 model are 28.6 MB), so a

@@ -212,11 +212,11 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
             const mi_layer_params &ly = p.layers[l];
             MI_STEP(mi_norm_v2_in_proj_conv(r, l == 0 ? stats : parts, l == 0 ? 1 : P, ly.gamma, ly.w_in, ly.s_in,
                                             ly.conv_w, ly.conv_b, conv_state[l], xs, xz, m, d, D, stream));
-            MI_STEP(mi_bitlinear_gemv(xs, D, ly.w_x, xp, W, MI_OUT_INT8, m, W, D, ly.s_x, 0, 0, nullptr, 0.0f,
+            MI_STEP(mi_bitlinear_gemv(xs, D, ly.w_x, xp, W, MI_OUT_INT8, m, W, D, ly.s_x, 0, 0, 0, nullptr, 0.0f,
                                       nullptr, stream));
             MI_STEP(mi_ssd_block_scan(xs, xp, W, xz, 2 * D, D, ly.decay_tab, p.n_heads, ly.s_y, yo, h_state[l],
                                       h_state[l], m, 1, D, N, stream));
-            MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
+            MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, ly.out_clamp, parts,
                                                 stream));
         }
         MI_STEP(mi_norm_bitlinear_argmax(r, parts, P, p.gamma_f, p.w_head, logits, ld_logits, keys, m, p.vocab_size,
@@ -236,7 +236,7 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
             const mi_layer_params &ly = p.layers[l];
             if (l == 0) MI_STEP(mi_bitshift_norm(r, ly.gamma, a, m, d, stats, stream));
             else MI_STEP(mi_bitshift_norm_parts(r, ly.gamma, a, m, d, parts, P, 0, stream));
-            MI_STEP(mi_bitlinear_gemv(a, d, ly.w_in, xz, 2 * D, MI_OUT_INT8, m, 2 * D, d, ly.s_in, 0, 0, nullptr, 0.0f,
+            MI_STEP(mi_bitlinear_gemv(a, d, ly.w_in, xz, 2 * D, MI_OUT_INT8, m, 2 * D, d, ly.s_in, 0, 0, 0, nullptr, 0.0f,
                                       nullptr, stream));
             if (quarters(p)) {
                 MI_STEP(mi_conv_step_xpart(xz, 2 * D, ly.conv_w, ly.conv_b, conv_state[l], xs, ly.w_x, nx, xq, m, D,
@@ -249,11 +249,11 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
                 MI_STEP(mi_dt_scan_step(xp, W, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base, ly.decay_shift, ly.s_y,
                                         h_state[l], yo, m, D, N, stream));
             }
-            MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
+            MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, ly.out_clamp, parts,
                                                 stream));
         }
         MI_STEP(mi_bitshift_norm_parts(r, p.gamma_f, a, m, d, parts, P, 0, stream));
-        MI_STEP(mi_bitlinear_gemv(a, d, p.w_head, lg, ldl, MI_OUT_INT32, m, p.vocab_size, d, 0, 0, 0, nullptr, 0.0f,
+        MI_STEP(mi_bitlinear_gemv(a, d, p.w_head, lg, ldl, MI_OUT_INT32, m, p.vocab_size, d, 0, 0, 0, 0, nullptr, 0.0f,
                                   nullptr, stream));
         MI_STEP(mi_argmax_i32(lg, ldl, next_ids, m, p.vocab_size, stream));
         if (logits) {
@@ -274,7 +274,7 @@ extern "C" mi_status mi_decode_step(const mi_model_params *params, int m, const 
                                            stream));
         MI_STEP(mi_xpart_dt_scan_step(xpart, D / 16, ly.s_x, R, ly.w_dt, ly.s_dt, xs, xz, 2 * D, D, ly.base,
                                       ly.decay_shift, ly.s_y, h_state[l], yo, m, D, N, stream));
-        MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, parts,
+        MI_STEP(mi_bitlinear_residual_parts(yo, D, ly.w_out, r, d, m, d, D, ly.res_mult, ly.res_shift, ly.out_clamp, parts,
                                             stream));
     }
     MI_STEP(mi_norm_bitlinear_argmax(r, parts, P, p.gamma_f, p.w_head, logits, ld_logits, keys, m, p.vocab_size, d,

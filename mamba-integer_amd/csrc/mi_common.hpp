@@ -1,5 +1,5 @@
 // Shared helpers of libmamba_int: status reporting, argument checks and the
-// integer rounding/saturation primitives of spec mi-spec-1.
+// integer rounding/saturation primitives of spec mi-spec-2.
 #pragma once
 
 #include <hip/hip_runtime.h>

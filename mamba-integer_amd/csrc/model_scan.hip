@@ -1,4 +1,4 @@
-// Fused model scan for prefill on gfx950 (spec mi-spec-1, rules 4.7-4.11):
+// Fused model scan for prefill on gfx950 (spec mi-spec-2, rules 4.7-4.11):
 // decay from base + dm, dt from dm, input xs*dt (x) B, the exact floor
 // recurrence, y = C.h, the gate by z and the requant of the out_proj input.
 //

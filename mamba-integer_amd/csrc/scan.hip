@@ -1,4 +1,4 @@
-// Dyadic selective scans for gfx950 (spec mi-spec-1, rule 1 and 4.7-4.11).
+// Dyadic selective scans for gfx950 (spec mi-spec-2, rule 1 and 4.7-4.11).
 //
 // The recurrence h_t = sat32(floor(h_{t-1} * n / 2^k) + u_t) is not
 // associative (the floor does not compose), so exact parallelism comes only

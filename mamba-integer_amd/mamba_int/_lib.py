@@ -31,10 +31,10 @@ SIGNATURES = {
     "mi_ssd_chunked_scan": [P, P, P, P, I, P, P, P, P, I, I, I, I, I, I, P],
     "mi_pack_ternary": [P, P, I, I, P],
     "mi_act_quant_f32": [P, P, P, I, I, P],
-    "mi_bitlinear": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
-    "mi_bitlinear_gemm": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
-    "mi_bitlinear_gemv": [P, I, P, P, I, I, I, I, I, I, I32, I, P, F, P, P],
-    "mi_bitlinear_residual_parts": [P, I, P, P, I, I, I, I, I32, I, P, P],
+    "mi_bitlinear": [P, I, P, P, I, I, I, I, I, I, I32, I, I32, P, F, P, P],
+    "mi_bitlinear_gemm": [P, I, P, P, I, I, I, I, I, I, I32, I, I32, P, F, P, P],
+    "mi_bitlinear_gemv": [P, I, P, P, I, I, I, I, I, I, I32, I, I32, P, F, P, P],
+    "mi_bitlinear_residual_parts": [P, I, P, P, I, I, I, I, I32, I, I32, P, P],
     "mi_bitshift_norm": [P, P, P, I, I, P, P],
     "mi_embed": [P, P, P, I, I, I, P, I, P],
     "mi_conv_squareplus": [P, I, P, P, P, P, P, I, I, I, P],

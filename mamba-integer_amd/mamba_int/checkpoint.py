@@ -1,17 +1,18 @@
-"""Integer checkpoints (format 1, spec mi-spec-1) and the converter from the
-reference's float checkpoints.
+"""Integer checkpoints (format 2, spec mi-spec-2; format-1 files of spec
+mi-spec-1 are read too) and the converter from the reference's float
+checkpoints.
 
 The reference exports inference weights as a bare 0xDAD1C stream
 (``scripts/export_int8.py:50-135``) and reads them back with a loader that
-stops after the conv taps (``src/cpp_engine/mamba_infer.cpp:46-118``).  A
-format-1 file instead holds the integer parameters of ``ModelParams`` as a
+stops after the conv taps (``src/cpp_engine/mamba_infer.cpp:46-118``).  An
+integer checkpoint instead holds the integer parameters of ``ModelParams`` as a
 table of named, typed, shaped tensors, each at a 256-byte aligned offset with
 its CRC-32, so the native loader (``mi_checkpoint_open`` /
 ``mi_checkpoint_upload``) can validate it and copy it into one device buffer
 with the kernels' alignment.  Layout (little-endian):
 
-- header, 128 bytes: magic ``MIQCKPT\\0``, u32 format 1, u32 header bytes 128,
-  char spec[16] ``mi-spec-1``, u32 d_model, n_layer, vocab_size, d_state,
+- header, 128 bytes: magic ``MIQCKPT\\0``, u32 format 2, u32 header bytes 128,
+  char spec[16] ``mi-spec-2``, u32 d_model, n_layer, vocab_size, d_state,
   dt_rank, u32 tensor count, u64 table offset, u64 file bytes, f32
   logit_scale, u32 CRC-32 of the table, u32 block (0 dyadic scan, 1
   multi-head SSD), u32 n_heads, u32 d_head, zeros;
@@ -19,14 +20,16 @@ with the kernels' alignment.  Layout (little-endian):
   4 i32, 5 f32), u32 ndim, u32 shape[4], u64 offset, u64 bytes, u32 CRC-32,
   u32 zero;
 - the tensors: ``emb``, ``gamma_f``, ``w_head``, ``layer_scalars`` (int32
-  [n_layer, 8]: s_in, s_x, s_dt, decay_shift, s_y, res_mult, res_shift, 0) and
+  [n_layer, 8]: s_in, s_x, s_dt, decay_shift, s_y, res_mult, res_shift,
+  out_clamp; out_clamp is the SSD block's out_proj bound, >= 1, and 0 in
+  dyadic-block layers and in every layer of a format-1 file) and
   per layer ``layers.{i}.{gamma, w_in, conv_w, conv_b, w_x, w_dt, base,
   w_out}`` (the SSD block: ``decay_tab`` in place of ``w_dt`` and ``base``).
 
 ``convert_state_dict`` maps a ``MambaIntegerModel`` float state dict (keys of
 ``mamba_integer_model.py:368-394,449-484``, ``ssd_multihead.py:481-522`` for
 the multi-head SSD block, and ``rational_bitnet.py:150-158``) onto these
-integers with the fixed-point formats of spec mi-spec-1 (sections 6 and 7 of
+integers with the fixed-point formats of spec mi-spec-2 (sections 6 and 7 of
 the spec list the rules).
 """
 from __future__ import annotations
@@ -39,12 +42,13 @@ from typing import Dict, List, Mapping, Tuple
 
 import numpy as np
 
-from .params import (DECAY_MAX, DECAY_SHIFT, LayerParams, ModelDims, ModelParams, SSDLayerParams, pack_ternary,
-                     ssd_decay_table)
+from .params import (DECAY_MAX, DECAY_SHIFT, LayerParams, ModelDims, ModelParams, SSDLayerParams, out_clamp_for,
+                     pack_ternary, ssd_decay_table)
 
 MAGIC = b"MIQCKPT\0"
-FORMAT = 1
-SPEC = "mi-spec-1"
+FORMAT = 2
+SPEC = "mi-spec-2"
+_SPEC_OF_FORMAT = {1: "mi-spec-1", 2: "mi-spec-2"}
 ALIGN = 256
 _HEADER = struct.Struct("<8sII16s5IIQQfIIII36x")
 _ENTRY = struct.Struct("<48sII4IQQII")
@@ -81,7 +85,10 @@ def _tensors(params: ModelParams) -> Dict[str, np.ndarray]:
     sc = np.zeros((params.dims.n_layer, 8), np.int32)
     ssd = params.dims.ssd
     for i, ly in enumerate(params.layers):
-        sc[i, :7] = (ly.s_in, ly.s_x, 0 if ssd else ly.s_dt, ly.k, ly.s_y, ly.res_mult, ly.res_shift)
+        sc[i] = (ly.s_in, ly.s_x, 0 if ssd else ly.s_dt, ly.k, ly.s_y, ly.res_mult, ly.res_shift,
+                 ly.out_clamp if ssd else 0)
+        if ssd and ly.out_clamp < 1:
+            raise CheckpointError(f"layer {i}: out_clamp {ly.out_clamp} must be >= 1")
         for k in (_SSD_KEYS if ssd else _LAYER_KEYS):
             t[f"layers.{i}.{k}"] = getattr(ly, k)
     t["layer_scalars"] = sc
@@ -89,7 +96,7 @@ def _tensors(params: ModelParams) -> Dict[str, np.ndarray]:
 
 
 def save(params: ModelParams, path: str, logit_scale: float) -> None:
-    """Writes ``params`` as a format-1 checkpoint; ``logit_scale`` (> 0) turns the
+    """Writes ``params`` as a format-2 checkpoint; ``logit_scale`` (> 0) turns the
     int32 logits into the float logits of the drop-in model."""
     dims = params.dims
     dims.validate()
@@ -129,8 +136,9 @@ def save(params: ModelParams, path: str, logit_scale: float) -> None:
 
 
 def load(path: str) -> Tuple[ModelParams, float]:
-    """Reads and validates a format-1 checkpoint (the checks of
-    ``mi_checkpoint_open``); returns the integer parameters and logit_scale."""
+    """Reads and validates a format-2 (or format-1) checkpoint (the checks of
+    ``mi_checkpoint_open``); returns the integer parameters and logit_scale.  A
+    format-1 file is an mi-spec-1 model: its SSD layers get out_clamp 0 (none)."""
     with open(path, "rb") as f:
         b = f.read()
     if len(b) < _HEADER.size:
@@ -139,11 +147,11 @@ def load(path: str) -> Tuple[ModelParams, float]:
      tcrc, block, n_heads, d_head) = _HEADER.unpack_from(b, 0)
     if magic != MAGIC:
         raise CheckpointError(f"{path}: not an integer checkpoint (bad magic)")
-    if fmt != FORMAT or hbytes != _HEADER.size:
-        raise CheckpointError(f"{path}: format {fmt} (this reader takes {FORMAT})")
+    if fmt not in _SPEC_OF_FORMAT or hbytes != _HEADER.size:
+        raise CheckpointError(f"{path}: format {fmt} (this reader takes {sorted(_SPEC_OF_FORMAT)})")
     spec = spec.rstrip(b"\0").decode(errors="replace")
-    if spec != SPEC:
-        raise CheckpointError(f"{path}: spec {spec!r} (this reader computes {SPEC})")
+    if spec != _SPEC_OF_FORMAT[fmt]:
+        raise CheckpointError(f"{path}: spec {spec!r} in a format-{fmt} file (expected {_SPEC_OF_FORMAT[fmt]})")
     if fbytes != len(b):
         raise CheckpointError(f"{path}: header says {fbytes} bytes, file has {len(b)}")
     if not logit_scale > 0:
@@ -192,11 +200,15 @@ def load(path: str) -> Tuple[ModelParams, float]:
         if dt == np.uint8 and np.any((a >> 1) & ~a & 0x55):
             raise CheckpointError(f"{path}: tensor {name!r} holds the invalid ternary code 0b10")
     if len(found) != len(want):
-        raise CheckpointError(f"{path}: {len(found)} tensors, format 1 holds {len(want)}")
+        raise CheckpointError(f"{path}: {len(found)} tensors, the format holds {len(want)}")
     sc = found["layer_scalars"]
     layers = []
     for i in range(n_layer):
-        s_in, s_x, s_dt, k, s_y, res_mult, res_shift, _ = (int(v) for v in sc[i])
+        s_in, s_x, s_dt, k, s_y, res_mult, res_shift, out_clamp = (int(v) for v in sc[i])
+        if (fmt == 1 or not dims.ssd) and out_clamp != 0:
+            raise CheckpointError(f"{path}: layer {i}: out_clamp {out_clamp} where the format or block has none")
+        if fmt == 2 and dims.ssd and out_clamp < 1:
+            raise CheckpointError(f"{path}: layer {i}: out_clamp {out_clamp} must be >= 1")
         if not all(0 <= v <= 30 for v in (s_in, s_x, s_dt, s_y)) or not 0 <= res_shift <= 62:
             raise CheckpointError(f"{path}: layer {i}: a requant shift is outside its range")
         if k != DECAY_SHIFT:
@@ -207,7 +219,8 @@ def load(path: str) -> Tuple[ModelParams, float]:
                 raise CheckpointError(f"{path}: layer {i}: decay numerator outside [0,32768]")
             layers.append(SSDLayerParams(gamma=g("gamma"), w_in=g("w_in"), s_in=s_in, conv_w=g("conv_w"),
                                          conv_b=g("conv_b"), w_x=g("w_x"), s_x=s_x, decay_tab=g("decay_tab"),
-                                         s_y=s_y, w_out=g("w_out"), res_mult=res_mult, res_shift=res_shift, k=k))
+                                         s_y=s_y, w_out=g("w_out"), res_mult=res_mult, res_shift=res_shift,
+                                         out_clamp=out_clamp, k=k))
             continue
         if g("base").min(initial=0) < 0 or g("base").max(initial=0) > DECAY_MAX:
             raise CheckpointError(f"{path}: layer {i}: decay numerator outside [0,{DECAY_MAX}]")
@@ -283,7 +296,7 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     block, ``mamba_integer_model.py:368-394,466-484``, or with ``use_ssd`` the
     multi-head SSD block, ``ssd_multihead.py:471-522``) from its float state dict.
 
-    Fixed-point formats of spec mi-spec-1: residual Q8, block activations Q4,
+    Fixed-point formats of spec mi-spec-2: residual Q8, block activations Q4,
     conv taps Q6, conv bias Q10, gains Q8, decay_mod integer.  Hence
     emb = sat8(round(E * 16)); gamma = round(gamma * step_size * 256); ternary
     weights by weight_quant_ternary with the scale folded into a power-of-2
@@ -292,7 +305,9 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     bias round(b * 1024); decays clamp(round(base_decay_nums), 0, 32000) with
     the decay_shifts buffer (all 15); s_y = 14 (B, C in Q4: y in Q18 -> Q4);
     logit_scale = lm_head scale / 16 / sqrt(d_model) (the reference's
-    output_scale, ``:483``)."""
+    output_scale, ``:483``); the SSD block's out_proj clamp to +-100
+    (``ssd_multihead.py:589-590``) as the accumulator bound floor(1600 / s)
+    of its out_proj weight scale s."""
     sd = _strip(state_dict)
     dims = ModelDims.from_config(config)
     dims.validate()
@@ -325,7 +340,7 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
         w_out, s_out_w = ternary(get(p + "out_proj.weight", (d, D)))
         if p + "dt_proj.bias" in sd:
             if float(get(p + "dt_proj.bias", (D,)).abs().max()) != 0.0:
-                raise CheckpointError(f"{p}dt_proj.bias is non-zero: the mi-spec-1 block has no dt bias")
+                raise CheckpointError(f"{p}dt_proj.bias is non-zero: the integer block has no dt bias")
         shifts = get(p + "decay_shifts", (D, N))
         if float(shifts.min()) != float(shifts.max()) or float(shifts.min()) != DECAY_SHIFT:
             raise CheckpointError(f"{p}decay_shifts: the scan kernels take a uniform shift of {DECAY_SHIFT}")
@@ -344,7 +359,7 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     params = ModelParams(dims=dims, emb=emb, layers=layers, gamma_f=gain("norm_f"), w_head=pack_ternary(w_head))
     extra = sorted(k for k in sd if k not in used and not k.endswith("dt_proj.bias"))
     if extra:
-        raise CheckpointError(f"state dict keys the mi-spec-1 model does not use: {extra[:5]}")
+        raise CheckpointError(f"state dict keys the integer model does not use: {extra[:5]}")
     return params, s_head / 16.0 / math.sqrt(d)
 
 
@@ -370,12 +385,12 @@ def _convert_ssd_layer(p: str, dims: ModelDims, get, gain) -> SSDLayerParams:
         conv_b=_fixed(get(p + "conv1d.bias", (D,)), 1024.0, -(2**31), 2**31 - 1, np.int32),
         w_x=pack_ternary(planar), s_x=requant_shift_for(s_x_w, 4, 4),
         decay_tab=ssd_decay_table(get(p + "A_log", (H,)).numpy().astype(np.float64)), s_y=14,
-        w_out=pack_ternary(w_out), res_mult=res_mult, res_shift=res_shift)
+        w_out=pack_ternary(w_out), res_mult=res_mult, res_shift=res_shift, out_clamp=out_clamp_for(s_out_w))
 
 
 def convert_reference_checkpoint(state_dict_path: str, config: dict, out_path: str) -> ModelParams:
     """Loads a reference ``torch.save`` state dict (tensors only:
-    ``weights_only=True``), converts it and writes a format-1 checkpoint."""
+    ``weights_only=True``), converts it and writes a format-2 checkpoint."""
     import torch
     sd = torch.load(state_dict_path, map_location="cpu", weights_only=True)
     if isinstance(sd, dict) and "model" in sd and isinstance(sd["model"], dict):

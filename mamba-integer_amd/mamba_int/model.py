@@ -37,6 +37,7 @@ class DeviceLayer:
     w_out: torch.Tensor
     res_mult: int
     res_shift: int
+    out_clamp: int = 0
     k: int = 15
     w_dt: Optional[torch.Tensor] = None
     s_dt: int = 0
@@ -132,7 +133,7 @@ class IntegerMambaRunner:
             common = dict(gamma=_dev(lp.gamma, dv), w_in=_dev(lp.w_in, dv), s_in=lp.s_in,
                           conv_w=_dev(lp.conv_w, dv), conv_b=_dev(lp.conv_b, dv), w_x=_dev(lp.w_x, dv),
                           s_x=lp.s_x, k=lp.k, s_y=lp.s_y, w_out=_dev(lp.w_out, dv), res_mult=lp.res_mult,
-                          res_shift=lp.res_shift)
+                          res_shift=lp.res_shift, out_clamp=lp.out_clamp)
             if self.dims.ssd:
                 self.layers.append(DeviceLayer(**common, decay_tab=_dev(lp.decay_tab, dv)))
             else:
@@ -198,10 +199,11 @@ class IntegerMambaRunner:
                                  ws.yo)
             if self._step_parts(ws):
                 # the next norm sums these per-16-feature statistics partials
-                ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)
+                ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts,
+                                             res_clamp=ly.out_clamp)
             else:
                 ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                              res_shift=ly.res_shift, row_stats=stats_out)
+                              res_shift=ly.res_shift, res_clamp=ly.out_clamp, row_stats=stats_out)
             return
         if not conv_done:
             ops.conv_squareplus(ws.xz, D, ly.conv_w, ly.conv_b, state_in=None if fresh else conv_state,
@@ -211,7 +213,7 @@ class IntegerMambaRunner:
             # one recurrent step per sequence (any batch): dt_proj + scan step + gate
             ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
             ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                          res_shift=ly.res_shift, row_stats=stats_out)
+                          res_shift=ly.res_shift, res_clamp=ly.out_clamp, row_stats=stats_out)
             return
         ops.bitlinear(ws.xp, ly.w_dt, ops.OUT_DECAY_MOD, D, k=R, shift=ly.s_dt, out=ws.dm,
                       lda=dims.xp_width, m=T)
@@ -222,7 +224,7 @@ class IntegerMambaRunner:
         if self.scan_timer is not None:
             self.scan_timer[1]()
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                      res_shift=ly.res_shift, row_stats=stats_out)
+                      res_shift=ly.res_shift, res_clamp=ly.out_clamp, row_stats=stats_out)
 
     def _layer_ssd(self, ly: DeviceLayer, ws: _Workspace, B: int, L: int, conv_state: torch.Tensor,
                    h_state: torch.Tensor, fresh: bool, stats_in: Optional[torch.Tensor],
@@ -246,7 +248,7 @@ class IntegerMambaRunner:
         if self.scan_timer is not None:
             self.scan_timer[1]()
         ops.bitlinear(ws.yo, ly.w_out, ops.OUT_RESIDUAL, d, out=ws.r, res_mult=ly.res_mult,
-                      res_shift=ly.res_shift, row_stats=stats_out)
+                      res_shift=ly.res_shift, res_clamp=ly.out_clamp, row_stats=stats_out)
 
     def _in_proj_conv_ok(self) -> bool:
         """mi_in_proj_conv's limits: d_inner a multiple of 128, d_model of 64."""
@@ -301,7 +303,8 @@ class IntegerMambaRunner:
             ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
             ops.ssd_block_scan(ws.xs, ws.xp, ws.xz, D, ly.decay_tab, dims.n_heads, dims.d_state, ly.s_y,
                                h_in=h_state, h_out=h_state, out=ws.yo, batch=ws.T)
-            ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)
+            ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts,
+                                             res_clamp=ly.out_clamp)
             return
         if ws.xpart is not None:
             # x_proj partials from the in_proj blocks, summed by the scan step
@@ -318,7 +321,8 @@ class IntegerMambaRunner:
             else:
                 ops.bitlinear(ws.xs, ly.w_x, ops.OUT_INT8, dims.xp_width, shift=ly.s_x, out=ws.xp)
                 ops.dt_scan_step(ws.xp, R, ly.w_dt, ly.s_dt, ws.xs, ws.xz, D, ly.base, ly.k, ly.s_y, h_state, ws.yo)
-        ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts)
+        ops.bitlinear_residual_parts(ws.yo, ly.w_out, ws.r, ly.res_mult, ly.res_shift, ws.parts,
+                                             res_clamp=ly.out_clamp)
 
     def _head(self, r_rows: torch.Tensor, stats: Optional[torch.Tensor],
               out: Optional[torch.Tensor] = None) -> torch.Tensor:

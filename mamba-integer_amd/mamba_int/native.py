@@ -24,7 +24,7 @@ class LayerParams(ctypes.Structure):
     _fields_ = [("gamma", _P), ("w_in", _P), ("s_in", _I), ("conv_w", _P), ("conv_b", _P),
                 ("w_x", _P), ("s_x", _I), ("w_dt", _P), ("s_dt", _I), ("base", _P),
                 ("decay_shift", _I), ("s_y", _I), ("w_out", _P), ("res_mult", ctypes.c_int32),
-                ("res_shift", _I), ("decay_tab", _P)]
+                ("res_shift", _I), ("decay_tab", _P), ("out_clamp", ctypes.c_int32)]
 
 
 class ModelParams(ctypes.Structure):
@@ -91,7 +91,7 @@ class NativeDecoder:
         for i, ly in enumerate(runner.layers):
             layers[i] = LayerParams(_ptr(ly.gamma), _ptr(ly.w_in), ly.s_in, _ptr(ly.conv_w), _ptr(ly.conv_b),
                                     _ptr(ly.w_x), ly.s_x, opt(ly.w_dt), ly.s_dt, opt(ly.base), ly.k, ly.s_y,
-                                    _ptr(ly.w_out), ly.res_mult, ly.res_shift, opt(ly.decay_tab))
+                                    _ptr(ly.w_out), ly.res_mult, ly.res_shift, opt(ly.decay_tab), ly.out_clamp)
         params = ModelParams(dims.d_model, dims.n_layer, dims.vocab_size, dims.d_state, dims.dt_rank,
                              _ptr(runner.emb), layers, _ptr(runner.gamma_f), _ptr(runner.w_head),
                              MI_BLOCK_SSD if dims.ssd else MI_BLOCK_DYADIC, dims.n_heads, dims.d_head)

@@ -138,9 +138,10 @@ def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Opt
               shift: int = 0, out: Optional[torch.Tensor] = None, res_mult: int = 0, res_shift: int = 0,
               x_scale: Optional[torch.Tensor] = None, w_scale: float = 0.0, path: str = "auto",
               lda: Optional[int] = None, m: Optional[int] = None,
-              row_stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+              row_stats: Optional[torch.Tensor] = None, res_clamp: int = 0) -> torch.Tensor:
     """out = kind(a[:, :k] @ W^T).  a int8 [m, lda] (a row-strided view is passed by
-    its storage with ``lda``); RESIDUAL updates ``out`` (int32 [m, n]) in place."""
+    its storage with ``lda``); RESIDUAL updates ``out`` (int32 [m, n]) in place, its
+    accumulator bounded to +-res_clamp first when res_clamp > 0."""
     if a.dtype != torch.int8 or not a.is_cuda:
         raise TypeError("a must be an int8 device tensor")
     if lda is None:
@@ -157,7 +158,7 @@ def bitlinear(a: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int, k: Opt
         out = torch.empty((m, n), dtype=_OUT_DTYPE[kind], device=a.device)
     _req(out, _OUT_DTYPE[kind], "out")
     _lib.call(_ENTRY[path], _ptr(a), lda, _ptr(w_packed), _ptr(out), out.shape[-1], kind, m, n, k,
-              shift, int(res_mult), res_shift, _ptr(_opt(x_scale, torch.float32, "x_scale")),
+              shift, int(res_mult), res_shift, int(res_clamp), _ptr(_opt(x_scale, torch.float32, "x_scale")),
               ctypes.c_float(w_scale), _ptr(_opt(row_stats, torch.int64, "row_stats")), _stream())
     return out
 
@@ -285,9 +286,10 @@ def _stats(row_stats: Optional[torch.Tensor], m: int):
 
 
 def bitlinear_residual_parts(a: torch.Tensor, w_packed: torch.Tensor, r: torch.Tensor, res_mult: int,
-                             res_shift: int, stats_parts: torch.Tensor) -> None:
-    """Decode out_proj: r (int32 [m, n], m <= 64) += rescaled a @ W^T, and stats_parts
-    (int64 [m, ceil(n/16), 2]) <- the per-16-feature (sum, sum of squares) of the new rows."""
+                             res_shift: int, stats_parts: torch.Tensor, res_clamp: int = 0) -> None:
+    """Decode out_proj: r (int32 [m, n], m <= 64) += rescaled a @ W^T (accumulator bounded to
+    +-res_clamp first when res_clamp > 0), and stats_parts (int64 [m, ceil(n/16), 2]) <- the
+    per-16-feature (sum, sum of squares) of the new rows."""
     _req(a, torch.int8, "a"); _req(w_packed, torch.uint8, "w_packed"); _req(r, torch.int32, "r")
     _req(stats_parts, torch.int64, "stats_parts")
     m, n = r.shape
@@ -295,7 +297,7 @@ def bitlinear_residual_parts(a: torch.Tensor, w_packed: torch.Tensor, r: torch.T
     if a.shape[0] != m or tuple(stats_parts.shape) != (m, (n + 15) // 16, 2):
         raise ValueError(f"a must be [{m}, k] and stats_parts [{m}, {(n + 15) // 16}, 2]")
     _lib.call("mi_bitlinear_residual_parts", _ptr(a), k, _ptr(w_packed), _ptr(r), n, m, n, k, int(res_mult),
-              res_shift, _ptr(stats_parts), _stream())
+              res_shift, int(res_clamp), _ptr(stats_parts), _stream())
 
 
 def norm_bitlinear(r: torch.Tensor, gamma: torch.Tensor, w_packed: torch.Tensor, kind: int, n: int,

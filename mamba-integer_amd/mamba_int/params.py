@@ -1,4 +1,4 @@
-"""Integer parameters of the integer Mamba model (spec mi-spec-1).
+"""Integer parameters of the integer Mamba model (spec mi-spec-2).
 
 The reference keeps float parameters and quantizes at run time
 (``rational_bitnet.py:185-188``); the integer path stores what that
@@ -141,6 +141,7 @@ class LayerParams:
     w_out: np.ndarray        # uint8 [d, D/4]
     res_mult: int
     res_shift: int
+    out_clamp: int = 0       # MambaIntegerBlock has no out_proj clamp
 
 
 @dataclass
@@ -158,7 +159,25 @@ class SSDLayerParams:
     w_out: np.ndarray        # uint8 [d, D/4]
     res_mult: int
     res_shift: int
+    out_clamp: int           # out_proj accumulator bound (spec rule 7.9), >= 1
     k: int = DECAY_SHIFT
+
+
+def out_clamp_for(w_scale: float) -> int:
+    """The SSD block's out_proj clamp (spec rule 7.9) for an out_proj weight scale:
+    out = acc * w_scale / 16 (Q4 input) lies in [-100, 100] (``ssd_multihead.py:589-590``)
+    exactly when |acc| <= floor(1600 / w_scale)."""
+    if not w_scale > 0:
+        raise ValueError("the out_proj weight scale must be positive")
+    return int(min(2**31 - 1, max(1, math.floor(1600.0 / w_scale))))
+
+
+def synthetic_out_clamp(n_layer: int, res_mult: int, res_shift: int) -> int:
+    """out_clamp_for the weight scale a synthetic layer's (res_mult, res_shift) stands
+    for under the reference's initial res_gate 1/sqrt(2 n_layer) (``ssd_multihead.py:518``):
+    res_mult / 2^res_shift = 16 * w_scale * res_gate."""
+    res_gate = 1.0 / math.sqrt(2.0 * n_layer)
+    return out_clamp_for(res_mult / 2.0**res_shift / (16.0 * res_gate))
 
 
 def ssd_decay_table(a_log) -> np.ndarray:
@@ -208,7 +227,8 @@ def init_random_params(dims: ModelDims, seed: int) -> ModelParams:
                 conv_b=rng.integers(-512, 513, size=D, dtype=np.int32),
                 w_x=pack_ternary(wx), s_x=requant_shift(D),
                 decay_tab=ssd_decay_table(rng.uniform(-2.3, -0.01, size=H)), s_y=14,
-                w_out=_ternary(rng, d, D), res_mult=4719, res_shift=16))
+                w_out=_ternary(rng, d, D), res_mult=4719, res_shift=16,
+                out_clamp=synthetic_out_clamp(dims.n_layer, 4719, 16)))
         return ModelParams(dims=dims, emb=emb, layers=layers, gamma_f=np.full(d, 256, dtype=np.int16),
                            w_head=_ternary(rng, V, d))
     for _ in range(dims.n_layer):

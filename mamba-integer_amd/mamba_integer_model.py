@@ -4,7 +4,7 @@ MI355X path.
 Same module names and constructor signatures as the reference
 (``MambaIntegerModel(config)``, ``MambaIntegerBlock(config, layer_idx)``,
 ``BitShiftNorm(dim)``, ``DyadicScanFunction.apply(u, decay_nums,
-decay_shifts)``), computing the integer rules of spec mi-spec-1 on the GPU:
+decay_shifts)``), computing the integer rules of spec mi-spec-2 on the GPU:
 
 - ``MambaIntegerModel.forward(input_ids)`` (``:486-495``) returns float logits
   ``fp32(logit_int) * logit_scale`` (a positive scale, so greedy argmax equals

@@ -6,7 +6,7 @@ reference's contract (``:382-422``): u and nums are [B, L, D], the shift is
 read from ``shifts`` (the reference takes its first element, ``:406-409``),
 and the result is ``(h, final_h, decay_to_end)`` with ``final_h`` and
 ``decay_to_end`` of shape [B, ceil(L / chunk_size), D].  The arithmetic is
-the integer recurrence of spec mi-spec-1:
+the integer recurrence of spec mi-spec-2:
 
 - ``h[t] = sat32(floor(h[t-1] * nums[t] / 2^shift) + u[t])`` on int32 u;
 - ``final_h`` is the state at the last step of each chunk;

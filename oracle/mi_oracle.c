@@ -5,7 +5,7 @@
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The
  * product (libmamba_int.so) never links, calls or falls back to it.
  *
- * Every function states the rule it follows (spec version mi-spec-1) and the
+ * Every function states the rule it follows (spec version mi-spec-2) and the
  * reference file:line it restates. The integer rules the reference leaves
  * undefined (saturation, rounding, packing, the integer norm, squareplus, dt
  * and gate) are frozen in SPEC.md of this repository; the code below is the
@@ -20,7 +20,7 @@
 #include <omp.h>
 #endif
 
-#define MO_VERSION "mi-spec-1 oracle 1"
+#define MO_VERSION "mi-spec-2 oracle 2"
 
 static int g_threads = 1;
 /* Mutation switch for the tests that show the pins catch a planted mistake.
@@ -35,7 +35,9 @@ int mo_get_threads(void) { return g_threads; }
 /* 1: scan rounds to nearest instead of flooring; 2: scan drops the input
  * term's sign (uses |u|); 3: y saturates partial sums per state instead of
  * once; 4: pack swaps the +1/-1 codes; 5: norm truncates the mean; 6: gemm
- * swaps weights 0 and 3 of every group of four. */
+ * swaps weights 0 and 3 of every group of four; 7 / 8: the float-compat scan
+ * rounds / floors x * 2^sb instead of truncating; 9: the float-compat scan's
+ * shift rounds instead of flooring. */
 void mo_set_mutation(int m) { g_mutation = m; }
 
 /* ---------------------------------------------------------------- helpers */
@@ -308,10 +310,11 @@ static int32_t dot_i8(const int8_t *a, const int8_t *w, int K) {
  * kind of spec rule 3.  out: int32/int8/float [M,N] or the int32 residual
  * [M,N] updated in place.  x_scale[M] and w_scale only for MO_OUT_FLOAT. */
 void mo_bitlinear_unpacked(const int8_t *a, const int8_t *wu, void *out, int kind, int M, int N, int K, int shift,
-                           int32_t res_mult, int res_shift, const float *x_scale, float w_scale);
+                           int32_t res_mult, int res_shift, int32_t res_clamp, const float *x_scale, float w_scale);
 
 void mo_bitlinear(const int8_t *a, const uint8_t *wp, void *out, int kind, int M, int N, int K,
-                  int shift, int32_t res_mult, int res_shift, const float *x_scale, float w_scale) {
+                  int shift, int32_t res_mult, int res_shift, int32_t res_clamp, const float *x_scale,
+                  float w_scale) {
     int8_t *wu = (int8_t *)malloc((size_t)N * K);
     mo_unpack_ternary(wp, wu, N, K);
     if (g_mutation == 6) {
@@ -322,14 +325,14 @@ void mo_bitlinear(const int8_t *a, const uint8_t *wp, void *out, int kind, int M
                 q[3] = t0;
             }
     }
-    mo_bitlinear_unpacked(a, wu, out, kind, M, N, K, shift, res_mult, res_shift, x_scale, w_scale);
+    mo_bitlinear_unpacked(a, wu, out, kind, M, N, K, shift, res_mult, res_shift, res_clamp, x_scale, w_scale);
     free(wu);
 }
 
 /* The same with the weights already unpacked to int8 [N][K] (a caller that
  * applies one matrix many times unpacks it once). */
 void mo_bitlinear_unpacked(const int8_t *a, const int8_t *wu, void *out, int kind, int M, int N, int K, int shift,
-                           int32_t res_mult, int res_shift, const float *x_scale, float w_scale) {
+                           int32_t res_mult, int res_shift, int32_t res_clamp, const float *x_scale, float w_scale) {
     /* (row, output) pairs are independent: one flat loop keeps every thread busy
      * at a single row (decode) as well as at many */
 #pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
@@ -342,8 +345,11 @@ void mo_bitlinear_unpacked(const int8_t *a, const int8_t *wu, void *out, int kin
             case MO_OUT_INT8: ((int8_t *)out)[o] = sat8(rshr(acc, shift)); break;
             case MO_OUT_DECAY_MOD: ((int8_t *)out)[o] = (int8_t)clamp64(rshr(acc, shift), -20, 20); break;
             case MO_OUT_RESIDUAL: {
+                /* res_clamp > 0: the out_proj output clamp of MambaIntegerBlockV2
+                 * (ssd_multihead.py:589-590, spec rule 7.9) on the accumulator */
                 int32_t *r = (int32_t *)out;
-                r[o] = satR((int64_t)r[o] + rshr((int64_t)acc * res_mult, res_shift));
+                int64_t v = res_clamp > 0 ? clamp64(acc, -res_clamp, res_clamp) : acc;
+                r[o] = satR((int64_t)r[o] + rshr(v * res_mult, res_shift));
                 break;
             }
             case MO_OUT_FLOAT: {

@@ -61,8 +61,9 @@ def lib() -> ctypes.CDLL:
         L.mo_dyadic_chunked_scan.argtypes = [P, P, I, I, P, P, P, P, I, I, I]
         L.mo_pack_ternary.argtypes = [P, P, I, I]
         L.mo_unpack_ternary.argtypes = [P, P, I, I]
-        L.mo_bitlinear.argtypes = [P, P, P, I, I, I, I, I, ctypes.c_int32, I, P, ctypes.c_float]
-        L.mo_bitlinear_unpacked.argtypes = [P, P, P, I, I, I, I, I, ctypes.c_int32, I, P, ctypes.c_float]
+        L.mo_bitlinear.argtypes = [P, P, P, I, I, I, I, I, ctypes.c_int32, I, ctypes.c_int32, P, ctypes.c_float]
+        L.mo_bitlinear_unpacked.argtypes = [P, P, P, I, I, I, I, I, ctypes.c_int32, I, ctypes.c_int32, P,
+                                            ctypes.c_float]
         L.mo_act_quant_f32.argtypes = [P, P, P, I, I]
         L.mo_bitshift_norm.argtypes = [P, P, P, I, I]
         L.mo_squareplus_q.argtypes = [ctypes.c_int32]
@@ -186,9 +187,10 @@ def unpack_ternary(p, K):
 
 
 def bitlinear(a, wp, kind, shift=0, residual=None, res_mult=0, res_shift=0,
-              x_scale=None, w_scale=0.0):
+              x_scale=None, w_scale=0.0, res_clamp=0):
     """BitLinear of int8 rows a [M,K] against packed ternary wp [N,K/4], or
-    against weights already unpacked to int8 [N,K] (same result)."""
+    against weights already unpacked to int8 [N,K] (same result).  res_clamp > 0
+    bounds the RESIDUAL accumulator to +-res_clamp first (spec rule 7.9)."""
     a = _c(a, np.int8)
     unpacked = wp.dtype == np.int8
     wp = _c(wp, np.int8 if unpacked else np.uint8)
@@ -204,7 +206,8 @@ def bitlinear(a, wp, kind, shift=0, residual=None, res_mult=0, res_shift=0,
         out = np.empty((M, N), np.float32)
     xs = None if x_scale is None else _c(x_scale, np.float32)
     fn = lib().mo_bitlinear_unpacked if unpacked else lib().mo_bitlinear
-    fn(_p(a), _p(wp), _p(out), kind, M, N, K, shift, int(res_mult), res_shift, _p(xs), ctypes.c_float(w_scale))
+    fn(_p(a), _p(wp), _p(out), kind, M, N, K, shift, int(res_mult), res_shift, int(res_clamp), _p(xs),
+       ctypes.c_float(w_scale))
     return out
 
 
@@ -312,7 +315,8 @@ def embed(ids, emb):
 #   "block_norm_v1"  the SSD block's norm uses the BitShiftNorm table
 #   "no_residual"    a block returns out * res_gate without the residual
 #   "conv_reset"     the recurrent step forgets the conv ring
-_WIRING = {"swap_xz", "norm_f_v2", "block_norm_v1", "no_residual", "conv_reset"}
+#   "no_out_clamp"   the SSD block's out_proj output is not clamped
+_WIRING = {"swap_xz", "norm_f_v2", "block_norm_v1", "no_residual", "conv_reset", "no_out_clamp"}
 _wiring_mutation: Optional[str] = None
 
 
@@ -392,7 +396,8 @@ class OracleModel:
         yo, h = ssd_v2_scan(xs, xp.reshape(B, L, -1), xz.reshape(B, L, 2 * D), D, lp.decay_tab, lp.s_y,
                             self.dims.n_heads, self.dims.d_state, None if state is None else state.h)
         r = bitlinear(yo.reshape(T, D), self._w(lp.w_out), OUT_RESIDUAL, residual=_residual(r),
-                      res_mult=lp.res_mult, res_shift=lp.res_shift)
+                      res_mult=lp.res_mult, res_shift=lp.res_shift,
+                      res_clamp=0 if _wiring_mutation == "no_out_clamp" else lp.out_clamp)
         return r, LayerState(conv=conv_state, h=h)
 
     def _run(self, ids, states: Optional[List[LayerState]], last_only: bool):

@@ -160,6 +160,7 @@ def norm_row(row, gamma, v2):
 NORM_K_SEEN = set()   # (table, shift) pairs met while writing a fixture
 NORM_F_K = set()      # shifts of the final norm
 RES_SAT = [0]         # residual updates that hit the saturation bound
+OUT_CLAMPED = [0]     # SSD out_proj accumulators beyond the out clamp
 
 
 def ternary_rows(a_rows, w):
@@ -275,6 +276,9 @@ def block_ssd(P, rows_seq):
                 yo[ch] = sat(rshr(yg, P["s_y"]), -127, 127)
         out_rows.append(yo)
     acc = ternary_rows(out_rows, P["w_out"])                                      # :588
+    c = P["out_clamp"]                                                            # :589-590 clamp(out, +-100)
+    OUT_CLAMPED[0] += sum(abs(a) > c for row in acc for a in row)
+    acc = [[sat(a, -c, c) for a in row] for row in acc]
     return residual_update(rows_seq, acc, P)                                      # :592
 
 
@@ -322,10 +326,11 @@ def decay_table(a_log):
     return tab
 
 
-def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
+def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14, out_clamps=(None, None)):
     """A 2-layer model of one block type, its all-position logits on two
     12-token prompts, and 8 greedy tokens per prompt.  res_shifts sets how
-    strongly each layer updates the residual."""
+    strongly each layer updates the residual; out_clamps the SSD block's
+    out_proj accumulator bound per layer."""
     rng = np.random.default_rng(seed)
     d, V, nl, L, n_new = 64, 96, 2, 12, 8
     if ssd:
@@ -354,6 +359,7 @@ def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
               "conv_b": rng.integers(-512, 513, size=D, dtype=np.int32), "w_out": tern(d, D)}
         sc = {"s_in": 3, "s_x": 3, "s_y": s_y, "res_mult": res_mults[i], "res_shift": res_shifts[i]}
         if ssd:
+            sc["out_clamp"] = out_clamps[i]
             wx = tern(W, D)
             wx[2 * H * N + H:] = 0
             la["w_x"] = wx
@@ -376,8 +382,10 @@ def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
     NORM_K_SEEN.clear()
     NORM_F_K.clear()
     RES_SAT[0] = 0
+    OUT_CLAMPED[0] = 0
     logits = np.array([model_logits(M, list(map(int, s))) for s in ids], np.int64)
     logits_fk = set(NORM_F_K)          # final-norm shifts of the stored logits
+    n_clamped = OUT_CLAMPED[0]         # out clamps that bind in the stored logits
     gen = np.array([model_generate(M, list(map(int, s)), n_new) for s in ids], np.int64)
     assert np.abs(logits).max() < 2**31
     # packed forms for the loaders (2-bit layout of the packing fixture)
@@ -387,24 +395,28 @@ def model_fixture(name, ssd, seed, res_shifts, res_mults=(4719, 5719), s_y=14):
     arrays["scalar_names"] = np.array(sorted(sc))
     np.savez_compressed(os.path.join(HERE, name), ids=ids, logits=logits.astype(np.int32), gen=gen, **arrays)
     print(name, "distinct greedy tokens:", sorted(set(gen.ravel().tolist())), "norm shifts (v2, k):",
-          sorted(NORM_K_SEEN), "final norm k of the logits:", sorted(logits_fk), "saturated residual updates:", RES_SAT[0])
-    return NORM_K_SEEN, logits_fk, RES_SAT[0]
+          sorted(NORM_K_SEEN), "final norm k of the logits:", sorted(logits_fk), "saturated residual updates:", RES_SAT[0],
+          "clamped out_proj accumulators:", n_clamped)
+    return NORM_K_SEEN, logits_fk, RES_SAT[0], n_clamped
 
 
 def main_models():
     # "small": varied greedy tokens that depend on the history; the final norm
     # meets the bottom threshold (k = -3), where the two norm tables differ
-    _, fk, _ = model_fixture("model_dyadic_small.npz", False, 7305, (11, 10))
+    _, fk, _, _ = model_fixture("model_dyadic_small.npz", False, 7305, (11, 10))
     assert -3 in fk
-    _, fk, _ = model_fixture("model_ssd_small.npz", True, 7302, (12, 11))
-    assert -3 in fk
+    # the SSD block's out_proj clamp (ssd_multihead.py:589-590) binds on a few
+    # percent of the accumulators in both SSD fixtures
+    _, fk, _, ncl = model_fixture("model_ssd_small.npz", True, 7302, (12, 11), out_clamps=(100, 120))
+    assert -3 in fk and ncl > 0
     # "wide": strong residual updates that saturate, and final-norm shifts past
     # the BitShiftNormV2 table's top (k = 7, 8); the greedy tokens of such a
     # random model settle on one id, so the logits carry this fixture
-    ks, fk, nsat = model_fixture("model_dyadic_wide.npz", False, 7301, (6, 0), (4719, 32767), 10)
+    ks, fk, nsat, _ = model_fixture("model_dyadic_wide.npz", False, 7301, (6, 0), (4719, 32767), 10)
     assert max(fk) >= 7 and nsat > 0
-    ks, fk, nsat = model_fixture("model_ssd_wide.npz", True, 7302, (8, 0), (4719, 32767), 10)
-    assert max(fk) >= 7 and nsat > 0
+    ks, fk, nsat, ncl = model_fixture("model_ssd_wide.npz", True, 7302, (8, 0), (4719, 32767), 10,
+                                      out_clamps=(900, 1000))
+    assert max(fk) >= 7 and nsat > 0 and ncl > 0
 
 
 def main():

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_names_spec_and_arch():
     from mamba_int import _lib
     v = _lib.version()
-    assert "mi-spec-1" in v and "gfx950" in v
+    assert "mi-spec-2" in v and "gfx950" in v
 
 
 def _fake(n=64):
@@ -46,20 +46,23 @@ def _fake(n=64):
     (("mi_dyadic_scan", None, None, None, None, 0, None, None, None, 1, 4, 16, 16, None), 4, "decay_shift"),
     (("mi_dyadic_scan", None, None, None, None, 15, None, None, None, 1, 4, 16, 16, None), 1, "required"),
     (("mi_ssd_chunked_scan", None, None, None, None, 15, None, None, None, None, 1, 8, 2, 16, 16, 0, None), 4, "chunk"),
-    (("mi_bitlinear", None, 16, None, None, 16, 1, 4, 4, 17, 0, 0, 0, None, ctypes.c_float(0), None, None), 2, "multiple of 16"),
-    (("mi_bitlinear", None, 16, None, None, 16, 9, 4, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 4, "kind"),
-    (("mi_bitlinear_gemv", "A16", 16, "W4", "O16", 16, 1, 100, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 2, "m <= 64"),
-    (("mi_bitlinear", "A16", 8, "W4", "O16", 16, 1, 4, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 3, "lda"),
-    (("mi_bitlinear", "A16", 16, "W4", "O16", 16, 4, 4, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None, None), 1, "x_scale"),
+    (("mi_bitlinear", None, 16, None, None, 16, 1, 4, 4, 17, 0, 0, 0, 0, None, ctypes.c_float(0), None, None), 2, "multiple of 16"),
+    (("mi_bitlinear", None, 16, None, None, 16, 9, 4, 4, 16, 0, 0, 0, 0, None, ctypes.c_float(0), None, None), 4, "kind"),
+    (("mi_bitlinear_gemv", "A16", 16, "W4", "O16", 16, 1, 100, 4, 16, 0, 0, 0, 0, None, ctypes.c_float(0), None, None), 2, "m <= 64"),
+    (("mi_bitlinear", "A16", 8, "W4", "O16", 16, 1, 4, 4, 16, 0, 0, 0, 0, None, ctypes.c_float(0), None, None), 3, "lda"),
+    (("mi_bitlinear", "A16", 16, "W4", "O16", 16, 4, 4, 4, 16, 0, 0, 0, 0, None, ctypes.c_float(0), None, None), 1, "x_scale"),
     (("mi_bitshift_norm", None, None, None, 4, 0, None, None), 2, "dim"),
     (("mi_conv_squareplus", None, 16, None, None, None, None, None, 1, 4, 18, None), 2, "multiple of 4"),
     (("mi_block_scan", None, None, None, 48, 16, None, 32, 16, None, 14, 13, None, None, None, 1, 4, 16, 16, None), 4, "decay_shift"),
     (("mi_norm_bitlinear", None, None, 1, None, None, None, 16, 1, 65, 16, 64, 0, None), 2, "m=65"),
     (("mi_norm_bitlinear", "A16", "A16", 0, "A16", "A16", "O16", 16, 1, 1, 16, 64, 0, None), 4, "stats_parts=0"),
     (("mi_norm_bitlinear", "A16", "W4", 2, "A16", "A16", "O16", 16, 1, 1, 16, 64, 0, None), 3, "row_stats"),
-    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 65, 16, 64, 1, 0, "A16", None), 2, "m=65"),
-    (("mi_bitlinear_residual_parts", "A16", 32, "A16", "O16", 16, 1, 16, 32, 1, 0, "A16", None), 2, "multiple of 64"),
-    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 1, 16, 64, 1, 0, None, None), 1, "stats_parts"),
+    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 65, 16, 64, 1, 0, 0, "A16", None), 2, "m=65"),
+    (("mi_bitlinear_residual_parts", "A16", 32, "A16", "O16", 16, 1, 16, 32, 1, 0, 0, "A16", None), 2, "multiple of 64"),
+    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 1, 16, 64, 1, 0, 0, None, None), 1, "stats_parts"),
+    (("mi_bitlinear", "A16", 16, "W4", "O16", 16, 3, 4, 4, 16, 0, 1, 0, -1, None, ctypes.c_float(0), None, None), 4,
+     "res_clamp"),
+    (("mi_bitlinear_residual_parts", "A16", 64, "A16", "O16", 16, 1, 16, 64, 1, 0, -5, "A16", None), 4, "res_clamp"),
     (("mi_dt_scan_step", None, 80, 40, None, 2, None, None, 32, 16, None, 15, 13, None, None, 1, 16, 16, None), 2, "dt_rank"),
     (("mi_argmax_i32", None, 10, None, 1, 20, None), 2, "ld"),
     (("mi_bitshift_norm_parts", None, None, None, 4, 6, None, 1, 0, None), 2, "multiple of 4"),
@@ -111,7 +114,7 @@ def test_argument_validation(call, status, needle):
 def test_zero_sizes_are_noops():
     from mamba_int import _lib
     assert _lib.raw("mi_dyadic_scan", None, None, None, None, 15, None, None, None, 0, 4, 16, 16, None) == 0
-    assert _lib.raw("mi_bitlinear", None, 16, None, None, 16, 1, 0, 4, 16, 0, 0, 0, None, ctypes.c_float(0), None,
+    assert _lib.raw("mi_bitlinear", None, 16, None, None, 16, 1, 0, 4, 16, 0, 0, 0, 0, None, ctypes.c_float(0), None,
                     None) == 0
     assert _lib.last_error() == ""
 

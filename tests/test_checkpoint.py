@@ -1,4 +1,4 @@
-"""Integer checkpoints (format 1) and the float state-dict converter, on the
+"""Integer checkpoints (format 2, and format-1 files) and the float state-dict converter, on the
 CPU: the Python writer/reader, the native reader (mi_checkpoint_open, no
 device calls), and the conversion rules pinned by closed forms and hand-made
 rounding ties (the reference's float model is not run here)."""
@@ -48,7 +48,7 @@ def test_round_trip_and_layout(tmp_path):
     b = path.read_bytes()
     magic, fmt, hb, spec, d, nl, v, ns, dr, nt, toff, fb, ls, tcrc, blk, nh, dh = ckpt._HEADER.unpack_from(b, 0)
     assert (blk, nh, dh) == (0, 0, 0)
-    assert (magic, fmt, hb, spec.rstrip(b"\0"), fb) == (b"MIQCKPT\0", 1, 128, b"mi-spec-1", len(b))
+    assert (magic, fmt, hb, spec.rstrip(b"\0"), fb) == (b"MIQCKPT\0", 2, 128, b"mi-spec-2", len(b))
     assert (d, nl, v, ns, dr) == (64, 2, 100, 16, 16) and nt == 4 + 8 * 2
     assert zlib.crc32(b[toff:toff + 96 * nt]) == tcrc
     for i in range(nt):
@@ -59,7 +59,7 @@ def test_round_trip_and_layout(tmp_path):
     ck = NativeCheckpoint(str(path))
     i = ck.info
     assert (i.format_version, i.spec, i.d_model, i.n_layer, i.vocab_size, i.d_state, i.dt_rank) == \
-        (1, b"mi-spec-1", 64, 2, 100, 16, 16)
+        (2, b"mi-spec-2", 64, 2, 100, 16, 16)
     assert i.logit_scale == np.float32(0.0125)
     assert i.device_bytes == sum(-(-a.nbytes // 256) * 256 for a in ckpt._tensors(p).values())
 
@@ -377,5 +377,69 @@ def test_convert_ssd_state_dict(tmp_path):
         assert not got[2 * H * N + H:].any()
         assert np.array_equal(ly.decay_tab, ssd_decay_table(sd[f"layers.{i}.A_log"].numpy()))
         assert np.array_equal(ly.gamma, np.round(sd[f"layers.{i}.norm.gamma"].numpy() * np.float32(1.25) * 256))
+        # out clamp +-100 (ssd_multihead.py:589-590) on out = acc * s / 16: |acc| <= floor(1600 / s)
+        wo = sd[f"layers.{i}.out_proj.weight"].numpy()
+        so = float(np.float32(np.abs(wo).astype(np.float64).mean()))
+        assert ly.out_clamp == math.floor(1600 / so) and (ly.out_clamp + 1) * so / 16 > 100 >= ly.out_clamp * so / 16
     ckpt.save(p, str(tmp_path / "c.miq"), 1.0)
     _equal(p, ckpt.load(str(tmp_path / "c.miq"))[0])
+
+
+def _as_format1(path):
+    """Rewrites a format-2 file as the format-1 file of the same model under
+    mi-spec-1 (out_clamp slots zero: the SSD block had no out_proj clamp)."""
+    _rewrite(path, "layer_scalars",
+             lambda raw: (np.frombuffer(raw, np.int32).reshape(-1, 8) * np.array([1] * 7 + [0], np.int32)).tobytes())
+    b = bytearray(path.read_bytes())
+    struct.pack_into("<I", b, 8, 1)
+    b[16:32] = b"mi-spec-1".ljust(16, b"\0")
+    path.write_bytes(bytes(b))
+
+
+@pytest.mark.parametrize("ssd", [False, True])
+def test_format1_files_are_read(tmp_path, ssd):
+    """A format-1 (mi-spec-1) file loads in both readers; its SSD layers get
+    out_clamp 0, the unclamped out_proj that spec computed."""
+    from mamba_int.native import NativeCheckpoint
+    p = init_random_params(ModelDims(**(SSD_DIMS if ssd else DIMS).__dict__), 9)
+    path = tmp_path / "f1.miq"
+    ckpt.save(p, str(path), 0.5)
+    _as_format1(path)
+    q, _ = ckpt.load(str(path))
+    for ly in p.layers:
+        ly.out_clamp = 0
+    _equal(p, q)
+    i = NativeCheckpoint(str(path)).info
+    assert (i.format_version, i.spec) == (1, b"mi-spec-1")
+
+
+@pytest.mark.parametrize("case,needle", [
+    ("ssd_zero", "must be >= 1"), ("dyadic_nonzero", "has none"), ("format1_nonzero", "has none"),
+    ("format1_spec2", "expected mi-spec-1"), ("format3", "format 3"),
+])
+def test_out_clamp_and_format_rules(tmp_path, case, needle):
+    """Format-2 SSD layers carry an out clamp >= 1; dyadic layers and format-1
+    files carry 0; the spec string matches the format."""
+    ssd = case in ("ssd_zero", "format1_nonzero")
+    p = init_random_params(ModelDims(**(SSD_DIMS if ssd else DIMS).__dict__), 9)
+    path = tmp_path / "c.miq"
+    ckpt.save(p, str(path), 0.5)
+    put = lambda v: lambda raw: (np.frombuffer(raw, np.int32).reshape(-1, 8) * np.array([1] * 7 + [0], np.int32)
+                                 + np.array([0] * 7 + [v], np.int32)).tobytes()  # noqa: E731
+    if case == "ssd_zero":
+        _rewrite(path, "layer_scalars", put(0))
+    elif case == "dyadic_nonzero":
+        _rewrite(path, "layer_scalars", put(500))
+    elif case == "format1_nonzero":
+        _as_format1(path)
+        _rewrite(path, "layer_scalars", put(500))
+    b = bytearray(path.read_bytes())
+    if case == "format1_spec2":
+        struct.pack_into("<I", b, 8, 1)
+    elif case == "format3":
+        struct.pack_into("<I", b, 8, 3)
+    path.write_bytes(bytes(b))
+    with pytest.raises(ckpt.CheckpointError, match=needle):
+        ckpt.load(str(path))
+    st, msg = _native_open(path)
+    assert st != 0 and needle in msg, msg

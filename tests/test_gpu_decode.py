@@ -389,6 +389,38 @@ def test_decode_residual_parts(cuda, m, n, k):
     assert np.array_equal(H(parts), exp)
 
 
+@pytest.mark.parametrize("path,m,n,k", [("gemm", 300, 768, 1536), ("gemm", 130, 100, 192), ("gemv", 8, 768, 1536),
+                                         ("gemv", 40, 200, 512), ("parts", 8, 768, 1536), ("parts", 37, 768, 1536),
+                                         ("parts", 3, 20, 320)])
+def test_residual_out_clamp_every_path(cuda, path, m, n, k):
+    """The SSD block's out_proj clamp (ssd_multihead.py:589-590; res_clamp on the
+    RESIDUAL accumulator) on the prefill GEMM, the decode GEMV (with row
+    statistics) and the statistics-partials out_proj, with a bound that binds on a
+    good share of the accumulators, against the oracle."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(5 * m + n + k)
+    a = i8(rng, m, k)
+    wp = pack_ternary(rng.integers(-1, 2, size=(n, k), dtype=np.int8))
+    r0 = rng.integers(-(2**23) + 1, 2**23, size=(m, n), dtype=np.int32)
+    c = 400
+    acc = O.bitlinear(a, wp, O.OUT_INT32)
+    assert 0.05 < (np.abs(acc) > c).mean() < 0.95
+    ref = O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0, res_mult=4719, res_shift=16, res_clamp=c)
+    rt = T(r0)
+    if path == "parts":
+        parts = torch.zeros((m, (n + 15) // 16, 2), dtype=torch.int64, device="cuda")
+        ops.bitlinear_residual_parts(T(a), T(wp), rt, 4719, 16, parts, res_clamp=c)
+        assert np.array_equal(H(parts).sum(1)[:, 0], ref.astype(np.int64).sum(1))
+    else:
+        stats = torch.zeros((m, 2), dtype=torch.int64, device="cuda")
+        ops.bitlinear(T(a), T(wp), ops.OUT_RESIDUAL, n, out=rt, res_mult=4719, res_shift=16, res_clamp=c,
+                      row_stats=stats, path=path)
+        r64 = ref.astype(np.int64)
+        assert np.array_equal(H(stats), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
+    assert np.array_equal(H(rt), ref)
+
+
 def _split_stats(rng, r, P):
     """Row statistics of r as P random int64 partials [m, P, 2] that sum to them."""
     r64 = r.astype(np.int64)

@@ -34,10 +34,12 @@ def test_bitlinear_random_shapes(cuda, seed):
     s = int(rng.integers(0, 12))
     r0 = rng.integers(-(2**23) + 1, 2**23, size=(m, n), dtype=np.int32)
     mult, rsh = int(rng.integers(-70000, 70000)), int(rng.integers(0, 24))
+    clamp = int(rng.choice([0, 0, 1, 40, 300, 2000]))         # RESIDUAL accumulator bound, 0 = none
     refs = {ops.OUT_INT32: O.bitlinear(a, wp, O.OUT_INT32),
             ops.OUT_INT8: O.bitlinear(a, wp, O.OUT_INT8, s),
             ops.OUT_DECAY_MOD: O.bitlinear(a, wp, O.OUT_DECAY_MOD, s),
-            ops.OUT_RESIDUAL: O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0, res_mult=mult, res_shift=rsh)}
+            ops.OUT_RESIDUAL: O.bitlinear(a, wp, O.OUT_RESIDUAL, residual=r0, res_mult=mult, res_shift=rsh,
+                                          res_clamp=clamp)}
     import torch
     ldo = n + (-n) % 4                      # output rows: a multiple of 4 elements
     dtypes = {ops.OUT_INT32: torch.int32, ops.OUT_INT8: torch.int8, ops.OUT_DECAY_MOD: torch.int8}
@@ -45,11 +47,12 @@ def test_bitlinear_random_shapes(cuda, seed):
         for kind, ref in refs.items():
             if kind == ops.OUT_RESIDUAL:
                 out = T(np.pad(r0, ((0, 0), (0, ldo - n))))
-                ops.bitlinear(T(a), T(wp), kind, n, out=out, res_mult=mult, res_shift=rsh, path=path)
+                ops.bitlinear(T(a), T(wp), kind, n, out=out, res_mult=mult, res_shift=rsh, res_clamp=clamp,
+                              path=path)
             else:
                 out = torch.zeros((m, ldo), dtype=dtypes[kind], device="cuda")
                 ops.bitlinear(T(a), T(wp), kind, n, shift=s, out=out, path=path)
-            assert np.array_equal(H(out)[:, :n], ref), (path, kind, m, n, k)
+            assert np.array_equal(H(out)[:, :n], ref), (path, kind, m, n, k, clamp)
 
 
 @pytest.mark.parametrize("seed", range(8))

@@ -10,7 +10,9 @@ to those vectors: all-position logits of two 12-token prompts and 8 greedy
 tokens each, for 2-layer models of each block type: "small" ones whose greedy
 tokens vary and depend on the history, and "wide" ones whose residual
 updates saturate and whose final norm runs past the top of the BitShiftNormV2
-table.  Planted wiring mistakes in OracleModel must fail them.
+table.  In both SSD fixtures the block's out_proj clamp (ssd_multihead.py:
+589-590) binds on a hundred-odd accumulators of the stored logits.  Planted
+wiring mistakes in OracleModel must fail them.
 """
 import os
 
@@ -41,7 +43,7 @@ def load(name):
                       s_x=sc["s_x"], s_y=sc["s_y"], w_out=g[f"l{i}_w_out_packed"], res_mult=sc["res_mult"],
                       res_shift=sc["res_shift"])
         if ssd:
-            layers.append(SSDLayerParams(decay_tab=g[f"l{i}_decay_tab"], **common))
+            layers.append(SSDLayerParams(decay_tab=g[f"l{i}_decay_tab"], out_clamp=sc["out_clamp"], **common))
         else:
             layers.append(LayerParams(w_dt=g[f"l{i}_w_dt_packed"], s_dt=sc["s_dt"], base=g[f"l{i}_base"], k=15,
                                       **common))
@@ -86,7 +88,7 @@ def test_oracle_model_matches_whole_model_fixture(name):
 
 @pytest.mark.parametrize("name,mutation", [
     (f"model_{blk}_{kind}.npz", m) for kind in ("small", "wide") for blk in ("dyadic", "ssd")
-    for m in ("swap_xz", "norm_f_v2", "no_residual") + (("block_norm_v1",) if blk == "ssd" else ())
+    for m in ("swap_xz", "norm_f_v2", "no_residual") + (("block_norm_v1", "no_out_clamp") if blk == "ssd" else ())
 ] + [("model_dyadic_small.npz", "conv_reset"), ("model_ssd_small.npz", "conv_reset")])
 def test_wiring_mutations_are_caught(name, mutation):
     """Each planted wiring mistake in OracleModel changes the logits or the

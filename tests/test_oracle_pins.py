@@ -323,6 +323,14 @@ def test_bitlinear_equals_reference_f_linear(rng):
     r = O.bitlinear(a, O.pack_ternary(w), O.OUT_RESIDUAL, residual=r0, res_mult=4719, res_shift=16)
     expect = np.clip(r0 + np.floor(ref.astype(np.float64) * 4719 / 65536 + 0.5), -(2**23 - 1), 2**23 - 1)
     assert np.array_equal(r, expect.astype(np.int32))
+    # the SSD block's out clamp: clamp(out_proj(y), -100, 100) before the residual gate
+    # (ssd_multihead.py:589-590), on the accumulator: +-c, then the same residual rule
+    for c in (1, 300, 2000):
+        assert (np.abs(ref) > c).any()
+        r = O.bitlinear(a, O.pack_ternary(w), O.OUT_RESIDUAL, residual=r0, res_mult=4719, res_shift=16, res_clamp=c)
+        expect = np.clip(r0 + np.floor(np.clip(ref.astype(np.float64), -c, c) * 4719 / 65536 + 0.5),
+                         -(2**23 - 1), 2**23 - 1)
+        assert np.array_equal(r, expect.astype(np.int32)), c
 
 
 def test_act_quant_matches_reference_torch(rng):
