@@ -291,7 +291,8 @@ def _strip(sd: Mapping[str, object]) -> Dict[str, object]:
     return out
 
 
-def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[ModelParams, float]:
+def convert_state_dict(state_dict: Mapping[str, object], config: dict,
+                       strict: bool = True) -> Tuple[ModelParams, float]:
     """Integer parameters of a reference ``MambaIntegerModel`` (the dyadic-scan
     block, ``mamba_integer_model.py:368-394,466-484``, or with ``use_ssd`` the
     multi-head SSD block, ``ssd_multihead.py:471-522``) from its float state dict.
@@ -308,59 +309,91 @@ def convert_state_dict(state_dict: Mapping[str, object], config: dict) -> Tuple[
     output_scale, ``:483``); the SSD block's out_proj clamp to +-100
     (``ssd_multihead.py:589-590``) as the accumulator bound floor(1600 / s)
     of its out_proj weight scale s."""
+    params, logit_scale, unused = convert_state_dict_keys(state_dict, config)
+    if strict and unused:
+        raise CheckpointError(f"state dict keys the integer model does not use: {unused[:5]}")
+    return params, logit_scale
+
+
+class _Reader:
+    """Typed, shape-checked access to a stripped float state dict, recording the
+    keys it reads."""
+
+    def __init__(self, sd: Mapping[str, object], d_model: int):
+        self.sd, self.d, self.used = sd, d_model, set()
+
+    def get(self, key, shape):
+        if key not in self.sd:
+            raise CheckpointError(f"state dict has no {key!r}")
+        t = _f32(self.sd[key])
+        if tuple(t.shape) != tuple(shape):
+            raise CheckpointError(f"{key}: shape {tuple(t.shape)}, config wants {tuple(shape)}")
+        self.used.add(key)
+        return t
+
+    def gain(self, prefix):
+        g = self.get(prefix + ".gamma", (self.d,)) * self.get(prefix + ".step_size", (1,))
+        return _fixed(g, 256.0, -32767, 32767, np.int16)
+
+    def unused(self):
+        return sorted(k for k in self.sd if k not in self.used and not k.endswith("dt_proj.bias"))
+
+
+def convert_state_dict_keys(state_dict: Mapping[str, object], config: dict) -> Tuple[ModelParams, float, List[str]]:
+    """``convert_state_dict`` that returns the keys the integer model does not use
+    (the ``unexpected_keys`` of ``load_state_dict(strict=False)``) instead of
+    rejecting them.  A key it needs that is missing, or a value it cannot
+    represent, still raises ``CheckpointError``."""
     sd = _strip(state_dict)
     dims = ModelDims.from_config(config)
     dims.validate()
-    d, D, N, R, V = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank, dims.vocab_size
-    used = set()
+    d, V = dims.d_model, dims.vocab_size
+    rd = _Reader(sd, d)
+    emb = _fixed(rd.get("embedding.weight", (V, d)), 16.0, -127, 127, np.int8)
+    layers = [_convert_layer(f"layers.{i}.", dims, rd) for i in range(dims.n_layer)]
+    w_head, s_head = ternary(rd.get("lm_head.weight", (V, d)))
+    params = ModelParams(dims=dims, emb=emb, layers=layers, gamma_f=rd.gain("norm_f"), w_head=pack_ternary(w_head))
+    return params, s_head / 16.0 / math.sqrt(d), rd.unused()
 
-    def get(key, shape):
-        if key not in sd:
-            raise CheckpointError(f"state dict has no {key!r}")
-        t = _f32(sd[key])
-        if tuple(t.shape) != tuple(shape):
-            raise CheckpointError(f"{key}: shape {tuple(t.shape)}, config wants {tuple(shape)}")
-        used.add(key)
-        return t
 
-    def gain(prefix):
-        g = get(prefix + ".gamma", (d,)) * get(prefix + ".step_size", (1,))
-        return _fixed(g, 256.0, -32767, 32767, np.int16)
+def convert_block_state_dict(state_dict: Mapping[str, object], config: dict):
+    """One block's float state dict (the keys of ``MambaIntegerBlock``,
+    ``mamba_integer_model.py:368-394``, or of ``MambaIntegerBlockV2`` with
+    ``use_ssd``, ``ssd_multihead.py:481-522``, without a ``layers.{i}.``
+    prefix) as (LayerParams or SSDLayerParams, unused keys)."""
+    sd = _strip(state_dict)
+    dims = ModelDims.from_config(config)
+    dims.validate()
+    rd = _Reader(sd, dims.d_model)
+    return _convert_layer("", dims, rd), rd.unused()
 
-    emb = _fixed(get("embedding.weight", (V, d)), 16.0, -127, 127, np.int8)
-    layers = []
-    for i in range(dims.n_layer):
-        p = f"layers.{i}."
-        if dims.ssd:
-            layers.append(_convert_ssd_layer(p, dims, get, gain))
-            continue
-        w_in, s_in_w = ternary(get(p + "in_proj.weight", (2 * D, d)))
-        w_x, s_x_w = ternary(get(p + "x_proj.weight", (R + 2 * N, D)))
-        w_dt, s_dt_w = ternary(get(p + "dt_proj.weight", (D, R)))
-        w_out, s_out_w = ternary(get(p + "out_proj.weight", (d, D)))
-        if p + "dt_proj.bias" in sd:
-            if float(get(p + "dt_proj.bias", (D,)).abs().max()) != 0.0:
-                raise CheckpointError(f"{p}dt_proj.bias is non-zero: the integer block has no dt bias")
-        shifts = get(p + "decay_shifts", (D, N))
-        if float(shifts.min()) != float(shifts.max()) or float(shifts.min()) != DECAY_SHIFT:
-            raise CheckpointError(f"{p}decay_shifts: the scan kernels take a uniform shift of {DECAY_SHIFT}")
-        res_mult, res_shift = residual_factor(s_out_w, float(get(p + "res_gate", (1,))[0]))
-        layers.append(LayerParams(
-            gamma=gain(p + "norm"),
-            w_in=pack_ternary(w_in), s_in=requant_shift_for(s_in_w, 4, 4),
-            conv_w=_fixed(get(p + "conv1d.weight", (D, 1, 4)).reshape(D, 4), 64.0, -127, 127, np.int8),
-            conv_b=_fixed(get(p + "conv1d.bias", (D,)), 1024.0, -(2**31), 2**31 - 1, np.int32),
-            w_x=pack_ternary(w_x), s_x=requant_shift_for(s_x_w, 4, 4),
-            w_dt=pack_ternary(w_dt), s_dt=requant_shift_for(s_dt_w, 4, 0),
-            base=_fixed(get(p + "base_decay_nums", (D, N)), 1.0, 0, DECAY_MAX, np.int32),
-            k=DECAY_SHIFT, s_y=14,
-            w_out=pack_ternary(w_out), res_mult=res_mult, res_shift=res_shift))
-    w_head, s_head = ternary(get("lm_head.weight", (V, d)))
-    params = ModelParams(dims=dims, emb=emb, layers=layers, gamma_f=gain("norm_f"), w_head=pack_ternary(w_head))
-    extra = sorted(k for k in sd if k not in used and not k.endswith("dt_proj.bias"))
-    if extra:
-        raise CheckpointError(f"state dict keys the integer model does not use: {extra[:5]}")
-    return params, s_head / 16.0 / math.sqrt(d)
+
+def _convert_layer(p: str, dims: ModelDims, rd: "_Reader"):
+    if dims.ssd:
+        return _convert_ssd_layer(p, dims, rd.get, rd.gain)
+    d, D, N, R = dims.d_model, dims.d_inner, dims.d_state, dims.dt_rank
+    get = rd.get
+    w_in, s_in_w = ternary(get(p + "in_proj.weight", (2 * D, d)))
+    w_x, s_x_w = ternary(get(p + "x_proj.weight", (R + 2 * N, D)))
+    w_dt, s_dt_w = ternary(get(p + "dt_proj.weight", (D, R)))
+    w_out, s_out_w = ternary(get(p + "out_proj.weight", (d, D)))
+    if p + "dt_proj.bias" in rd.sd:
+        if float(get(p + "dt_proj.bias", (D,)).abs().max()) != 0.0:
+            raise CheckpointError(f"{p}dt_proj.bias is non-zero: the integer block has no dt bias")
+    shifts = get(p + "decay_shifts", (D, N))
+    if float(shifts.min()) != float(shifts.max()) or float(shifts.min()) != DECAY_SHIFT:
+        raise CheckpointError(f"{p}decay_shifts: the scan kernels take a uniform shift of {DECAY_SHIFT}")
+    res_mult, res_shift = residual_factor(s_out_w, float(get(p + "res_gate", (1,))[0]))
+    return LayerParams(
+        gamma=rd.gain(p + "norm"),
+        w_in=pack_ternary(w_in), s_in=requant_shift_for(s_in_w, 4, 4),
+        conv_w=_fixed(get(p + "conv1d.weight", (D, 1, 4)).reshape(D, 4), 64.0, -127, 127, np.int8),
+        conv_b=_fixed(get(p + "conv1d.bias", (D,)), 1024.0, -(2**31), 2**31 - 1, np.int32),
+        w_x=pack_ternary(w_x), s_x=requant_shift_for(s_x_w, 4, 4),
+        w_dt=pack_ternary(w_dt), s_dt=requant_shift_for(s_dt_w, 4, 0),
+        base=_fixed(get(p + "base_decay_nums", (D, N)), 1.0, 0, DECAY_MAX, np.int32),
+        k=DECAY_SHIFT, s_y=14,
+        w_out=pack_ternary(w_out), res_mult=res_mult, res_shift=res_shift)
 
 
 def _convert_ssd_layer(p: str, dims: ModelDims, get, gain) -> SSDLayerParams:
