@@ -480,16 +480,21 @@ mi_status mi_decode_step(const mi_model_params *params, int m, const int64_t *id
 /* mi_decode_step for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * It has no counterpart in the reference.  The workspace is a file-scope
- * device array of the library, 16 MiB (16777216 bytes) per GPU, held until
- * the process ends; its address is looked up once per device on the first
- * call (with that device current).  A model and batch whose workspace
- * (mi_decode_workspace_size) exceeds 16 MiB is rejected with MI_ERR_BAD_DIM
- * before anything is enqueued; the d768 x 24 model fits up to m = 64 and the
- * d2048 x 48 model (batched stages, vocab 32000) up to m = 64.  Every call on
- * one GPU shares that array: calls that overlap on one GPU (other streams,
- * other threads) race and must be serialized by the caller.  The step writes
- * every part of the workspace it reads, so nothing needs clearing between
- * calls.  Same arguments and results as mi_decode_step otherwise. */
+ * device array of the library, 16 MiB (16777216 bytes) per GPU: every process
+ * that runs any kernel of this library on a GPU holds it there until the
+ * process ends, whether or not it calls this entry.  Its address (and an
+ * event) are set up once per device on the first call, with that device
+ * current; make that first call outside stream capture.  A model and batch
+ * whose workspace (mi_decode_workspace_size) exceeds 16 MiB is rejected with
+ * MI_ERR_BAD_DIM before anything is enqueued; the d768 x 24 model fits up to
+ * m = 64 and the d2048 x 48 model (batched stages, vocab 32000) up to m = 64.
+ * Every call on one GPU shares that array, so calls must not overlap on one
+ * GPU: a call on another stream than the previous eager call, while that one
+ * is still running, is refused with MI_ERR_BAD_ARG; calls from several host
+ * threads are serialized.  Replays of a captured step are not tracked: the
+ * caller orders them against other calls.  The step writes every part of the
+ * workspace it reads, so nothing needs clearing between calls.  Same
+ * arguments and results as mi_decode_step otherwise. */
 mi_status mi_decode_step_static(const mi_model_params *params, int m, const int64_t *ids, int64_t *next_ids,
                                 int32_t *logits, int ld_logits, int8_t *const *conv_state,
                                 int32_t *const *h_state, void *stream);

@@ -109,13 +109,28 @@ mi_status check_model(const char *fn, const mi_model_params *p, int m) {
 }
 
 // The workspace of mi_decode_step_static: one array in device memory per GPU,
-// held by the loaded library until the process ends (no allocation call).
-// Host code never uses the name `scratch` as an address (on the host it is a
-// stand-in symbol); it uses the per-device address hipGetSymbolAddress returns.
+// reserved wherever the library's code object is loaded on a GPU (its first
+// kernel launch there) and held until the process ends, whether or not the
+// static entry is called (no allocation call).  Host code never uses the name
+// `scratch` as an address (on the host it is a stand-in symbol); it uses the
+// per-device address hipGetSymbolAddress returns.
+//
+// Calls share the array, so two calls whose kernels overlap on one GPU would
+// race.  Each device keeps the stream of its last eager call and an event
+// recorded after it: a call on another stream while that event is pending is
+// refused.  Host threads are serialized by one mutex, so check and record are
+// one step.  Work under stream capture is neither checked nor recorded (the
+// graph's replays are the caller's to order).
 constexpr size_t kStaticScratchBytes = (size_t)16 << 20;
 constexpr int kMaxDevices = 64;
-std::atomic<void *> g_scratch_ptr[kMaxDevices];
-std::mutex g_scratch_mu;
+struct StaticSlot {
+    void *ptr = nullptr;            // this device's address of `scratch`
+    hipEvent_t done = nullptr;      // recorded after the last eager call
+    hipStream_t last = nullptr;     // the stream of that call
+    bool recorded = false;
+};
+StaticSlot g_static[kMaxDevices];
+std::mutex g_static_mu;
 
 }  // namespace
 }  // namespace mi
@@ -125,26 +140,27 @@ static __device__ __align__(256) unsigned char scratch[mi::kStaticScratchBytes];
 namespace mi {
 namespace {
 
-// The current device's address of `scratch`, looked up once per device.
-mi_status static_scratch(const char *fn, void **out) {
+// The current device's slot, set up on its first call (the address of
+// `scratch` and the event).  The caller holds g_static_mu.
+mi_status static_slot(const char *fn, StaticSlot **out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
     MI_REQUIRE(dev >= 0 && dev < kMaxDevices, MI_ERR_BAD_ARG, "%s: device %d beyond the %d this library tracks", fn,
                dev, kMaxDevices);
-    void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
-    if (!ptr) {
-        std::lock_guard<std::mutex> lock(g_scratch_mu);
-        ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
-        if (!ptr) {
-            e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-            if (e != hipSuccess || !ptr)
-                return fail(MI_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", fn, dev,
-                            hipGetErrorString(e));
-            g_scratch_ptr[dev].store(ptr, std::memory_order_release);
-        }
+    StaticSlot &sl = g_static[dev];
+    if (!sl.ptr) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(MI_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", fn, dev,
+                        hipGetErrorString(e));
+        e = hipEventCreateWithFlags(&sl.done, hipEventDisableTiming);
+        if (e != hipSuccess)
+            return fail(MI_ERR_HIP, "%s: hipEventCreate on device %d failed: %s", fn, dev, hipGetErrorString(e));
+        sl.ptr = ptr;
     }
-    *out = ptr;
+    *out = &sl;
     return MI_OK;
 }
 
@@ -297,9 +313,32 @@ extern "C" mi_status mi_decode_step_static(const mi_model_params *params, int m,
                "(call mi_decode_step with a workspace of your own)", m, need, kStaticScratchBytes);
     MI_REQUIRE(ids && next_ids && conv_state && h_state, MI_ERR_NULL_POINTER,
                "mi_decode_step_static: ids, next_ids, conv_state and h_state are required");
-    void *ws = nullptr;
-    st = static_scratch("mi_decode_step_static", &ws);
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    StaticSlot *sl = nullptr;
+    st = static_slot("mi_decode_step_static", &sl);
     if (st != MI_OK) return st;
-    return mi_decode_step(params, m, ids, next_ids, logits, ld_logits, conv_state, h_state, ws, kStaticScratchBytes,
-                          stream);
+    const hipStream_t s = as_stream(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &cap);
+    if (e != hipSuccess)
+        return fail(MI_ERR_HIP, "mi_decode_step_static: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    if (!capturing && sl->recorded && sl->last != s) {
+        e = hipEventQuery(sl->done);
+        MI_REQUIRE(e != hipErrorNotReady, MI_ERR_BAD_ARG,
+                   "mi_decode_step_static: the previous call, on another stream, is still running and holds the "
+                   "static workspace (order the calls: one stream, or wait for the other)");
+        if (e != hipSuccess)
+            return fail(MI_ERR_HIP, "mi_decode_step_static: hipEventQuery failed: %s", hipGetErrorString(e));
+    }
+    st = mi_decode_step(params, m, ids, next_ids, logits, ld_logits, conv_state, h_state, sl->ptr, kStaticScratchBytes,
+                        stream);
+    if (st == MI_OK && !capturing) {
+        e = hipEventRecord(sl->done, s);
+        if (e != hipSuccess)
+            return fail(MI_ERR_HIP, "mi_decode_step_static: hipEventRecord failed: %s", hipGetErrorString(e));
+        sl->last = s;
+        sl->recorded = true;
+    }
+    return st;
 }
