@@ -1025,10 +1025,8 @@ __global__ __launch_bounds__(512) void resid_gemv16_kernel(GemmArgs g0) {
                 s1 += v;
                 s2 += v * v;
             }
-            s1 += __shfl_xor(s1, 1);
-            s2 += __shfl_xor(s2, 1);
-            s1 += __shfl_xor(s1, 2);
-            s2 += __shfl_xor(s2, 2);
+            s1 = quad_sum64(s1);   // wave 0, all lanes active
+            s2 = quad_sum64(s2);
             if (q == 0 && i < g.M) {
                 if (g.stats_parts) {
                     *reinterpret_cast<v2l *>(g.stats_parts + 2 * ((int64_t)i * gridDim.x + blockIdx.x)) =

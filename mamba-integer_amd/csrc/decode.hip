@@ -89,7 +89,9 @@ struct StatParts {
     v2l v[kStatLoads];
 };
 
-__device__ __forceinline__ int stat_group(int M) { return min(norm_tpr(M), 64); }
+// (16 lanes at most: the sum then stays inside a DPP row, with no cross-row
+// shuffle through LDS; the 16 lanes of a row group's other halves repeat it)
+__device__ __forceinline__ int stat_group(int M) { return min(norm_tpr(M), 16); }
 
 __device__ __forceinline__ StatParts load_stat_parts(const NormGemvArgs &g, int mr) {
     const bool have = g.row_stats != nullptr;
@@ -105,14 +107,8 @@ __device__ __forceinline__ StatParts load_stat_parts(const NormGemvArgs &g, int 
     return p;
 }
 
-// v + (v of the lane the DPP control names), 64-bit, within rows of 16 lanes
-template <int kCtrl>
-__device__ __forceinline__ int64_t dpp_add64(int64_t v) {
-    const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)v, kCtrl, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)((uint64_t)v >> 32), kCtrl, 0xF, 0xF, false);
-    return v + (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
-
+// (dpp_add64: v + the value of the lane a DPP control names, 64-bit, within
+// rows of 16 lanes; mi_common.hpp)
 // Sum over a lane group of 2^k lanes (aligned), every lane getting the total:
 // quad swaps (xor 1, xor 2), then the half-row and row mirrors (lane i with
 // 7 - i, then 15 - i: after the quad step each pairs with a lane of the other
@@ -185,25 +181,39 @@ __device__ void stage_norm_rows(const NormGemvArgs &g, int8_t *a, int pitch, con
         const int ngrp = (K4 + TPR - 1) >> lt;
         for (int j0 = 0; j0 < ngrp; j0 += kC) {
             if (j0 > 0) load_chunk(j0);
+            // two groups (8 values) at a time: their 64-bit products are
+            // independent chains written out one after another, every group
+            // computed from its clamped load and stored unconditionally, a
+            // group outside the rows into its row's padding bytes [K, K + 4)
+            // that no MFMA reads (one basic block per pair: a branch per
+            // group made each value wait on the one before it)
 #pragma unroll
-            for (int c = 0; c < kC; ++c) {
-                const int grp = tr + (j0 + c) * TPR;
-                if (m < g.M && grp < K4) {
-                    const int vv[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
-                    const int gg[4] = {(int16_t)(gv[c].x & 0xFFFF), (int16_t)(gv[c].x >> 16),
-                                       (int16_t)(gv[c].y & 0xFFFF), (int16_t)(gv[c].y >> 16)};
-                    uint32_t o = 0;
+            for (int c0 = 0; c0 < kC; c0 += 2) {
+                if (j0 + c0 >= ngrp) break;  // the same for the whole block
+                int64_t p[8];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        // |r - mu| < 2^24 and |gamma| < 2^15, so the rounded
-                        // quotient (shift >= 9) fits 32 bits: the low word of
-                        // the 64-bit shift is the exact value
-                        const int64_t p = (int64_t)(vv[q] - mu) * gg[q] + rnd;
-                        const int32_t v = (int32_t)__builtin_amdgcn_alignbit((uint32_t)((uint64_t)p >> 32),
-                                                                             (uint32_t)p, (uint32_t)sh);
-                        o |= (uint32_t)(min(max(v, -127), 127) & 255) << (8 * q);
-                    }
-                    *reinterpret_cast<uint32_t *>(&a[m * pitch + 4 * grp]) = o;
+                for (int e = 0; e < 8; ++e) {
+                    const int c = c0 + (e >> 2), q = e & 3;
+                    const int v = q == 0 ? rv[c].x : q == 1 ? rv[c].y : q == 2 ? rv[c].z : rv[c].w;
+                    const uint32_t gw = q < 2 ? gv[c].x : gv[c].y;
+                    const int gm = (int16_t)((q & 1) ? (gw >> 16) : (gw & 0xFFFF));
+                    // |r - mu| < 2^24 and |gamma| < 2^15, so the rounded
+                    // quotient (shift >= 9) fits 32 bits: the low word of
+                    // the 64-bit shift is the exact value
+                    p[e] = (int64_t)(v - mu) * gm + rnd;
+                }
+                uint32_t o[2] = {0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int32_t v = (int32_t)__builtin_amdgcn_alignbit((uint32_t)((uint64_t)p[e] >> 32),
+                                                                         (uint32_t)p[e], (uint32_t)sh);
+                    o[e >> 2] |= (uint32_t)(min(max(v, -127), 127) & 255) << (8 * (e & 3));
+                }
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int grp = tr + (j0 + c0 + e) * TPR;
+                    const int col = m < g.M && grp < K4 ? 4 * grp : g.K;   // m < 16 rows of a
+                    *reinterpret_cast<uint32_t *>(&a[m * pitch + col]) = o[e];
                 }
             }
         }
@@ -631,7 +641,9 @@ __device__ __forceinline__ void xproj_token_c16(const DtScanArgs &g, int m, int3
 // [q*NPL, q*NPL+NPL), read and written as int4; NPL == 0: lane q owns states
 // q, q+4, ... (any nstate <= 64).  Every load is issued unconditionally from
 // an in-bounds address before the first wait.
-template <int XNT, int NPL>
+// S24 (NPL = 4, decay_shift 15): the state update in 24-bit multiplies
+// (update16, as in dt_scan_tok_kernel) and y as two int32 partial sums.
+template <int XNT, int NPL, bool S24 = false>
 __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     __shared__ __align__(16) int8_t s_dt[kMaxR];
     __shared__ int8_t s_bc[2 * kMaxN];
@@ -751,19 +763,36 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
                 acc = __builtin_amdgcn_sdot4(wt[j], *reinterpret_cast<const int *>(&s_dt[16 * w + 4 * j]), acc, false);
         }
     }
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
+    acc = quad_sum(acc);
     const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
     const int64_t xd = rshr64((int64_t)xsv * s_dtq[dm + 20], 10);
     int64_t y = 0;
     if constexpr (NPL > 0) {
         int32_t hn[NPL];
+        if constexpr (S24) {
+            // |x * dt| <= 127 * 6554: the rounded shift is exact in 32 bits;
+            // the base is clamped to [-21, 32021] first (with |dm| <= 20 the
+            // decay clamp(base + dm, 0, 32000) is unchanged) and doubled
+            static_assert(NPL == 4, "S24 takes 4 states a lane");
+            const int xd32 = (xsv * s_dtq[dm + 20] + 512) >> 10;
+            int yh = 0, yl = 0;
 #pragma unroll
-        for (int i = 0; i < NPL; ++i) {
-            const int n = q * NPL + i;
-            const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
-            hn[i] = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[n] * xd);
-            y += (int64_t)s_bc[g.N + n] * hn[i];
+            for (int i = 0; i < NPL; ++i) {
+                const int n = q * NPL + i;
+                const int n2 = min(max(2 * clamp32(bv[i], -21, 32021) + 2 * dm, 0), 64000);
+                hn[i] = hv[i];
+                update16(hn[i], n2, __mul24((int)s_bc[n], xd32), (int)s_bc[g.N + n], yh, yl);
+            }
+            y = (int64_t)quad_sum(yh) * 65536 + quad_sum(yl);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int n = q * NPL + i;
+                const int64_t nt = clamp64((int64_t)bv[i] + dm, 0, 32000);
+                hn[i] = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[n] * xd);
+                y += (int64_t)s_bc[g.N + n] * hn[i];
+            }
+            y = quad_sum64(y);
         }
         if (active) {
 #pragma unroll
@@ -782,9 +811,8 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
                 y += (int64_t)s_bc[g.N + n] * hn;
             }
         }
+        y = quad_sum64(y);
     }
-    y += __shfl_xor(y, 1);
-    y += __shfl_xor(y, 2);
     if (active && q == 0) {
         const int64_t yg = ((int64_t)sat32_64(y) * s_gate[zv + 128]) >> 15;
         g.yo[(int64_t)m * g.D + d] = (int8_t)clamp64(rshr64(yg, g.s_y), -127, 127);
@@ -904,8 +932,7 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
                                                  acc, false);
             }
         }
-        acc += __shfl_xor(acc, 1);
-        acc += __shfl_xor(acc, 2);
+        acc = quad_sum(acc);
         const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
         const int hv[4] = {h4[t][0], h4[t][1], h4[t][2], h4[t][3]};
         const int bv[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -924,11 +951,7 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
                 hn[i] = hv[i];
                 update16(hn[i], n2, __mul24(bn, xd), cn, yh, yl);
             }
-            yh += __shfl_xor(yh, 1);
-            yl += __shfl_xor(yl, 1);
-            yh += __shfl_xor(yh, 2);
-            yl += __shfl_xor(yl, 2);
-            y = (int64_t)yh * 65536 + yl;
+            y = (int64_t)quad_sum(yh) * 65536 + quad_sum(yl);
         } else {
             const int64_t xd = rshr64((int64_t)xsv[t] * s_dtq[dm + 20], 10);
 #pragma unroll
@@ -938,8 +961,7 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
                 hn[i] = sat32_64((((int64_t)hv[i] * nt) >> g.k) + (int64_t)s_bc[t][n] * xd);
                 y += (int64_t)s_bc[t][16 + n] * hn[i];
             }
-            y += __shfl_xor(y, 1);
-            y += __shfl_xor(y, 2);
+            y = quad_sum64(y);
         }
         if (active && m < g.M)
             __builtin_nontemporal_store(v4i{hn[0], hn[1], hn[2], hn[3]},
@@ -1185,7 +1207,9 @@ extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s
             hipLaunchKernelGGL((dt_scan_tok_kernel<2, true, true>), tgrid, dim3(256), 0, as_stream(stream), g);
         else
             hipLaunchKernelGGL((dt_scan_tok_kernel<2, true, false>), tgrid, dim3(256), 0, as_stream(stream), g);
-    } else if (vec)
+    } else if (vec && decay_shift == 15)
+        hipLaunchKernelGGL((dt_scan_step_kernel<-1, 4, true>), grid, dim3(256), 0, as_stream(stream), g);
+    else if (vec)
         hipLaunchKernelGGL((dt_scan_step_kernel<-1, 4>), grid, dim3(256), 0, as_stream(stream), g);
     else
         hipLaunchKernelGGL((dt_scan_step_kernel<-1, 0>), grid, dim3(256), 0, as_stream(stream), g);

@@ -23,6 +23,22 @@ inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintp
 // branches on it as uniform (no per-lane masking around loads).
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// Sums over the 4 lanes of a quad by DPP quad swaps (quad_perm [1,0,3,2],
+// then [2,3,0,1]), with no LDS round trip; every lane of the quad must be
+// active.
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+template <int kCtrl>
+__device__ __forceinline__ int64_t dpp_add64(int64_t v) {
+    const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)v, kCtrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)((uint64_t)v >> 32), kCtrl, 0xF, 0xF, false);
+    return v + (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ int64_t quad_sum64(int64_t v) { return dpp_add64<0x4E>(dpp_add64<0xB1>(v)); }
+
 // ------------------------------------------------------ integer primitives
 __host__ __device__ __forceinline__ constexpr int64_t rshr64(int64_t v, int s) {
     return s <= 0 ? v : ((v + ((int64_t)1 << (s - 1))) >> s);
