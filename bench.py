@@ -14,7 +14,7 @@ OpenMP on every host core) on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-kernels]
     python bench.py --pmc-probe     # only the dominant kernel + a copy of known size, for rocprofv3 --pmc
-    python bench.py --gemm-probe    # only the config-2 prefill GEMM (20 launches), for rocprofv3 counters
+    python bench.py --gemm-probe [--gemm-shape M,K,N]   # only a prefill GEMM (20 launches; default config 2), for rocprofv3 counters
     python bench.py --scan-probe    # only the scan kernels at their benchmark shapes, for rocprofv3 counters
 """
 import argparse
@@ -214,14 +214,14 @@ def in_proj_stage_launch(run, ws, state):
                                          ws.xs, ws.xz, row_stats=ws.parts, w_x=ly.w_x, xpart=ws.xpart)
 
 
-def gemm_probe():
-    """For rocprofv3: 20 launches of the config-2 prefill GEMM (M 4096, K 768,
-    N 3072, int8 requant out) on the MFMA tile path."""
+def gemm_probe(shape=(4096, 768, 3072)):
+    """For rocprofv3: 20 launches of a prefill GEMM (default: config 2, M 4096,
+    K 768, N 3072; int8 requant out) on the MFMA tile path."""
     import numpy as np
     import torch
     from mamba_int import ops, pack_ternary
     rng = np.random.default_rng(1)
-    M, K, N = 4096, 768, 3072
+    M, K, N = shape
     a = torch.from_numpy(rng.integers(-127, 128, size=(M, K), dtype=np.int8)).to("cuda:0")
     wp = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(N, K), dtype=np.int8))).to("cuda:0")
     o = torch.empty((M, N), dtype=torch.int8, device="cuda:0")
@@ -366,10 +366,19 @@ def kernel_table():
         idx["i"] += 1
     ms = _time_kernel(gemv, iters=copies)
     byt = 593664
+    # the floor a single dependent launch cannot go below: the period of an
+    # empty (one-element fill) kernel replayed the same way
+    tiny = torch.zeros(1, device=dev)
+    null_ms = _time_kernel(lambda: tiny.fill_(1.0), iters=copies)
     out["config2_gemv_m1"] = {"ms": ms, "GB_s": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
-                              "note": "weights rotated over 512 copies (302 MB > MALL)",
-                              "roofline": {"bound": "hbm", "achieved": byt / ms / 1e6, "peak": HBM_PEAK_GBS,
-                                           "unit": "GB/s", "frac": byt / ms / 1e6 / HBM_PEAK_GBS}}
+                              "note": "weights rotated over 512 copies (302 MB > MALL); 0.59 MB is "
+                                      f"{byt / HBM_PEAK_GBS / 1e3:.3f} us of HBM time, below the "
+                                      f"{null_ms * 1e3:.2f} us period of an empty kernel: launch-latency bound",
+                              "hbm_byte_time_us": byt / HBM_PEAK_GBS / 1e3,
+                              "empty_kernel_period_us": null_ms * 1e3,
+                              "roofline": {"bound": "hbm (latency-bound at this size)", "achieved": byt / ms / 1e6,
+                                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                           "frac": byt / ms / 1e6 / HBM_PEAK_GBS}}
     # config-3 decode GEMVs at batch 8
     for name, (NN, KK) in {"in_proj": (3072, 768), "out_proj": (768, 1536), "lm_head": (32000, 768)}.items():
         w = torch.from_numpy(pack_ternary(rng.integers(-1, 2, size=(NN, KK), dtype=np.int8))).to(dev)
@@ -478,6 +487,7 @@ def main():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
     ap.add_argument("--pmc-probe", action="store_true", help="only the dominant kernel and a copy (for counters)")
     ap.add_argument("--gemm-probe", action="store_true", help="only the config-2 prefill GEMM (for counters)")
+    ap.add_argument("--gemm-shape", default="4096,768,3072", help="M,K,N of --gemm-probe")
     ap.add_argument("--scan-probe", action="store_true", help="only the scan kernels at their benchmark shapes "
                     "(for counters)")
     ap.add_argument("--decode5-probe", action="store_true",
@@ -498,7 +508,7 @@ def main():
         pmc_probe()
         return
     if args.gemm_probe:
-        gemm_probe()
+        gemm_probe(tuple(int(v) for v in args.gemm_shape.split(",")))
         return
     if args.decode5_probe:
         decode5_probe()
