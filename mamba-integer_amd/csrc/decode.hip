@@ -973,6 +973,184 @@ __global__ __launch_bounds__(256) void dt_scan_tok_kernel(DtScanArgs g) {
     }
 }
 
+// The batched scan step with the per-channel work split over the quad
+// (nstate 16, decay shift 15, x_proj as <= kTokMaxParts int32 partials per
+// token; d_inner a multiple of 64).  A wave owns 64 channels c0 + [0, 64) of
+// TPB tokens; a block, four waves (256 channels).  The states stream as in dt_scan_tok_kernel: load j
+// of a token moves bytes [1 KB j, 1 KB (j + 1)) of the wave's 4 KB state
+// tile, so lane l = 4k + q holds states 4q..4q+3 of channel c0 + 16j + k, for
+// j = 0..3.  Each lane also owns one of its four channels, c0 + 16q + k, and
+// runs that channel's per-channel work once: the dt_proj dot (its channel's
+// KW >= R/16 words unpacked once for the TPB tokens), dm, dt, x*dt, and the
+// gate of y.  The quad passes each channel's 2*dm and x*dt from its owner with
+// a DPP broadcast, and the four lanes' partial sums of y = C . h meet at the
+// owner in a DPP reduce-scatter.  Where dt_scan_tok_kernel's lanes each
+// repeat their channel's dot, dt and gate, this kernel does that work once.
+// The state update is dt_scan_tok_kernel's S24 form (update16 with the input
+// term as one clamped multiply-add); y accumulates C * H and C * L in int32
+// (|sum| < 2^28 over a channel's 16 states).
+template <int J>
+__device__ __forceinline__ int quad_bcast(int v) {
+    return __builtin_amdgcn_mov_dpp(v, J * 0x55, 0xF, 0xF, false);
+}
+// lane q of each quad gets sum over the quad's lanes of their v[q]
+__device__ __forceinline__ int quad_reduce_scatter(const int (&v)[4], int q) {
+    const bool odd = q & 1;
+    // exchange with lane q ^ 1: keep the two channels of this lane's parity
+    int k0 = odd ? v[1] : v[0], k1 = odd ? v[3] : v[2];
+    const int s0 = odd ? v[0] : v[1], s1 = odd ? v[2] : v[3];
+    k0 += __builtin_amdgcn_mov_dpp(s0, 0xB1, 0xF, 0xF, false);
+    k1 += __builtin_amdgcn_mov_dpp(s1, 0xB1, 0xF, 0xF, false);
+    // exchange with lane q ^ 2: k0 holds channel q & 1, k1 channel (q & 1) + 2
+    const bool hi = q & 2;
+    const int mine = hi ? k1 : k0, other = hi ? k0 : k1;
+    return mine + __builtin_amdgcn_mov_dpp(other, 0x4E, 0xF, 0xF, false);
+}
+
+template <int TPB, int KW>
+__global__ __launch_bounds__(256) void dt_scan_quad_kernel(DtScanArgs g) {
+    __shared__ __align__(16) int8_t s_dt[TPB][16 * KW];
+    __shared__ __align__(16) int32_t s_bc[TPB][32];   // B at [0, 16), C at [16, 32), as int32
+    __shared__ int32_t s_dtq[41];
+    __shared__ int32_t s_gate[256];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int q = lane & 3, k = lane >> 2;
+    const int32_t tab_dt = kStepTables.dtq[min(tid, 40)];
+    const int32_t tab_gate = kStepTables.gate[tid];
+    const int m0 = blockIdx.y * TPB;
+    const int c0 = blockIdx.x * 256 + (tid >> 6) * 64;
+    const bool wave_on = c0 < g.D;              // uniform: the wave's 64 channels all exist
+    const int cl0 = wave_on ? c0 : g.D - 64;    // loads of a wave past d_inner read the last 64 channels
+    const int own = cl0 + 16 * q + k;
+    const int kw = g.R / 16;   // 1 <= kw <= KW
+    // every load before the first wait, the x_proj partials first (their sum
+    // is staged while the states stream in).  The TPB x_proj rows: thread
+    // i < TPB * nxr / 4 sums outputs 4i..4i+3 of every partial (nxr = R + 32,
+    // a multiple of 16: a group never straddles two tokens or the dt_raw / B /
+    // C boundaries)
+    const int nxr = g.R + 32;
+    const int ngrp = TPB * nxr / 4;
+    const int gi = min(tid, ngrp - 1);
+    const int tq = 4 * gi / nxr, cq = 4 * gi - tq * nxr;
+    v4i xq4[kTokMaxParts];
+    {
+        const int mt = min(m0 + tq, g.M - 1);
+#pragma unroll
+        for (int b = 0; b < kTokMaxParts; ++b)
+            xq4[b] = *reinterpret_cast<const v4i *>(g.xpart + ((int64_t)mt * g.nblk + min(b, g.nblk - 1)) * nxr + cq);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the partial loads ahead of the state loads
+    // then the per-channel operands, then the wave's state tiles (token t's
+    // starts at channel cl0, its load j at + 1 KB * j)
+    int xsv[TPB], zv[TPB];
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) {
+        const int mt = min(m0 + t, g.M - 1);
+        xsv[t] = g.xs[(int64_t)mt * g.D + own];
+        zv[t] = g.z[(int64_t)mt * g.z_stride + own];
+    }
+    uint32_t wdt[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) wdt[i] = g.w_dt[(int64_t)own * kw + min(i, kw - 1)];  // words past kw zeroed below
+    v4i b4[4];
+    {
+        const v4i *bp = reinterpret_cast<const v4i *>(g.base + (int64_t)(cl0 + k) * 16 + 4 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b4[j] = bp[64 * j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    v4i h[TPB][4];
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) {
+        const v4i *hp =
+            reinterpret_cast<const v4i *>(g.h + ((int64_t)min(m0 + t, g.M - 1) * g.D + cl0 + k) * 16 + 4 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[t][j] = __builtin_nontemporal_load(hp + 64 * j);
+    }
+    // words past kw are zero, so the dot runs over all KW words (dt_raw past R
+    // in LDS is never written; it meets zero weights)
+    v4i wt[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) wt[i] = unpack16(wdt[i] & (0u - (uint32_t)(i < kw)));  // code 0 is weight 0
+    if (tid < ngrp) {
+        v4i sum = xq4[0];
+#pragma unroll
+        for (int b = 1; b < kTokMaxParts; ++b)
+            if (b < g.nblk) sum += xq4[b];
+        v4i qv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qv[r] = clamp32(rshr32(sum[r], g.s_x), -127, 127);
+        if (cq < g.R) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w |= (uint32_t)(qv[r] & 255) << (8 * r);
+            *reinterpret_cast<uint32_t *>(&s_dt[tq][cq]) = w;
+        } else {
+            *reinterpret_cast<v4i *>(&s_bc[tq][cq - g.R]) = qv;
+        }
+    }
+    if (tid < 41) s_dtq[tid] = tab_dt;
+    s_gate[tid] = tab_gate;
+    __syncthreads();
+    // 2 * base, the base first clamped to [-21, 32021] (with |dm| <= 20,
+    // clamp(base + dm, 0, 32000) is unchanged and the doubling cannot overflow)
+    int b2[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b2[j][e] = 2 * clamp32(b4[j][e], -21, 32021);
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) {
+        const int m = m0 + t;
+        // the owned channel's dt_proj dot, dm and x * dt
+        int acc = 0;
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+            const v4i xv = *reinterpret_cast<const v4i *>(&s_dt[t][16 * i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot4(wt[i][j], xv[j], acc, false);
+        }
+        const int dm = clamp32(rshr32(acc, g.s_dt), -20, 20);
+        // |x * dt| <= 127 * 6554: the rounded shift is exact in 32 bits
+        const int xd = (__mul24(xsv[t], s_dtq[dm + 20]) + 512) >> 10;
+        const int dm2 = 2 * dm;
+        const int dmj[4] = {quad_bcast<0>(dm2), quad_bcast<1>(dm2), quad_bcast<2>(dm2), quad_bcast<3>(dm2)};
+        const int xdj[4] = {quad_bcast<0>(xd), quad_bcast<1>(xd), quad_bcast<2>(xd), quad_bcast<3>(xd)};
+        const v4i bb = *reinterpret_cast<const v4i *>(&s_bc[t][4 * q]);
+        const v4i cc = *reinterpret_cast<const v4i *>(&s_bc[t][16 + 4 * q]);
+        const bool store = wave_on && m < g.M;   // uniform
+        v4i *hp = reinterpret_cast<v4i *>(g.h + ((int64_t)min(m, g.M - 1) * g.D + cl0 + k) * 16 + 4 * q);
+        int yh[4], yl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            yh[j] = 0;
+            yl[j] = 0;
+            v4i hn;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int n2 = min(max(b2[j][e] + dmj[j], 0), 64000);
+                int32_t hv = h[t][j][e];
+                update16_b(hv, n2, bb[e], xdj[j], cc[e], yh[j], yl[j]);
+                hn[e] = hv;
+            }
+            if (store) __builtin_nontemporal_store(hn, hp + 64 * j);
+        }
+        const int YH = quad_reduce_scatter(yh, q), YL = quad_reduce_scatter(yl, q);
+        if (store) {
+            const int64_t y = (int64_t)YH * 65536 + YL;
+            const int64_t yg = ((int64_t)sat32_64(y) * s_gate[zv[t] + 128]) >> 15;
+            g.yo[(int64_t)m * g.D + own] = (int8_t)clamp64(rshr64(yg, g.s_y), -127, 127);
+        }
+    }
+}
+
+template <int TPB>
+void launch_scan_quad(int kw, dim3 grid, hipStream_t hs, const DtScanArgs &g) {
+    if (kw <= 4) hipLaunchKernelGGL((dt_scan_quad_kernel<TPB, 4>), grid, dim3(256), 0, hs, g);
+    else if (kw <= 8) hipLaunchKernelGGL((dt_scan_quad_kernel<TPB, 8>), grid, dim3(256), 0, hs, g);
+    else hipLaunchKernelGGL((dt_scan_quad_kernel<TPB, 16>), grid, dim3(256), 0, hs, g);
+}
+
 template <int NPL>
 void launch_xproj_scan(int ntiles, dim3 grid, hipStream_t hs, const DtScanArgs &g) {
     if (ntiles <= 2) hipLaunchKernelGGL((dt_scan_step_kernel<2, NPL>), grid, dim3(256), 0, hs, g);
@@ -1200,7 +1378,21 @@ extern "C" mi_status mi_xpart_dt_scan_step(const int32_t *xpart, int nblk, int s
     g.h = h_state; g.yo = yo; g.M = m; g.D = d_inner; g.N = nstate;
     const dim3 grid((unsigned)((d_inner + 63) / 64), (unsigned)m);
     const bool vec = nstate == 16 && aligned(h_state, 16) && aligned(base, 16);
-    if (vec && nblk <= kTokMaxParts && m >= 2 && aligned(xpart, 16)) {
+    const bool few = vec && nblk <= kTokMaxParts && aligned(xpart, 16);
+    // the quad-split scan step where its grid still has 256 blocks (the most
+    // tokens per block that does)
+    const int cblk = (d_inner + 255) / 256;
+    const int quad_tpb = (int64_t)cblk * ((m + 3) / 4) >= 256   ? 4
+                         : (int64_t)cblk * ((m + 1) / 2) >= 256 ? 2
+                         : (int64_t)cblk * m >= 256             ? 1
+                                                                : 0;
+    if (few && decay_shift == 15 && quad_tpb > 0 && d_inner % 64 == 0) {
+        const dim3 qgrid((unsigned)cblk, (unsigned)((m + quad_tpb - 1) / quad_tpb));
+        const int kw = dt_rank / 16;
+        if (quad_tpb == 4) launch_scan_quad<4>(kw, qgrid, as_stream(stream), g);
+        else if (quad_tpb == 2) launch_scan_quad<2>(kw, qgrid, as_stream(stream), g);
+        else launch_scan_quad<1>(kw, qgrid, as_stream(stream), g);
+    } else if (few && m >= 2) {
         // few partials (mi_conv_step_xpart's channel quarters): two tokens per block
         const dim3 tgrid((unsigned)((d_inner + 63) / 64), (unsigned)((m + 1) / 2));
         if (decay_shift == 15)

@@ -81,6 +81,44 @@ def test_dt_scan_step(cuda, m, D, N, R):
     assert np.array_equal(H(hg), h_ref)
 
 
+@pytest.mark.parametrize("m,D,R", [(63, 4160, 128), (64, 4096, 224), (40, 4160, 48), (30, 4096, 96),
+                                   (1, 65536, 16), (33, 2048, 128), (20, 1024, 64)])
+def test_quad_split_scan_step(cuda, m, D, R):
+    """The batched scan step from channel-quarter x_proj partials where the
+    grid has 256 blocks of 256 channels (mi_xpart_dt_scan_step's quad-split
+    kernel: one, two or four tokens per block, each lane owning one channel's
+    dot, dt and gate, the quad exchanging them by DPP), over the whole int32
+    state range.  Covers a last block of one token (m 63 at four per block),
+    one token in a four-token block (m 1), d_inner not a multiple of 256
+    (4160: waves past d_inner), dt_rank from 16 to 224, and a grid under 256
+    blocks (D 1024, m 20: the two-lane-per-token kernel)."""
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(m * 7 + D + R)
+    N = 16
+    W = R + 2 * N
+    xs = i8(rng, m, D)
+    z = i8(rng, m, 2 * D, lo=-128)
+    wdt = pack_ternary(rng.integers(-1, 2, size=(D, R), dtype=np.int8))
+    base = rng.integers(0, 32001, size=(D, N), dtype=np.int64)
+    base[::7, 3] = -50
+    base[::11, 5] = 40000
+    base[0, :4] = [2**31 - 1, 2**31 - 10, -2**31, -2**31 + 5]
+    base = base.astype(np.int32)
+    h0 = rng.integers(-2**31, 2**31, size=(m, D, N), dtype=np.int64).astype(np.int32)
+    h0[:, ::5, 0] = 2**31 - 1
+    h0[:, ::9, 1] = -2**31
+    xq = rng.integers(-3000, 3000, size=(m, 4, W), dtype=np.int32)
+    xp = np.clip((xq.sum(1) + 16) >> 5, -127, 127).astype(np.int8)
+    dm = O.bitlinear(np.ascontiguousarray(xp[:, :R]), wdt, O.OUT_DECAY_MOD, 2)
+    yo_ref, h_ref = O.block_scan(xs.reshape(m, 1, D), dm.reshape(m, 1, D), xp.reshape(m, 1, W), R,
+                                 z.reshape(m, 1, 2 * D), D, base, 15, 13, h_state=h0)
+    hg = T(h0)
+    yo = T(np.zeros((m, D), np.int8))
+    ops.xpart_dt_scan_step(T(xq), 5, R, T(wdt), 2, T(xs), T(z), D, T(base), 15, 13, hg, yo)
+    assert np.array_equal(H(yo), yo_ref[:, 0])
+    assert np.array_equal(H(hg), h_ref)
+
+
 @pytest.mark.parametrize("m,k", [(2, 15), (64, 15), (5, 15), (8, 12), (3, 17)])
 def test_batched_scan_step_full_range(cuda, m, k):
     """The batched scan step (two tokens per block: 24-bit multiplies at decay
