@@ -124,6 +124,21 @@ __device__ __forceinline__ void update16_cs(int32_t &h, int n2, int b, int x, in
     ylo += pl;
 }
 
+// update16_cs for a lane's first state: its products start y's two partial
+// sums (yhi = C*H, ylo = C*L, one word-select multiply each) instead of
+// accumulating onto zeroed sums
+__device__ __forceinline__ void update16_cs_first(int32_t &h, int n2, int b, int x, int cs, int &yhi, int &ylo) {
+    int dh = __mul24(h >> 16, n2);
+    asm("" : "+v"(dh));
+    const uint32_t cl = __umul24((uint32_t)h & 0xffffu, (uint32_t)n2);
+    h = mad24_sat(b, x, dh + (int)(cl >> 16));
+    // (kept out of mad formation: a v_mad_i32_i24 with the first DPP stage
+    // would need H and L shifted and masked out first)
+    yhi = __mul24(cs >> 16, h >> 16);
+    ylo = __mul24(cs >> 16, h & 0xffff);
+    asm("" : "+v"(yhi), "+v"(ylo));
+}
+
 // Exact floor(sqrt(v)) for v < 2^62 (host and device): a float estimate
 // refined by integer correction steps.
 __host__ __device__ __forceinline__ uint64_t isqrt64(uint64_t v) {

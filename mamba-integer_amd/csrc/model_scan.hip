@@ -103,18 +103,28 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     constexpr int BCPER = (BCPIECES + NT - 1) / NT;
     static_assert(N % 16 == 0 && CH % 16 == 0 && (S == 1 || S == 2 || S % 4 == 0), "state split");
     static_assert(!MIX || N / G2 == 1 || N / G2 == 2 || (N / G2) % 4 == 0, "state split");
+    // The mixed block (its CU to itself, 160 KB of LDS) reduces each step's y
+    // partials only within quads of lanes and leaves the channel's G/4 quad
+    // sums in LDS for the chunk epilogue to add (two DPP stages a step fewer
+    // for 16 lanes, one for 8), and stages xd as int32 (no unpacking per
+    // step).  The other layouts reduce over all G lanes and stage xd as int16.
+    constexpr int PA = MIX && G >= 8 ? G / 4 : 1;     // y partials per channel, layout G
+    constexpr int PB = MIX && G2 >= 8 ? G2 / 4 : 1;   // and layout G2
+    constexpr int YW = CHA * PA + (CH - CHA) * PB;    // y partials per step
+    using XdT = std::conditional_t<MIX, int32_t, int16_t>;
     // staging buffers: two (chunk c + 1 is staged while chunk c's epilogue runs)
     // where they fit in 64 KB of LDS (160 KB for a mixed block), else one
-    constexpr int kStage = 2 * CH * XP + CH * XP * 2 + 2 * kMTC * N * 4;
+    constexpr int kStage = 2 * CH * XP + CH * XP * (int)sizeof(XdT) + 2 * kMTC * N * 4;
     constexpr int kLds = MIX ? 163840 : 65536;   // a mixed block has its CU to itself
-    constexpr int NB = 2 * kStage + kMTC * CH * 9 + 297 * 4 <= kLds ? 2 : 1;
-    static_assert(NB * kStage + kMTC * CH * 9 + 297 * 4 <= kLds, "LDS budget");
+    constexpr int kFixed = kMTC * (YW * 8 + CH) + 297 * 4;
+    constexpr int NB = 2 * kStage + kFixed <= kLds ? 2 : 1;
+    static_assert(NB * kStage + kFixed <= kLds, "LDS budget");
 
     __shared__ __align__(16) int8_t s_x[NB][2][CH][XP];    // 2*dm, z (channel-major)
-    __shared__ __align__(16) int16_t s_xd[NB][CH][XP];      // rshr(xs * dt(dm), 10), |xd| <= 813
+    __shared__ __align__(16) XdT s_xd[NB][CH][XP];          // rshr(xs * dt(dm), 10), |xd| <= 813
     __shared__ __align__(16) int32_t s_b[NB][kMTC][N];
     __shared__ __align__(16) int32_t s_c[NB][kMTC][N];
-    __shared__ __align__(16) int2 s_y[kMTC][CH];            // (yhi, ylo) per step and channel
+    __shared__ __align__(16) int2 s_y[kMTC][YW];            // (yhi, ylo) partials per step
     __shared__ __align__(16) int8_t s_o[kMTC][CH];
     __shared__ int32_t s_dt[41];
     __shared__ int32_t s_gate[256];
@@ -129,6 +139,8 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     const int b = blockIdx.y;
     const int p = p0 + ch;
     const bool active = p < a.D;
+    // this lane's y partial: its channel's slot plus its quad (g / 4 < G / 4)
+    const int yslot = second ? CHA * PA + (ch - CHA) * PB + g / 4 : ch * PA + (PA > 1 ? g / 4 : 0);
 
     for (int i = tid; i < 41; i += NT) s_dt[i] = dt_q16(i - 20);
     for (int i = tid; i < 256; i += NT) s_gate[i] = gate_q15(i - 128);
@@ -190,7 +202,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
                 const int dmv = clamp32(sb(wd[e >> 2], e & 3), -20, 20);
                 s_x[bf][0][c16 * 16 + e][tt] = (int8_t)(2 * dmv);  // the decay takes 2n
                 s_x[bf][1][c16 * 16 + e][tt] = (int8_t)sb(wz[e >> 2], e & 3);
-                s_xd[bf][c16 * 16 + e][tt] = (int16_t)((sb(wx[e >> 2], e & 3) * s_dt[dmv + 20] + 512) >> 10);
+                s_xd[bf][c16 * 16 + e][tt] = (XdT)((sb(wx[e >> 2], e & 3) * s_dt[dmv + 20] + 512) >> 10);
             }
         }
         for (int j = 0; j < BCPER; ++j) {
@@ -228,16 +240,16 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         }
     };
     // the recurrence of this lane's SS states for one step: returns the exact
-    // int32 partials (sum C*H, sum C*L) of y over the lane's states
+    // int32 partials (sum C*H, sum C*L) of y over the lane's states (the first
+    // state's products start the sums: no zeroed accumulator)
     auto update = [&](int xd, int dm2, const auto &bv, const auto &cs, int &yhi, int &ylo, auto clamp_tag) {
         constexpr bool CLAMP = decltype(clamp_tag)::value;
         constexpr int SS = sizeof(bv) / sizeof(int);
-        yhi = 0;
-        ylo = 0;
 #pragma unroll
         for (int s = 0; s < SS; ++s) {
             const int n2 = CLAMP ? clamp32(base2[s] + dm2, 0, 64000) : base2[s] + dm2;
-            update16_cs(h[s], n2, bv[s], xd, cs[s], yhi, ylo);
+            if (s == 0) update16_cs_first(h[s], n2, bv[s], xd, cs[s], yhi, ylo);
+            else update16_cs(h[s], n2, bv[s], xd, cs[s], yhi, ylo);
         }
     };
 
@@ -258,6 +270,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
 
         auto run_chunk = [&](auto clamp_tag, auto g_tag) {
             constexpr int GG = decltype(g_tag)::value, SS = N / GG;
+            constexpr int GQ = MIX && GG >= 8 ? 4 : GG;   // lanes a step's y is reduced over
             const int t4n = tn & ~3;  // steps in whole groups of four
             // groups of four steps: the next group's coefficients are read from
             // LDS while this group's recurrence runs, and the y partials of the
@@ -268,15 +281,22 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) load_bc(cur, min(t4 + 4 + tt, kMTC - 1), bn[tt], cn[tt]);
                 const uint32_t dw = *reinterpret_cast<const uint32_t *>(&s_x[cur][0][ch][t4]);
-                const uint2 xw = *reinterpret_cast<const uint2 *>(&s_xd[cur][ch][t4]);
-                const int xdv[4] = {(int)(int16_t)xw.x, (int)xw.x >> 16, (int)(int16_t)xw.y, (int)xw.y >> 16};
+                int xdv[4];
+                if constexpr (MIX) {
+                    const int4 xw = *reinterpret_cast<const int4 *>(&s_xd[cur][ch][t4]);
+                    xdv[0] = xw.x; xdv[1] = xw.y; xdv[2] = xw.z; xdv[3] = xw.w;
+                } else {
+                    const uint2 xw = *reinterpret_cast<const uint2 *>(&s_xd[cur][ch][t4]);
+                    xdv[0] = (int)(int16_t)xw.x; xdv[1] = (int)xw.x >> 16;
+                    xdv[2] = (int)(int16_t)xw.y; xdv[3] = (int)xw.y >> 16;
+                }
                 int y[8];
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt)
                     update(xdv[tt], sb(dw, tt), bq[tt], cq[tt], y[2 * tt], y[2 * tt + 1], clamp_tag);
-                msum_all<GG>(y);
+                msum_all<GQ>(y);
 #pragma unroll
-                for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][ch] = make_int2(y[2 * tt], y[2 * tt + 1]);
+                for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][yslot] = make_int2(y[2 * tt], y[2 * tt + 1]);
             };
             int b0[4][SS], c0[4][SS], b1[4][SS], c1[4][SS];
 #pragma unroll
@@ -291,8 +311,8 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
                 const int dm2 = s_x[cur][0][ch][t];
                 int y[2];
                 update(s_xd[cur][ch][t], dm2, bv, cv, y[0], y[1], clamp_tag);
-                msum_all<GG>(y);
-                s_y[t][ch] = make_int2(y[0], y[1]);  // all G lanes hold the same sums: no branch
+                msum_all<GQ>(y);
+                s_y[t][yslot] = make_int2(y[0], y[1]);  // the lanes of a quad hold the same sums: no branch
             }
         };
         using GA = std::integral_constant<int, G>;
@@ -313,7 +333,18 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         for (int i = tid; i < kMTC * CH; i += NT) {
             const int tt = i / CH, cc = i % CH;
             if (tt < tn) {
-                const int2 yv = s_y[tt][cc];
+                // the channel's quad partials (one where the lanes reduced fully)
+                const int np = cc < CHA ? PA : PB;
+                const int y0 = cc < CHA ? cc * PA : CHA * PA + (cc - CHA) * PB;
+                int2 yv = s_y[tt][y0];
+#pragma unroll
+                for (int q = 1; q < (PA > PB ? PA : PB); ++q) {
+                    if (q < np) {
+                        const int2 w = s_y[tt][y0 + q];
+                        yv.x += w.x;
+                        yv.y += w.y;
+                    }
+                }
                 const int32_t y32 = sat32_64(((int64_t)yv.x << 16) + yv.y);
                 const int zv = s_x[cur][1][cc][tt];
                 const int32_t gt = s_gate[zv + 128];
