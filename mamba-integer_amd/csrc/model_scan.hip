@@ -104,13 +104,15 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     static_assert(N % 16 == 0 && CH % 16 == 0 && (S == 1 || S == 2 || S % 4 == 0), "state split");
     static_assert(!MIX || N / G2 == 1 || N / G2 == 2 || (N / G2) % 4 == 0, "state split");
     // The mixed block (its CU to itself, 160 KB of LDS) reduces each step's y
-    // partials only within quads of lanes and leaves the channel's G/4 quad
-    // sums in LDS for the chunk epilogue to add (two DPP stages a step fewer
-    // for 16 lanes, one for 8), and stages xd as int32 (no unpacking per
+    // partials only within quads of lanes and leaves the channel's quad sums
+    // in LDS, PW slots a channel (slots a layout of G/4 < PW quads never
+    // writes stay zero), for the chunk epilogue to add: two DPP stages a step
+    // fewer for 16 lanes, one for 8.  It stages xd as int32 (no unpacking per
     // step).  The other layouts reduce over all G lanes and stage xd as int16.
-    constexpr int PA = MIX && G >= 8 ? G / 4 : 1;     // y partials per channel, layout G
+    constexpr int PA = MIX && G >= 8 ? G / 4 : 1;     // quads of a channel, layout G
     constexpr int PB = MIX && G2 >= 8 ? G2 / 4 : 1;   // and layout G2
-    constexpr int YW = CHA * PA + (CH - CHA) * PB;    // y partials per step
+    constexpr int PW = PA > PB ? PA : PB;             // y partial slots per channel
+    constexpr int YW = CH * PW;                       // y partials per step
     using XdT = std::conditional_t<MIX, int32_t, int16_t>;
     // staging buffers: two (chunk c + 1 is staged while chunk c's epilogue runs)
     // where they fit in 64 KB of LDS (160 KB for a mixed block), else one
@@ -139,8 +141,11 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     const int b = blockIdx.y;
     const int p = p0 + ch;
     const bool active = p < a.D;
-    // this lane's y partial: its channel's slot plus its quad (g / 4 < G / 4)
-    const int yslot = second ? CHA * PA + (ch - CHA) * PB + g / 4 : ch * PA + (PA > 1 ? g / 4 : 0);
+    // this lane's y partial: its channel's slots, its quad (g / 4 < PW)
+    const int yslot = ch * PW + (PW > 1 ? g / 4 : 0);
+    // the chunk epilogue's channel and first step for this thread
+    constexpr int TPC = NT / CH;
+    const int ecc = tid % CH, et1 = tid / CH;
 
     for (int i = tid; i < 41; i += NT) s_dt[i] = dt_q16(i - 20);
     for (int i = tid; i < 256; i += NT) s_gate[i] = gate_q15(i - 128);
@@ -202,7 +207,8 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
                 const int dmv = clamp32(sb(wd[e >> 2], e & 3), -20, 20);
                 s_x[bf][0][c16 * 16 + e][tt] = (int8_t)(2 * dmv);  // the decay takes 2n
                 s_x[bf][1][c16 * 16 + e][tt] = (int8_t)sb(wz[e >> 2], e & 3);
-                s_xd[bf][c16 * 16 + e][tt] = (XdT)((sb(wx[e >> 2], e & 3) * s_dt[dmv + 20] + 512) >> 10);
+                // |x| <= 128, dt <= 6554: a 24-bit product
+                s_xd[bf][c16 * 16 + e][tt] = (XdT)((__mul24(sb(wx[e >> 2], e & 3), s_dt[dmv + 20]) + 512) >> 10);
             }
         }
         for (int j = 0; j < BCPER; ++j) {
@@ -259,6 +265,14 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     // of the chunk after next.  One buffer: chunk c+1 is staged after the
     // stores, behind a third barrier.
     const int nchunks = (a.L + kMTC - 1) / kMTC;
+    if constexpr (PA < PW) {
+        // the layout-G channels' slots [PA, PW), never written by their lanes
+        constexpr int kz = CHA * (PW - PA);
+        for (int i = tid; i < kMTC * kz; i += NT) {
+            const int tt = i / kz, r = i - tt * kz;
+            s_y[tt][(r / (PW - PA)) * PW + PA + r % (PW - PA)] = make_int2(0, 0);
+        }
+    }
     prefetch(0);
     stash(0);
     if (nchunks > 1) prefetch(kMTC);
@@ -329,29 +343,32 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         if constexpr (NB == 2)
             if (cidx + 1 < nchunks) stash(cur ^ 1);
         __syncthreads();
-        // epilogue of the chunk: y = sat32(yhi*2^16 + ylo), gate, requant
-        for (int i = tid; i < kMTC * CH; i += NT) {
-            const int tt = i / CH, cc = i % CH;
-            if (tt < tn) {
-                // the channel's quad partials (one where the lanes reduced fully)
-                const int np = cc < CHA ? PA : PB;
-                const int y0 = cc < CHA ? cc * PA : CHA * PA + (cc - CHA) * PB;
-                int2 yv = s_y[tt][y0];
+        // epilogue of the chunk: y = sat32(yhi*2^16 + ylo), gate, requant; a
+        // thread keeps one channel and walks the chunk's steps t1, t1 + TPC, ...
+        if (tid < TPC * CH) {
+            for (int tt = et1; tt < tn; tt += TPC) {
+                int yh = 0, yl = 0;
 #pragma unroll
-                for (int q = 1; q < (PA > PB ? PA : PB); ++q) {
-                    if (q < np) {
-                        const int2 w = s_y[tt][y0 + q];
-                        yv.x += w.x;
-                        yv.y += w.y;
-                    }
+                for (int q = 0; q < PW; ++q) {
+                    const int2 w = s_y[tt][ecc * PW + q];
+                    yh += w.x;
+                    yl += w.y;
                 }
-                const int32_t y32 = sat32_64(((int64_t)yv.x << 16) + yv.y);
-                const int zv = s_x[cur][1][cc][tt];
-                const int32_t gt = s_gate[zv + 128];
-                // floor(y32 * gt / 2^15) with 32-bit pieces: y32 = yh*2^15 + yl, 0 <= yl < 2^15
-                const int32_t yh = y32 >> 15, yl = y32 & 0x7fff;
-                const int32_t yg = yh * gt + (int32_t)(((uint32_t)yl * (uint32_t)gt) >> 15);
-                s_o[tt][cc] = (int8_t)clamp64(rshr64(yg, a.s_y), -127, 127);
+                // y = hi * 2^16 + (yl mod 2^16) exactly (|yh|, |yl| < 2^28), and
+                // y fits int32 exactly when hi does in 16 bits
+                const int hi = yh + (yl >> 16);
+                const int hc = clamp32(hi, -32768, 32767);
+                int32_t y32 = (int32_t)(((uint32_t)hc << 16) | ((uint32_t)yl & 0xffffu));
+                if (hi != hc) y32 = hi > 0 ? INT32_MAX : INT32_MIN;
+                const int zv = s_x[cur][1][ecc][tt];
+                const int32_t gt = s_gate[zv + 128];   // in [0, 2^15]
+                // floor(y32 * gt / 2^15) with 24-bit products: y32 = yh15 * 2^15 +
+                // yl15, |yh15| <= 2^16, 0 <= yl15 < 2^15 (|result| <= |y32|)
+                const int32_t yh15 = y32 >> 15, yl15 = y32 & 0x7fff;
+                const int32_t yg = __mul24(yh15, gt) + (int32_t)(__umul24((uint32_t)yl15, (uint32_t)gt) >> 15);
+                // rshr(yg, s_y) exactly in 32 bits: floor(yg / 2^s) plus bit s-1
+                const int32_t qv = a.s_y > 0 ? (yg >> a.s_y) + ((yg >> (a.s_y - 1)) & 1) : yg;
+                s_o[tt][ecc] = (int8_t)clamp32(qv, -127, 127);
             }
         }
         __syncthreads();
