@@ -116,20 +116,36 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
     using XdT = std::conditional_t<MIX, int32_t, int16_t>;
     // staging buffers: two (chunk c + 1 is staged while chunk c's epilogue runs)
     // where they fit in 64 KB of LDS (160 KB for a mixed block), else one
-    constexpr int kStage = 2 * CH * XP + CH * XP * (int)sizeof(XdT) + 2 * kMTC * N * 4;
+    constexpr int kStage = 2 * CH * XP + CH * XP * (int)sizeof(XdT) + 2 * (kMTC + 4) * N * 4;
     constexpr int kLds = MIX ? 163840 : 65536;   // a mixed block has its CU to itself
     constexpr int kFixed = kMTC * (YW * 8 + CH) + 297 * 4;
     constexpr int NB = 2 * kStage + kFixed <= kLds ? 2 : 1;
     static_assert(NB * kStage + kFixed <= kLds, "LDS budget");
 
-    __shared__ __align__(16) int8_t s_x[NB][2][CH][XP];    // 2*dm, z (channel-major)
-    __shared__ __align__(16) XdT s_xd[NB][CH][XP];          // rshr(xs * dt(dm), 10), |xd| <= 813
-    __shared__ __align__(16) int32_t s_b[NB][kMTC][N];
-    __shared__ __align__(16) int32_t s_c[NB][kMTC][N];
-    __shared__ __align__(16) int2 s_y[kMTC][YW];            // (yhi, ylo) partials per step
-    __shared__ __align__(16) int8_t s_o[kMTC][CH];
-    __shared__ int32_t s_dt[41];
-    __shared__ int32_t s_gate[256];
+    // One LDS block with the arrays every step reads first, so their addresses
+    // stay below 64 KB, within a ds instruction's immediate offset (placed
+    // after the 98 KB of y partials, each look-ahead read needed an add).
+    // B and C have four rows past the chunk: the last group's look-ahead
+    // reads them and discards what it read, so the reads need no clamped row.
+    struct Smem {
+        int32_t b[NB][kMTC + 4][N];
+        int32_t c[NB][kMTC + 4][N];
+        int8_t x[NB][2][CH][XP];    // 2*dm, z (channel-major)
+        XdT xd[NB][CH][XP];         // rshr(xs * dt(dm), 10), |xd| <= 813
+        int2 y[kMTC][YW];           // (yhi, ylo) partials per step
+        int8_t o[kMTC][CH];
+        int32_t dt[41];
+        int32_t gate[256];
+    };
+    __shared__ __align__(16) Smem sm;
+    auto &s_b = sm.b;
+    auto &s_c = sm.c;
+    auto &s_x = sm.x;
+    auto &s_xd = sm.xd;
+    auto &s_y = sm.y;
+    auto &s_o = sm.o;
+    auto &s_dt = sm.dt;
+    auto &s_gate = sm.gate;
 
     const int tid = threadIdx.x;
     const bool second = MIX && tid >= NTA;                     // wave-uniform
@@ -293,7 +309,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
             auto group = [&](int t4, const int (&bq)[4][SS], const int (&cq)[4][SS], int (&bn)[4][SS],
                              int (&cn)[4][SS]) {
 #pragma unroll
-                for (int tt = 0; tt < 4; ++tt) load_bc(cur, min(t4 + 4 + tt, kMTC - 1), bn[tt], cn[tt]);
+                for (int tt = 0; tt < 4; ++tt) load_bc(cur, t4 + 4 + tt, bn[tt], cn[tt]);
                 const uint32_t dw = *reinterpret_cast<const uint32_t *>(&s_x[cur][0][ch][t4]);
                 int xdv[4];
                 if constexpr (MIX) {
