@@ -302,16 +302,13 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
             constexpr int GG = decltype(g_tag)::value, SS = N / GG;
             constexpr int GQ = MIX && GG >= 8 ? 4 : GG;   // lanes a step's y is reduced over
             const int t4n = tn & ~3;  // steps in whole groups of four
-            // groups of four steps: the next group's coefficients are read from
-            // LDS while this group's recurrence runs, and the y partials of the
-            // four steps are reduced together afterwards; two register sets of
-            // coefficients alternate between the groups of a pair
-            auto group = [&](int t4, const int (&bq)[4][SS], const int (&cq)[4][SS], int (&bn)[4][SS],
-                             int (&cn)[4][SS]) {
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) load_bc(cur, t4 + 4 + tt, bn[tt], cn[tt]);
-                const uint32_t dw = *reinterpret_cast<const uint32_t *>(&s_x[cur][0][ch][t4]);
-                int xdv[4];
+            // groups of four steps: the next group's coefficients, 2*dm and xd
+            // are read from LDS while this group's recurrence runs, and the y
+            // partials of the four steps are reduced together afterwards; two
+            // register sets alternate between the groups of a pair (reads past
+            // the chunk land in the staging arrays' four padding steps)
+            auto load_dx = [&](int t4, uint32_t &dw, int (&xdv)[4]) {
+                dw = *reinterpret_cast<const uint32_t *>(&s_x[cur][0][ch][t4]);
                 if constexpr (MIX) {
                     const int4 xw = *reinterpret_cast<const int4 *>(&s_xd[cur][ch][t4]);
                     xdv[0] = xw.x; xdv[1] = xw.y; xdv[2] = xw.z; xdv[3] = xw.w;
@@ -320,20 +317,28 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
                     xdv[0] = (int)(int16_t)xw.x; xdv[1] = (int)xw.x >> 16;
                     xdv[2] = (int)(int16_t)xw.y; xdv[3] = (int)xw.y >> 16;
                 }
+            };
+            auto group = [&](int t4, const int (&bq)[4][SS], const int (&cq)[4][SS], const uint32_t dq,
+                             const int (&xq)[4], int (&bn)[4][SS], int (&cn)[4][SS], uint32_t &dn, int (&xn)[4]) {
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) load_bc(cur, t4 + 4 + tt, bn[tt], cn[tt]);
+                load_dx(t4 + 4, dn, xn);
                 int y[8];
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt)
-                    update(xdv[tt], sb(dw, tt), bq[tt], cq[tt], y[2 * tt], y[2 * tt + 1], clamp_tag);
+                    update(xq[tt], sb(dq, tt), bq[tt], cq[tt], y[2 * tt], y[2 * tt + 1], clamp_tag);
                 msum_all<GQ>(y);
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][yslot] = make_int2(y[2 * tt], y[2 * tt + 1]);
             };
-            int b0[4][SS], c0[4][SS], b1[4][SS], c1[4][SS];
+            int b0[4][SS], c0[4][SS], b1[4][SS], c1[4][SS], x0[4], x1[4];
+            uint32_t d0, d1;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) load_bc(cur, tt, b0[tt], c0[tt]);
+            load_dx(0, d0, x0);
             for (int t4 = 0; t4 < t4n; t4 += 8) {
-                group(t4, b0, c0, b1, c1);
-                if (t4 + 4 < t4n) group(t4 + 4, b1, c1, b0, c0);
+                group(t4, b0, c0, d0, x0, b1, c1, d1, x1);
+                if (t4 + 4 < t4n) group(t4 + 4, b1, c1, d1, x1, b0, c0, d0, x0);
             }
             for (int t = t4n; t < tn; ++t) {
                 int bv[SS], cv[SS];
