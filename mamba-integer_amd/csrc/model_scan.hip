@@ -367,7 +367,10 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
         // epilogue of the chunk: y = sat32(yhi*2^16 + ylo), gate, requant; a
         // thread keeps one channel and walks the chunk's steps t1, t1 + TPC, ...
         if (tid < TPC * CH) {
-            for (int tt = et1; tt < tn; tt += TPC) {
+#pragma unroll
+            for (int k = 0; k < (kMTC + TPC - 1) / TPC; ++k) {
+                const int tw = et1 + k * TPC;
+                const int tt = min(tw, kMTC - 1);   // reads stay in the chunk; the store below checks tw
                 int yh = 0, yl = 0;
 #pragma unroll
                 for (int q = 0; q < PW; ++q) {
@@ -389,7 +392,7 @@ __global__ __launch_bounds__(NT) void model_scan_kernel(MScanArgs a) {
                 const int32_t yg = __mul24(yh15, gt) + (int32_t)(__umul24((uint32_t)yl15, (uint32_t)gt) >> 15);
                 // rshr(yg, s_y) exactly in 32 bits: floor(yg / 2^s) plus bit s-1
                 const int32_t qv = a.s_y > 0 ? (yg >> a.s_y) + ((yg >> (a.s_y - 1)) & 1) : yg;
-                s_o[tt][ecc] = (int8_t)clamp32(qv, -127, 127);
+                if (tw < tn) s_o[tw][ecc] = (int8_t)clamp32(qv, -127, 127);
             }
         }
         __syncthreads();
