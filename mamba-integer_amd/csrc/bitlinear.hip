@@ -45,6 +45,10 @@ struct RowStat {
     int64_t s1, s2;
 };
 
+// pointer types of global_load_lds (LDS-DMA) operands
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
 // The residual increment of one accumulator: rshr(clamp(acc, +-res_clamp) * res_mult, res_shift).
 __device__ __forceinline__ int64_t residual_delta(const GemmArgs &g, int32_t acc) {
     const int32_t c = clamp32(acc, -g.res_clamp, g.res_clamp);
@@ -493,6 +497,394 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     gemm_tile<MI_OUT_INT8, true, kGemmNI, true>(g, cv);
 }
 
+// ------------------------------------------- prefill GEMM, 256 x 128 tiles
+// gemm32_kernel: the large-shape form of the prefill GEMM on
+// v_mfma_i32_32x32x32_i8.  A 256(n) x 128(m) block tile, 4 waves stacked along
+// n, each 64 weight rows x 128 tokens (2 x 4 accumulators of 32 x 32), so an
+// activation fragment read from LDS feeds 2 MFMAs of 32x32x32 (half the LDS
+// bytes per operation of the 32-row waves of gemm_kernel) and an unpacked
+// weight fragment feeds 4.
+//
+// MFMA operands (C^T = W * A^T): lane l holds row l%32 of a 32-row fragment
+// and 16 k of half h = l/32.  The k order inside a 128-deep stage is free as
+// long as both operands agree: in k-step s (0..3) half h covers stage bytes
+// [16q, 16q + 16) with q = 4h + s, so the 4 words of a weight row that half h
+// needs in a stage are one 16-byte run (words 4h..4h+3).  Result register r of
+// lane l is feature 8(r/4) + 4h + r%4 of its fragment, token l%32.
+//
+// Staging: every global load is a global_load_lds_dwordx4 (LDS DMA, no VGPRs)
+// into a ring of three stages, issued two stages ahead of the stage being
+// multiplied; a wave waits only for its own loads of that stage (vmcnt counts
+// them in order: 6 a stage) and a bare s_barrier then makes all waves' loads
+// visible (__syncthreads would wait for every load in flight).  The activation
+// tile is 128 rows x 128 bytes with 16-byte segment q of row r at position
+// q ^ ((r >> 1) & 7): lane i of a DMA instruction lands at byte 16i, so the
+// lane picks the segment that belongs there, and the fragment reads (rows
+// l%32, one segment) fall in distinct bank groups.  Each wave's weight words
+// go to its own LDS region and are read back by the lanes that loaded them.
+//
+// Requires K % 128 == 0, N % 256 == 0, 16-byte aligned a / w with lda % 16 == 0.
+// Rows past M read row M - 1 (the conv x-half's halo rows before 0 read row 0)
+// and their outputs are not stored.  Epilogues: int8 requant through a
+// swizzled LDS tile and 16-byte row pieces; RESIDUAL read-modify-write of
+// 16-byte int32 vectors with row statistics; the conv form as gemm_conv_kernel
+// (x-half tiles of 128 staged rows storing the last 125).
+constexpr int kG2BN = 256, kG2BM = 128, kG2BK = 128, kG2Ring = 3;
+constexpr int kG2ConvRows = kG2BM - 3;
+static_assert(kG2BM == kBM, "the conv grid counts z-half tiles with kBM");
+
+struct G2Smem {
+    int8_t a[kG2Ring][kG2BM * kG2BK];   // 3 x 16 KB; the int8 output tile reuses a[0..1]
+    uint32_t w[kG2Ring][4][2][256];     // [stage][wave][fragment][lane * 4 + word]
+};
+
+__device__ __forceinline__ int g2_aoff(int r, int q) { return r * kG2BK + 16 * (q ^ ((r >> 1) & 7)); }
+// int8 output tile [128][256]: 16-byte granule gr of row m at gr ^ (m & 15)
+__device__ __forceinline__ int g2_ooff(int m, int nb) { return m * kG2BN + ((((nb >> 4) ^ (m & 15)) << 4) | (nb & 15)); }
+
+// word 3 of a raw buffer resource (32-bit data format, no swizzle)
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ v16i mfma32_i8(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+template <int KIND, bool CONV>
+__device__ __forceinline__ void gemm32_tile(const GemmArgs &g, const ConvArgs &cv) {
+    static_assert(KIND == MI_OUT_INT8 || KIND == MI_OUT_RESIDUAL, "int8 or residual output");
+    __shared__ __align__(16) G2Smem sm;
+    const int tid = threadIdx.x, lane = tid & 63, wid = wave_id();
+    const int l32 = lane & 31, h = lane >> 5;
+
+    int m0, n0;
+    bool xblk = false;   // block-uniform: a conv x-half tile
+    {
+        auto xcd_run = [](int b, int T) { return (T & 7) == 0 ? (b & 7) * (T >> 3) + (b >> 3) : b; };
+        int t = (int)blockIdx.x;
+        if constexpr (CONV) {
+            const int zb = (int)gridDim.x - cv.x_blocks;
+            t = (cv.x_blocks & 7) == 0 ? (t < cv.x_blocks ? xcd_run(t, cv.x_blocks) : cv.x_blocks + xcd_run(t - cv.x_blocks, zb))
+                                       : t;
+            if (t < cv.x_blocks) {
+                int mt, nt;
+                grouped_tile(t, (g.M + kG2ConvRows - 1) / kG2ConvRows, cv.D / kG2BN, mt, nt);
+                xblk = true;
+                m0 = mt * kG2ConvRows - 3;
+                n0 = nt * kG2BN;
+            } else {
+                int mt, nt;
+                grouped_tile(t - cv.x_blocks, (g.M + kG2BM - 1) / kG2BM, (g.N - cv.D) / kG2BN, mt, nt);
+                m0 = mt * kG2BM;
+                n0 = cv.D + nt * kG2BN;
+            }
+        } else {
+            t = xcd_run(t, (int)gridDim.x);
+            int mt, nt;
+            grouped_tile(t, (g.M + kG2BM - 1) / kG2BM, g.N / kG2BN, mt, nt);
+            m0 = mt * kG2BM;
+            n0 = nt * kG2BN;
+        }
+    }
+    const int nk = g.K / kG2BK;
+
+    // DMA sources.  Activation instruction j of wave wid fills tile rows
+    // 8 (4 wid + j) .. +7: lane i takes row + i / 8 and the segment that lands
+    // at position i % 8.  Weight instruction f: row n0 + 64 wid + 32 f + l32,
+    // words 4h .. 4h + 3 of the stage.
+    // Buffer loads (buffer_load_dwordx4 ... lds), byte offsets below 2^31:
+    // the compiler counts their LDS writes with vmcnt only, so the fragment
+    // reads keep exact lgkmcnt waits (with the FLAT-encoded global_load_lds in
+    // flight it waits for lgkmcnt(0), i.e. for the DMA).
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(g.a), 0, (int)min((int64_t)g.M * g.lda, (int64_t)INT32_MAX), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t *>(g.w), 0, (int)min((int64_t)g.N * g.kw * 4, (int64_t)INT32_MAX), kBufferRsrcWord3);
+    uint32_t aoffs[4], woffs[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 8 * (4 * wid + j) + (lane >> 3);
+        const int q = (lane & 7) ^ ((r >> 1) & 7);
+        int m = min(m0 + r, g.M - 1);
+        if constexpr (CONV) m = max(m, 0);
+        aoffs[j] = (uint32_t)((int64_t)m * g.lda + 16 * q);
+    }
+#pragma unroll
+    for (int f = 0; f < 2; ++f) woffs[f] = (uint32_t)(((int64_t)(n0 + 64 * wid + 32 * f + l32) * g.kw + 4 * h) * 4);
+    auto issue = [&](int kt) {
+        const int b = kt % kG2Ring;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t *)&sm.a[b][(4 * wid + j) * 1024], 16, aoffs[j],
+                                                     (uint32_t)(kt * kG2BK), 0, 0);
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *)&sm.w[b][wid][f][0], 16, woffs[f],
+                                                     (uint32_t)(kt * (kG2BK / 4)), 0, 0);
+    };
+
+    v16i acc[2][4];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[f][j][r] = 0;
+
+    // fragment read offsets: row l32 (+ 32 jj), segment 4h + s
+    int aoff[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) aoff[s] = g2_aoff(l32, 4 * h + s);
+
+    // Stage kt runs 4 k-steps of 8 MFMAs.  Each k-step's MFMAs are
+    // interleaved (sched_group_barrier) with the fragment reads and weight
+    // unpack of the next k-step, so one wave alone keeps its SIMD's MFMA pipe
+    // fed.  After the fragment reads of step 3 (issued in step 2) every wave
+    // waits for its own loads of stage kt + 1 and meets the others at one
+    // barrier: stage kt + 1 is then visible and stage kt's buffer free, so step
+    // 3 refills that buffer with stage kt + 3 and reads stage kt + 1's weights
+    // and first fragments under its MFMAs (no LDS latency exposed at a stage
+    // boundary; loads run 2.5 stages ahead).
+    auto read_w = [&](int kt, v4i (&wv)[2]) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f) wv[f] = *reinterpret_cast<const v4i *>(&sm.w[kt % kG2Ring][wid][f][lane * 4]);
+    };
+    auto read_frags = [&](int kt, int s, v4i (&fr)[4]) {
+        const int8_t *abase = &sm.a[kt % kG2Ring][0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fr[j] = *reinterpret_cast<const v4i *>(abase + j * 32 * kG2BK + aoff[s]);
+    };
+    auto mfmas = [&](const v4i (&u)[2], const v4i (&fr)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[0][j] = mfma32_i8(u[0], fr[j], acc[0][j]);
+            acc[1][j] = mfma32_i8(u[1], fr[j], acc[1][j]);
+        }
+    };
+    v4i fa[4], u[2], wv[2];
+    issue(0);
+    if (nk > 1) issue(1);
+    if (nk > 2) issue(2);
+    if (nk > 2)
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else if (nk > 1)
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_w(0, wv);
+    read_frags(0, 0, fa);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) u[f] = unpack16((uint32_t)wv[f][0]);
+
+    // DMA: refill with stage kt + 3; NEXT: a stage kt + 1 follows
+    auto stage = [&](int kt, auto dma, auto next) {
+        constexpr bool DMA = decltype(dma)::value, NEXT = decltype(next)::value;
+        v4i wn[2];   // stage kt + 1's weight words (this wave's own loads: no barrier needed)
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            if (NEXT && s == 2) {
+                if (kt + 2 < nk)
+                    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            v4i fn[4], un[2];
+            read_frags(kt, s + 1, fn);
+            if (NEXT && s == 2) read_w(kt + 1, wn);
+#pragma unroll
+            for (int f = 0; f < 2; ++f) un[f] = unpack16((uint32_t)wv[f][s + 1]);
+            mfmas(u, fa);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // 1 MFMA
+                if (NEXT && s == 2 && i < 2)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                   // 2 LDS reads
+                else if (i < 4)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                   // 1 LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                       // 3 VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fa[j] = fn[j];
+            u[0] = un[0];
+            u[1] = un[1];
+        }
+        if constexpr (NEXT) {
+            // step 3's fragments have landed; every wave's loads of stage kt + 1 too after the barrier
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            v4i fn[4], un[2];
+            if constexpr (DMA) issue(kt + 3);
+            read_frags(kt + 1, 0, fn);
+#pragma unroll
+            for (int f = 0; f < 2; ++f) un[f] = unpack16((uint32_t)wn[f][0]);
+            mfmas(u, fa);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // 1 MFMA
+                if (DMA && i < 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);     // 1 DMA load
+                if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);            // 1 LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                       // 3 VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fa[j] = fn[j];
+            u[0] = un[0];
+            u[1] = un[1];
+            wv[0] = wn[0];
+            wv[1] = wn[1];
+        } else {
+            mfmas(u, fa);
+        }
+    };
+    int kt = 0;
+    for (; kt + 3 < nk; ++kt) stage(kt, std::true_type{}, std::true_type{});
+    for (; kt + 1 < nk; ++kt) stage(kt, std::false_type{}, std::true_type{});
+    stage(kt, std::false_type{}, std::false_type{});
+    // acc[f][j][4c + i]: feature n0 + 64 wid + 32 f + 8 c + 4 h + i, token m0 + 32 j + l32
+
+    if constexpr (KIND == MI_OUT_INT8) {
+        int8_t *so = &sm.a[0][0];
+        const int cg = tid & 63, ch = n0 + 4 * cg;
+        uint32_t tw[4] = {0, 0, 0, 0};
+        int32_t tb[4] = {0, 0, 0, 0};
+        if constexpr (CONV) {
+            if (xblk) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    tw[r] = *reinterpret_cast<const uint32_t *>(cv.w + (int64_t)(ch + r) * 4);
+                    tb[r] = cv.b[ch + r];
+                }
+            }
+        }
+        __syncthreads();   // every wave is done reading the ring (no loads are in flight)
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    uint32_t pk = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int q = rshr32(acc[f][j][4 * c + i], g.shift);
+                        pk |= (uint32_t)(clamp32(q, -127, 127) & 255) << (8 * i);
+                    }
+                    *reinterpret_cast<uint32_t *>(&so[g2_ooff(32 * j + l32, 64 * wid + 32 * f + 8 * c + 4 * h)]) = pk;
+                }
+        __syncthreads();
+        if constexpr (CONV) {
+            if (xblk) {
+                // depthwise conv + squareplus (spec rules 4.3-4.4) down the tile:
+                // thread (cg, run) takes channels ch..ch+3 of staged rows
+                // 3 + 32 run .. (32 rows; the last run 29), as in gemm_tile
+                const int run = tid >> 6;
+                const int i0 = 3 + 32 * run, i1 = min(i0 + 32, kG2BM);
+                int gm = m0 + i0;
+                if (gm < g.M) {
+                    int sb = gm / cv.L, t = gm - sb * cv.L;
+                    auto row = [&](int i) { return *reinterpret_cast<const uint32_t *>(&so[g2_ooff(i, 4 * cg)]); };
+                    auto state = [&](int k) -> uint32_t {  // x[k] of sequence sb, k in [-3, -1]
+                        return cv.st_in ? *reinterpret_cast<const uint32_t *>(cv.st_in + ((int64_t)sb * 3 + 3 + k) * cv.D + ch)
+                                        : 0u;
+                    };
+                    uint32_t win[4] = {0, 0, 0, 0};
+                    auto push = [&](uint32_t v) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            win[r] = __builtin_amdgcn_perm(v, win[r], 0x00030201u | ((uint32_t)(4 + r) << 24));
+                    };
+                    for (int j = 3; j >= 1; --j) push(t - j >= 0 ? row(i0 - j) : state(t - j));
+                    for (int i = i0; i < i1 && gm < g.M; ++i, ++gm) {
+                        if (t == 0) {
+                            if (i > i0)
+                                for (int j = 3; j >= 1; --j) push(state(-j));
+                            for (int j = 0; j < 3 - cv.L; ++j)
+                                *reinterpret_cast<uint32_t *>(cv.st_out + ((int64_t)sb * 3 + j) * cv.D + ch) =
+                                    state(cv.L + j - 3);
+                        }
+                        const uint32_t cur = row(i);
+                        push(cur);
+                        uint32_t o = 0;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int32_t c = __builtin_amdgcn_sdot4((int)win[r], (int)tw[r], tb[r], false);
+                            o |= (uint32_t)(sqp_q(c) & 255) << (8 * r);
+                        }
+                        *reinterpret_cast<uint32_t *>(cv.xs + (int64_t)gm * cv.D + ch) = o;
+                        if (t >= cv.L - 3)
+                            *reinterpret_cast<uint32_t *>(cv.st_out + ((int64_t)sb * 3 + t - (cv.L - 3)) * cv.D + ch) = cur;
+                        if (++t == cv.L) {
+                            t = 0;
+                            ++sb;
+                        }
+                    }
+                }
+                return;
+            }
+        }
+        // 128 rows x 16 granules: thread t stores granule t % 16 of rows t / 16 + 16 p
+        const int gr = tid & 15;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int row = (tid >> 4) + 16 * p;
+            const int gm = m0 + row;
+            const v4i v = *reinterpret_cast<const v4i *>(&so[g2_ooff(row, 16 * gr)]);
+            if (gm < g.M) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>((int8_t *)g.out + (int64_t)gm * g.ldo + n0 + 16 * gr));
+        }
+    } else {
+        int32_t *ob = (int32_t *)g.out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + 32 * j + l32;
+            const int mc = min(m, g.M - 1);
+            v4i old[2][4];
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    old[f][c] = *reinterpret_cast<const v4i *>(ob + (int64_t)mc * g.ldo + n0 + 64 * wid + 32 * f + 8 * c + 4 * h);
+            RowStat st{0, 0};
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    v4i nv;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t delta = residual_delta(g, acc[f][j][4 * c + i]);
+                        nv[i] = (int32_t)clamp64((int64_t)old[f][c][i] + delta, -kResidualLimit, kResidualLimit);
+                        st.s1 += nv[i];
+                        st.s2 += (int64_t)nv[i] * nv[i];
+                    }
+                    if (m < g.M)
+                        *reinterpret_cast<v4i *>(ob + (int64_t)m * g.ldo + n0 + 64 * wid + 32 * f + 8 * c + 4 * h) = nv;
+                }
+            if (g.row_stats) {
+                st.s1 += __shfl_xor(st.s1, 32);
+                st.s2 += __shfl_xor(st.s2, 32);
+                if (h == 0 && m < g.M) {
+                    atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m), (unsigned long long)st.s1);
+                    atomicAdd(reinterpret_cast<unsigned long long *>(g.row_stats + 2 * (int64_t)m + 1),
+                              (unsigned long long)st.s2);
+                }
+            }
+        }
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm32_kernel(GemmArgs g) {
+    gemm32_tile<KIND, false>(g, ConvArgs{});
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm32_conv_kernel(GemmArgs g,
+                                                                                                ConvArgs cv) {
+    gemm32_tile<MI_OUT_INT8, true>(g, cv);
+}
+
 // gemm_any_kernel: any k % 16 == 0 and 4-byte aligned weights (e.g. dt_proj
 // with k = dt_rank): 4 waves of 64x64, weights fetched one word per thread.
 // 64-deep halves of a stage that lie wholly past K are skipped (k = 48 has
@@ -825,8 +1217,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv64_kernel(GemmArgs g) {
 // the XOR swizzle makes the 16 rows of an operand read fall in 16 different
 // bank groups.  Same chunk ownership and results as gemv64_kernel.
 constexpr int kG64Waves = 4, kG64U = 2;
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
 
 // Blocks along y take 64-row groups (rows [64y, 64y + 64)): the prefill form
 // for few outputs (x_proj, N <= 160, FT = 5), where 128 x 128 GEMM tiles would
@@ -1118,6 +1508,18 @@ GemmArgs make_args(const int8_t *a, int lda, const uint8_t *w, void *out, int ld
     return g;
 }
 
+// Shapes and layouts gemm32_kernel takes: no K or N tail, 31-bit byte offsets
+// for its buffer loads, and at least two of its tiles per CU (below that, e.g.
+// config 2's 384 tiles of 4096 x 768 -> 3072, the 128 x 128 tiles of
+// gemm_kernel are faster: 14.7 against 15.7 us).  `tiles` is the launch's
+// tile count.
+constexpr int64_t kG2MinTiles = 512;
+bool gemm32_fits(const GemmArgs &g, int64_t tiles) {
+    return g.K > 0 && g.K % kG2BK == 0 && g.N % kG2BN == 0 && g.M > 64 && aligned(g.a, 16) && g.lda % 16 == 0 &&
+           aligned(g.w, 16) && (int64_t)g.M * g.lda <= INT32_MAX && (int64_t)g.N * g.kw * 4 <= INT32_MAX &&
+           tiles >= kG2MinTiles;
+}
+
 template <int KIND>
 hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
     const dim3 grid((unsigned)(((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN)));
@@ -1131,6 +1533,15 @@ hipError_t launch_gemm_kind(const GemmArgs &g, hipStream_t st) {
             aligned(g.w, 16) && aligned(g.a, 16) && g.lda % 16 == 0) {
             hipLaunchKernelGGL((gemv64s_kernel<KIND, 5>), dim3((unsigned)((g.N + 79) / 80), (unsigned)((g.M + 63) / 64)),
                                dim3(256), 0, st, g);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (KIND == MI_OUT_INT8 || KIND == MI_OUT_RESIDUAL) {
+        const bool out_ok = KIND == MI_OUT_INT8 ? g.ldo % 16 == 0 && aligned(g.out, 16)
+                                                : g.ldo % 4 == 0 && aligned(g.out, 16);
+        const int64_t tiles = (int64_t)((g.M + kG2BM - 1) / kG2BM) * (g.N / kG2BN);
+        if (out_ok && gemm32_fits(g, tiles)) {
+            hipLaunchKernelGGL(gemm32_kernel<KIND>, dim3((unsigned)tiles), dim3(256), 0, st, g);
             return hipGetLastError();
         }
     }
@@ -1330,15 +1741,21 @@ extern "C" mi_status mi_in_proj_conv(const int8_t *a, int lda, const uint8_t *w_
         // write the new state of its last rows: the buffers must be distinct
         MI_REQUIRE(i0 + sbytes <= o0 || o0 + sbytes <= i0, MI_ERR_BAD_ARG, "%s: state_in and state_out overlap", fn);
     }
-    const int64_t nt = d_inner / kBN;
-    const int64_t xb = (int64_t)((m + kConvRows - 1) / kConvRows) * nt;
-    const int64_t zb = (int64_t)((m + kBM - 1) / kBM) * nt;
-    MI_REQUIRE(xb + zb <= INT32_MAX, MI_ERR_BAD_DIM, "%s: grid too large", fn);
     GemmArgs g = make_args(a, lda, w_in, xz, ldxz, m, 2 * d_inner, d_model, shift, 0, 0, nullptr, 0.0f, nullptr);
     ConvArgs cv{};
     cv.w = conv_w; cv.b = conv_b; cv.st_in = state_in; cv.st_out = state_out; cv.xs = xs;
-    cv.D = d_inner; cv.L = len; cv.x_blocks = (int)xb;
-    hipLaunchKernelGGL(gemm_conv_kernel, dim3((unsigned)(xb + zb)), dim3(256), 0, as_stream(stream), g, cv);
+    cv.D = d_inner; cv.L = len;
+    const int64_t tiles32 = (int64_t)((m + kG2ConvRows - 1) / kG2ConvRows + (m + kG2BM - 1) / kG2BM) * (d_inner / kG2BN);
+    const bool big = d_inner % kG2BN == 0 && gemm32_fits(g, tiles32);
+    const int64_t nt = d_inner / (big ? kG2BN : kBN);
+    const int64_t xb = (int64_t)((m + (big ? kG2ConvRows : kConvRows) - 1) / (big ? kG2ConvRows : kConvRows)) * nt;
+    const int64_t zb = (int64_t)((m + kBM - 1) / kBM) * nt;   // kG2BM == kBM
+    MI_REQUIRE(xb + zb <= INT32_MAX, MI_ERR_BAD_DIM, "%s: grid too large", fn);
+    cv.x_blocks = (int)xb;
+    if (big)
+        hipLaunchKernelGGL(gemm32_conv_kernel, dim3((unsigned)(xb + zb)), dim3(256), 0, as_stream(stream), g, cv);
+    else
+        hipLaunchKernelGGL(gemm_conv_kernel, dim3((unsigned)(xb + zb)), dim3(256), 0, as_stream(stream), g, cv);
     return check_launch(fn);
 }
 

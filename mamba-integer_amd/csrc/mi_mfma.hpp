@@ -6,6 +6,7 @@
 namespace mi {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 typedef long long v2l __attribute__((ext_vector_type(2)));  // (sum r, sum r^2) pairs
 
 // 16 ternary weights of one packed word -> 16 int8 in k order (4 dwords).

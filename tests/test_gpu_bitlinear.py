@@ -93,7 +93,8 @@ def test_bitlinear_kinds(cuda, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(200, 200, 192), (130, 36, 64), (257, 129, 320), (200, 200, 768), (130, 36, 704),
                                    (257, 129, 1536), (70, 300, 1472), (130, 36, 48), (257, 129, 80),
                                    (200, 300, 112), (300, 1536, 48), (200, 80, 1536), (130, 36, 256),
-                                   (300, 160, 2048), (65, 17, 512), (1000, 150, 4096)])
+                                   (300, 160, 2048), (65, 17, 512), (1000, 150, 4096),
+                                   (200, 256, 768), (257, 512, 1536), (1000, 1024, 2048)])
 @pytest.mark.parametrize("pad", [0, 4, 16])
 def test_gemm_tile_edges(cuda, M, N, K, pad):
     """Prefill GEMM edge tiles: a K tail of 64 past the last 128-deep stage, ragged
@@ -126,6 +127,43 @@ def test_gemm_tile_edges(cuda, M, N, K, pad):
     assert np.array_equal(H(st), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
     acc = H(ops.bitlinear(T(a), T(wp), ops.OUT_INT32, N, out=T(np.zeros((M, ldo), np.int32)), path="gemm"))
     assert np.array_equal(acc[:, :N], O.bitlinear(a, wp, O.OUT_INT32))
+
+
+@pytest.mark.parametrize("M,N,K", [(65409, 256, 128), (16385, 1024, 768), (8193, 2048, 2048)])
+@pytest.mark.parametrize("pad", [0, 4])
+def test_large_tile_gemm(cuda, M, N, K, pad):
+    """The 256 x 128-tile kernel (N % 256 == 0, K % 128 == 0, at least 512 tiles):
+    a last m-tile one row deep (rows past M clamped), one 128-deep stage, 6 and 16
+    stages through the three-stage ring.  int8 requant through the staged tile
+    (row pitch % 16 == 0; pad 4 takes the dword-store kernel) against the exact
+    product; RESIDUAL (both pitches) with row statistics against the oracle on
+    the first 256 and the last 129 rows (rows are independent)."""
+    import torch
+    from mamba_int import ops, pack_ternary
+    rng = np.random.default_rng(M + N + K + pad)
+    a = i8(rng, M, K)
+    w = _tern(rng, N, K)
+    wp = pack_ternary(w)
+    ldo = N + pad
+    s = 6
+    ref = _acc_exact(a, w)
+    out = T(np.full((M, ldo), 99, np.int8))
+    got = H(ops.bitlinear(T(a), T(wp), ops.OUT_INT8, N, shift=s, out=out, path="gemm"))
+    assert np.array_equal(got[:, :N], np.clip((ref + (1 << (s - 1))) >> s, -127, 127))
+    assert (got[:, N:] == 99).all(), "stored past n"
+    del ref
+    r0 = rng.integers(-(2**22), 2**22, size=(M, N), dtype=np.int32)
+    rp = np.zeros((M, ldo), np.int32)
+    rp[:, :N] = r0
+    rt = T(rp)
+    st = torch.zeros((M, 2), dtype=torch.int64, device="cuda")
+    ops.bitlinear(T(a), T(wp), ops.OUT_RESIDUAL, N, out=rt, res_mult=-3001, res_shift=11, path="gemm", row_stats=st)
+    rg = H(rt)[:, :N]
+    for rows in (slice(0, 256), slice(M - 129, M)):
+        ref = O.bitlinear(a[rows], wp, O.OUT_RESIDUAL, residual=r0[rows], res_mult=-3001, res_shift=11)
+        assert np.array_equal(rg[rows], ref)
+    r64 = rg.astype(np.int64)
+    assert np.array_equal(H(st), np.stack([r64.sum(1), (r64 * r64).sum(1)], 1))
 
 
 def test_squareplus_every_input(cuda):

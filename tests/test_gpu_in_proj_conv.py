@@ -33,6 +33,11 @@ def H(t):
     (5, 77, 768, 128, True),
     (2, 400, 64, 384, False),
     (1, 1000, 128, 128, True),
+    # d_inner % 256 == 0, d_model % 128 == 0 and at least 512 tiles: the 256 x 128-tile form
+    (4, 4100, 128, 512, True),   # sequences straddle x tiles of 125 rows
+    (1, 16400, 256, 512, False),
+    (8200, 2, 128, 512, True),   # sequences shorter than the conv window
+    (2, 8193, 768, 512, True),
 ])
 def test_in_proj_conv_matches_oracle(cuda, B, L, d, D, with_state):
     import torch
