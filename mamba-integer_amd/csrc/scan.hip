@@ -325,6 +325,201 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     }
 }
 
+// ------------------------------------------ head mode, N = 128: mixed block
+// At 16 lanes a channel (8 states a lane) a wave holds 4 channels; with B*H*P
+// channels a multiple of 6 per SIMD (e.g. 4 x 24 heads x 64 = 6144 on 1024
+// SIMDs) that leaves half the SIMDs two waves (8 channels) and the others one.
+// Here a 512-thread block owns 24 consecutive channels of one sequence, flat
+// over (head, p), so it may straddle two heads: waves 0-3 take 16 channels at
+// 16 lanes a channel (8 states a lane), waves 4-7 take 8 channels at 32 lanes
+// (4 states a lane).  Waves w and w + 4 of a block share a SIMD, so every SIMD
+// runs 4 + 2 channels.  The two heads' B and C rows are staged side by side
+// (B as int32 for the clamped multiply-add); the rest follows scan_kernel:
+// 64-step chunks prefetched one chunk ahead, x transposed so one ds_read_b32
+// serves 4 steps, four steps' y partials reduced together and recombined in a
+// chunk epilogue, 16-byte output stores.
+constexpr int kMixCH = 24, kMixCHA = 16;
+
+template <int G>
+__device__ __forceinline__ int group_sum_mix(int v) {
+    v = group_sum<16>(v);
+    if constexpr (G == 32) {
+        // add the neighbouring 16-lane row: v_permlane16_swap exchanges rows 0/2
+        // with rows 1/3, so the two results hold each lane's own and other row
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        v = (int)(r[0] + r[1]);
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(512) void scan_head_mix_kernel(ScanArgs a) {
+    constexpr int N = 128;
+    constexpr int XP = kTC + 4;
+    constexpr int NT = 512;
+    __shared__ __align__(16) int8_t s_x[kMixCH][XP];
+    __shared__ __align__(16) int32_t s_b[kTC][2 * N];
+    __shared__ __align__(16) int8_t s_c[kTC][2 * N];
+    __shared__ __align__(16) int32_t s_o32[kTC][kMixCH];
+    __shared__ __align__(16) int2 s_y[kTC][kMixCH];
+
+    const int tid = threadIdx.x;
+    const bool wa = tid < 256;   // wave-uniform: a 16-lane (8-state) wave
+    const int ch = wa ? tid / 16 : kMixCHA + (tid - 256) / 32;
+    const int g = wa ? tid % 16 : (tid - 256) % 32;
+    const int S = wa ? 8 : 4;
+    const int c0 = blockIdx.x * kMixCH;   // first channel of the block, flat over (head, p)
+    const int b = blockIdx.z;
+    const int hd0 = c0 / a.P;
+    const bool two = hd0 + 1 < a.H;        // a second head's B/C row exists
+    const int cf = c0 + ch;
+    const int hd = cf / a.P, p = cf - hd * a.P;
+    const int boff = (hd - hd0) * N + g * S;   // this lane's first state in the staged B/C rows
+
+    const int32_t n2 = 2 * a.decay[hd];
+    int32_t h[8];
+    const int64_t sidx = (((int64_t)b * a.H + hd) * a.P + p) * N + g * S;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) h[s] = (a.h_in && s < S) ? a.h_in[sidx + s] : 0;
+
+    // staging: x as 3 pieces of 8 bytes a step (192 a chunk), B and C as 16
+    // pieces of 16 bytes a step over the two heads (1024 each, 2 a thread)
+    uint2 rx;
+    uint4 rb[2], rc[2];
+    const int64_t row0 = (int64_t)b * a.L;
+    auto prefetch = [&](int t0) {
+        {
+            const int tt = tid / 3, q = tid % 3;
+            const bool ok = tid < kTC * 3 && t0 + tt < a.L;
+            rx = ok ? *reinterpret_cast<const uint2 *>(a.x + (row0 + t0 + tt) * a.x_row + c0 + 8 * q) : make_uint2(0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = tid + j * NT;
+            const int tt = i / 16, c16 = i % 16;
+            const bool ok = t0 + tt < a.L && (c16 < 8 || two);
+            const int64_t off = (row0 + t0 + tt) * a.bc_row + (int64_t)hd0 * N + c16 * 16;
+            rb[j] = load16(a.bsrc + off, ok);
+            rc[j] = load16(a.csrc + off, ok);
+        }
+    };
+    auto stash = [&]() {
+        if (tid < kTC * 3) {
+            const int tt = tid / 3, q = tid % 3;
+            const uint32_t w[2] = {rx.x, rx.y};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s_x[8 * q + e][tt] = (int8_t)(w[e >> 2] >> (8 * (e & 3)));
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = tid + j * NT;
+            const int tt = i / 16, c16 = i % 16;
+            const uint32_t w[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<int4 *>(&s_b[tt][c16 * 16 + 4 * q]) =
+                    make_int4(sbyte(w[q], 0), sbyte(w[q], 1), sbyte(w[q], 2), sbyte(w[q], 3));
+            *reinterpret_cast<uint4 *>(&s_c[tt][c16 * 16]) = rc[j];
+        }
+    };
+    // one step of this lane's SS states: the exact int32 partials of y
+    auto step = [&](auto ss, int t, int xv, int &yhi, int &ylo) {
+        constexpr int SS = decltype(ss)::value;
+        yhi = 0;
+        ylo = 0;
+        int bv[SS];
+        uint32_t cw[SS / 4];
+#pragma unroll
+        for (int q = 0; q < SS / 4; ++q) {
+            const int4 b4 = *reinterpret_cast<const int4 *>(&s_b[t][boff + 4 * q]);
+            bv[4 * q] = b4.x; bv[4 * q + 1] = b4.y; bv[4 * q + 2] = b4.z; bv[4 * q + 3] = b4.w;
+            cw[q] = *reinterpret_cast<const uint32_t *>(&s_c[t][boff + 4 * q]);
+        }
+#pragma unroll
+        for (int s = 0; s < SS; ++s) update16_b(h[s], n2, bv[s], xv, sbyte(cw[s >> 2], s & 3), yhi, ylo);
+    };
+    // four steps (or the chunk's last tend < 4) of one wave kind
+    auto group = [&](auto ss, int t4, int tend, uint32_t xw) {
+        constexpr int SS = decltype(ss)::value, GG = 128 / SS;
+        if (tend == 4) {
+            int y[8];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) step(ss, t4 + tt, sbyte(xw, tt), y[2 * tt], y[2 * tt + 1]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0xB1, 0xF, 0xF, false);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0x4E, 0xF, 0xF, false);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0x141, 0xF, 0xF, false);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) y[q] += __builtin_amdgcn_update_dpp(0, y[q], 0x140, 0xF, 0xF, false);
+            if constexpr (GG == 32) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)y[q], (unsigned)y[q], false, false);
+                    y[q] = (int)(r[0] + r[1]);
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) s_y[t4 + tt][ch] = make_int2(y[2 * tt], y[2 * tt + 1]);
+        } else {
+            for (int tt = 0; tt < tend; ++tt) {
+                int yhi, ylo;
+                step(ss, t4 + tt, sbyte(xw, tt), yhi, ylo);
+                s_y[t4 + tt][ch] = make_int2(group_sum_mix<GG>(yhi), group_sum_mix<GG>(ylo));
+            }
+        }
+    };
+
+    const int nchunks = (a.L + kTC - 1) / kTC;
+    prefetch(0);
+    for (int cidx = 0; cidx < nchunks; ++cidx) {
+        const int t0 = cidx * kTC;
+        const int tn = min(kTC, a.L - t0);
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (cidx + 1 < nchunks) prefetch(t0 + kTC);
+        for (int t4 = 0; t4 < tn; t4 += 4) {
+            const uint32_t xw = *reinterpret_cast<const uint32_t *>(&s_x[ch][t4]);
+            const int tend = min(4, tn - t4);
+            if (wa)
+                group(std::integral_constant<int, 8>{}, t4, tend, xw);
+            else
+                group(std::integral_constant<int, 4>{}, t4, tend, xw);
+        }
+        __syncthreads();
+        // chunk epilogue: y = sat32(yhi * 2^16 + ylo), then 16-byte stores of the 24 channels' rows
+        for (int i = tid; i < kTC * kMixCH; i += NT) {
+            const int tt = i / kMixCH, cc = i % kMixCH;
+            if (tt < tn) {
+                const int2 yv = s_y[tt][cc];
+                s_o32[tt][cc] = sat32_64(((int64_t)yv.x << 16) + yv.y);
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < kTC * (kMixCH / 4); i += NT) {
+            const int tt = i / (kMixCH / 4), c4 = i % (kMixCH / 4);
+            if (tt < tn)
+                *reinterpret_cast<uint4 *>(a.y + (row0 + t0 + tt) * a.x_row + c0 + c4 * 4) =
+                    *reinterpret_cast<const uint4 *>(&s_o32[tt][c4 * 4]);
+        }
+        // chunk_states at every multiple of cs (cs is a multiple of kTC) and at the end
+        const int tdone = t0 + tn;
+        if (a.chunk_states && (tdone % a.cs == 0 || tdone == a.L)) {
+            const int cc = (tdone - 1) / a.cs;
+            int32_t *dst = a.chunk_states + ((((int64_t)b * a.nchunks_out + cc) * a.H + hd) * a.P + p) * N + g * S;
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                if (s < S) dst[s] = h[s];
+        }
+    }
+    if (a.h_out) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            if (s < S) a.h_out[sidx + s] = h[s];
+    }
+}
+
 // ---------------------------------------------------------------- generic
 // Plain int64 kernels for every shape the fast kernel does not take, and for
 // chunk lengths that are not multiples of the staging chunk.  One thread per
@@ -588,7 +783,19 @@ extern "C" mi_status mi_ssd_chunked_scan(const int8_t *x, const int8_t *b, const
     a.cs = chunk; a.nchunks_out = (len + chunk - 1) / chunk;
     const bool fast = len > 0 && fast_shape(nstate, head_dim, decay_shift, kModeHead) && (chunk % kTC == 0) && aligned(x, 16) &&
                       aligned(b, 16) && aligned(c, 16) && aligned(y, 16);
-    hipError_t e = launch_scan<kModeHead>(a, nstate, fast, as_stream(stream));
+    // the mixed 24-channel block where its blocks fill every CU exactly (one
+    // block per CU at a time: 102 KB of LDS)
+    const int64_t hp = (int64_t)heads * head_dim, mix_blocks = hp / kMixCH * batch;
+    const bool mix = fast && nstate == 128 && hp % kMixCH == 0 && head_dim >= kMixCH && hp / kMixCH <= 65535 &&
+                     mix_blocks % device_cus() == 0;
+    hipError_t e;
+    if (mix) {
+        hipLaunchKernelGGL(scan_head_mix_kernel, dim3((unsigned)(hp / kMixCH), 1u, (unsigned)batch), dim3(512), 0,
+                           as_stream(stream), a);
+        e = hipGetLastError();
+    } else {
+        e = launch_scan<kModeHead>(a, nstate, fast, as_stream(stream));
+    }
     if (e != hipSuccess) return fail(MI_ERR_HIP, "mi_ssd_chunked_scan: launch failed: %s", hipGetErrorString(e));
     return MI_OK;
 }

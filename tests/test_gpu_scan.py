@@ -175,6 +175,32 @@ def test_ssd_chunked(cuda, B, L, H_, P, N, cs):
     assert np.array_equal(H(hout), h_ref)
 
 
+@pytest.mark.parametrize("B,L,H_,P,cs", [(2, 203, 48, 64, 64), (8, 192, 32, 24, 128), (1, 130, 96, 64, 64)])
+def test_ssd_chunked_mixed_block(cuda, B, L, H_, P, cs):
+    """N = 128 shapes whose 24-channel blocks fill 256 CUs exactly: the mixed
+    block (16- and 32-lane waves; blocks straddling two heads, the last head's
+    block without a neighbour, one head per block at P = 24), a ragged last
+    chunk (L = 203, 130: the 1-3 step tail), chunk states at every cs and at
+    the end, and a nonzero start state."""
+    import torch
+    from mamba_int import ops
+    N = 128
+    rng = np.random.default_rng(B * L + H_ + P)
+    x = i8(rng, B, L, H_, P)
+    b = i8(rng, B, L, H_, N)
+    c = i8(rng, B, L, H_, N)
+    n = rng.integers(24576, 32768, size=(H_,), dtype=np.int32)
+    h0 = rng.integers(-(2**31), 2**31, size=(B, H_, P, N), dtype=np.int64).astype(np.int32)
+    y_ref, cst_ref, h_ref = O.ssd_chunked_scan(x, b, c, n, 15, cs, want_chunk_states=True, h_state=h0.copy())
+    nc = -(-L // cs)
+    cst = torch.zeros((B, nc, H_, P, N), dtype=torch.int32, device="cuda")
+    hout = torch.zeros((B, H_, P, N), dtype=torch.int32, device="cuda")
+    y = ops.ssd_chunked_scan(T(x), T(b), T(c), T(n), 15, cs, chunk_states=cst, h_in=T(h0), h_out=hout)
+    assert np.array_equal(H(y), y_ref)
+    assert np.array_equal(H(cst), cst_ref)
+    assert np.array_equal(H(hout), h_ref)
+
+
 def test_ssd_config4_full_size(cuda):
     """Config 4 at full size (B4 L8192 H24 P64 N128, cs 256) on the GPU against
     the oracle, bit for bit: every output, every chunk-boundary state and the
