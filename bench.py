@@ -36,8 +36,9 @@ VALU_PEAK_GOPS = 256 * 64 * 2.4  # int32 lane-ops per ns (= G ops/s / 1000): 393
 # state update at the bench shape, measured with rocprofv3 --pmc SQ_INSTS_VALU
 # (wave64 instructions x 64 / updates; profiles/scan_kernels_valu_pmc.md)
 SCAN_LANE_OPS_PER_UPDATE = 13.61
-# the same for the config-4 chunked multi-head scan (B4 L8192, 24 heads x 64, N128)
-C4_LANE_OPS_PER_UPDATE = 9.03
+# the same for the config-4 chunked multi-head scan (B4 L8192, 24 heads x 64, N128; the mixed
+# 24-channel block)
+C4_LANE_OPS_PER_UPDATE = 10.21
 MFMA_I8_PEAK_TOPS = 5000.0
 
 
