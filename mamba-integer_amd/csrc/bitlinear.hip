@@ -512,16 +512,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 // needs in a stage are one 16-byte run (words 4h..4h+3).  Result register r of
 // lane l is feature 8(r/4) + 4h + r%4 of its fragment, token l%32.
 //
-// Staging: every global load is a global_load_lds_dwordx4 (LDS DMA, no VGPRs)
-// into a ring of three stages, issued two stages ahead of the stage being
-// multiplied; a wave waits only for its own loads of that stage (vmcnt counts
-// them in order: 6 a stage) and a bare s_barrier then makes all waves' loads
-// visible (__syncthreads would wait for every load in flight).  The activation
-// tile is 128 rows x 128 bytes with 16-byte segment q of row r at position
-// q ^ ((r >> 1) & 7): lane i of a DMA instruction lands at byte 16i, so the
-// lane picks the segment that belongs there, and the fragment reads (rows
-// l%32, one segment) fall in distinct bank groups.  Each wave's weight words
-// go to its own LDS region and are read back by the lanes that loaded them.
+// Staging: every global load is a buffer_load_dwordx4 ... lds (LDS DMA, no
+// VGPRs) into a ring of three stages; a wave waits only for its own loads of a
+// stage (vmcnt counts them in order: 6 a stage) and a bare s_barrier then
+// makes all waves' loads visible (__syncthreads would wait for every load in
+// flight).  The activation tile is 128 rows x 128 bytes with 16-byte segment
+// q of row r at position q ^ ((r >> 1) & 7): lane i of a DMA instruction lands
+// at byte 16i, so the lane picks the segment that belongs there, and the
+// fragment reads (rows l%32, one segment) fall in distinct bank groups.  Each
+// wave's weight words go to its own LDS region and are read back by the lanes
+// that loaded them.  The pipeline over a stage's 4 k-steps (the barrier in its
+// middle, MFMAs interleaved with the next k-step's reads and unpack, loads
+// three stages ahead) is described at the main loop.
 //
 // Requires K % 128 == 0, N % 256 == 0, 16-byte aligned a / w with lda % 16 == 0.
 // Rows past M read row M - 1 (the conv x-half's halo rows before 0 read row 0)
@@ -638,12 +640,13 @@ __device__ __forceinline__ void gemm32_tile(const GemmArgs &g, const ConvArgs &c
     // Stage kt runs 4 k-steps of 8 MFMAs.  Each k-step's MFMAs are
     // interleaved (sched_group_barrier) with the fragment reads and weight
     // unpack of the next k-step, so one wave alone keeps its SIMD's MFMA pipe
-    // fed.  After the fragment reads of step 3 (issued in step 2) every wave
-    // waits for its own loads of stage kt + 1 and meets the others at one
-    // barrier: stage kt + 1 is then visible and stage kt's buffer free, so step
-    // 3 refills that buffer with stage kt + 3 and reads stage kt + 1's weights
-    // and first fragments under its MFMAs (no LDS latency exposed at a stage
-    // boundary; loads run 2.5 stages ahead).
+    // fed.  Before step 2 every wave waits for its own loads of stage kt + 1
+    // and reads its weight words of that stage during step 2 (its own region:
+    // no barrier needed).  After the fragment reads of step 3 (issued in step
+    // 2) the waves meet at one barrier: stage kt + 1 is then visible and stage
+    // kt's buffer free, so step 3 refills that buffer with stage kt + 3 and
+    // reads stage kt + 1's first fragments under its MFMAs (no LDS latency
+    // exposed at a stage boundary; loads run 2.5 stages ahead).
     auto read_w = [&](int kt, v4i (&wv)[2]) {
 #pragma unroll
         for (int f = 0; f < 2; ++f) wv[f] = *reinterpret_cast<const v4i *>(&sm.w[kt % kG2Ring][wid][f][lane * 4]);
