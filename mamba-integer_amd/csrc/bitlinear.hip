@@ -11,11 +11,15 @@
 // Lane l holds 16 consecutive k of row l%16 for k-group l/16 in both
 // operands, and result register r of lane l is (n = 4*(l/16) + r, m = l%16):
 // four consecutive output features of one token, i.e. one dword of int8
-// output or one 16-byte vector of int32 output per lane.
+// output or one 16-byte vector of int32 output per lane.  (gemm32_kernel
+// uses v_mfma_i32_32x32x32_i8 the same way; its layout is described there.)
 //
-//   prefill GEMM: 128(n) x 128(m) block tile, 4 waves of 64x64, K staged 128 at
-//                 a time through LDS (packed weights stay packed in LDS and are
-//                 unpacked in registers), double buffered, one barrier per stage.
+//   prefill GEMM: 128(n) x 128(m) block tiles, 4 waves of 32 weight rows x 128
+//                 tokens, K staged 128 at a time through LDS (packed weights
+//                 stay packed in LDS and are unpacked in registers), double
+//                 buffered, one barrier per stage (gemm_kernel); from 512 tiles
+//                 up 256(n) x 128(m) tiles on 32x32x32 MFMAs with an LDS-DMA
+//                 ring (gemm32_kernel).
 //   decode GEMV:  m <= 64; a block owns 16 output features, its 4 waves split
 //                 K; each lane streams 16-byte words of packed weights straight
 //                 from HBM and unpacks them in registers.
