@@ -681,9 +681,12 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
     if constexpr (NPL > 0) {
 #pragma unroll
         for (int c = 0; c < NPL / 4; ++c) {
-            const int4 h4 = *reinterpret_cast<const int4 *>(hp + q * NPL + 4 * c);
+            // the state is read and written once a step: non-temporal, so its
+            // stream does not displace the weights in L2 (0.2950 -> 0.2943 ms
+            // per d768 x 24 step at batch 8)
+            const v4i h4 = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(hp + q * NPL + 4 * c));
             const int4 b4 = *reinterpret_cast<const int4 *>(bp + q * NPL + 4 * c);
-            hv[4 * c] = h4.x; hv[4 * c + 1] = h4.y; hv[4 * c + 2] = h4.z; hv[4 * c + 3] = h4.w;
+            hv[4 * c] = h4[0]; hv[4 * c + 1] = h4[1]; hv[4 * c + 2] = h4[2]; hv[4 * c + 3] = h4[3];
             bv[4 * c] = b4.x; bv[4 * c + 1] = b4.y; bv[4 * c + 2] = b4.z; bv[4 * c + 3] = b4.w;
         }
     } else {
@@ -797,8 +800,8 @@ __global__ __launch_bounds__(256) void dt_scan_step_kernel(DtScanArgs g) {
         if (active) {
 #pragma unroll
             for (int c = 0; c < NPL / 4; ++c)
-                *reinterpret_cast<int4 *>(hp + q * NPL + 4 * c) =
-                    make_int4(hn[4 * c], hn[4 * c + 1], hn[4 * c + 2], hn[4 * c + 3]);
+                __builtin_nontemporal_store(v4i{hn[4 * c], hn[4 * c + 1], hn[4 * c + 2], hn[4 * c + 3]},
+                                            reinterpret_cast<v4i *>(hp + q * NPL + 4 * c));
         }
     } else {
 #pragma unroll
